@@ -1,0 +1,327 @@
+// Device helpers shared by every kernel of the Linear/GEMM path: bf16/f16 rounding, the activation
+// math, and the fused register epilogue (bias, activation, residual add/ext/mul, typed stores).
+//
+// The epilogue reproduces the rounding points of the reference's separate passes:
+//   stage 0  GEMM result  -> rounded to C's dtype (RNE for bf16: Service::ConvertFp32ToBf16 after
+//            cblas_sbgemm + AddBias, src/dnn/src/kudnn_gemm.cpp:215-221, src/dnn/src/service.cpp:48-67)
+//   stage 1  activation   -> computed in f32 from the stored C, bf16 result TRUNCATED (top 16 bits;
+//            SvCvtBF16F32FullX, src/dnn/src/kernels/vml/vml_sve_base.h:111-118), RELU first maps
+//            |x| >= 0x7f7f8000 to +-Inf (SvF32CvtBf16InfSpecial, vml_sve_base.h:97-109, relu/relu.c:225-233)
+//   stage 2  residual     -> f32 math on the stored operands, RNE to bf16
+//            (AddOps, src/dnn/src/kudnn_linear_res.cpp:57-122)
+#ifndef KUDNN_DEVICE_COMMON_H
+#define KUDNN_DEVICE_COMMON_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "plan_types.h"
+
+namespace kudnn_dev {
+
+// ---------------------------------------------------------------------------------------------------
+// scalar conversions
+
+__device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
+__device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return u2f(static_cast<uint32_t>(h) << 16); }
+
+// Round-to-nearest-even f32 -> bf16 (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f)
+{
+    uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+        return static_cast<uint16_t>((u >> 16) | 0x0040u);
+    }
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+// Truncating f32 -> bf16 (keep the top 16 bits).
+__device__ __forceinline__ uint16_t f32_to_bf16_trunc(float f) { return static_cast<uint16_t>(f2u(f) >> 16); }
+
+// RELU's bf16 store: finite values at or above the largest bf16 (0x7f7f8000) become +-Inf, then truncate.
+__device__ __forceinline__ uint16_t f32_to_bf16_trunc_inf(float f)
+{
+    uint32_t u = f2u(f);
+    uint32_t a = u & 0x7fffffffu;
+    if (a >= 0x7f7f8000u && a < 0x7f800000u) {
+        u = (u & 0x80000000u) | 0x7f800000u;
+    }
+    return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
+__device__ __forceinline__ uint16_t f32_to_f16_rne(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
+
+// Value of f after a round trip through storage of dtype dt (RNE), as the reference's typed buffers do.
+__device__ __forceinline__ float round_store(int dt, float f)
+{
+    if (dt == KUDNN_DT_BF16) {
+        return bf16_to_f32(f32_to_bf16_rne(f));
+    }
+    if (dt == KUDNN_DT_F16) {
+        return f16_to_f32(f32_to_f16_rne(f));
+    }
+    return f;
+}
+
+__device__ __forceinline__ float load_elem(const void *p, int dt, int64_t idx)
+{
+    switch (dt) {
+        case KUDNN_DT_F32: return static_cast<const float *>(p)[idx];
+        case KUDNN_DT_BF16: return bf16_to_f32(static_cast<const uint16_t *>(p)[idx]);
+        case KUDNN_DT_F16: return f16_to_f32(static_cast<const uint16_t *>(p)[idx]);
+        default: return 0.0f;
+    }
+}
+
+// Stores a value that is already rounded to dt (exact conversion), or rounds with RNE.
+__device__ __forceinline__ void store_elem(void *p, int dt, int64_t idx, float v)
+{
+    switch (dt) {
+        case KUDNN_DT_F32: static_cast<float *>(p)[idx] = v; break;
+        case KUDNN_DT_BF16: static_cast<uint16_t *>(p)[idx] = f32_to_bf16_rne(v); break;
+        case KUDNN_DT_F16: static_cast<uint16_t *>(p)[idx] = f32_to_f16_rne(v); break;
+        default: break;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------
+// activations (f32 math)
+
+// exp via the hardware base-2 exponential: e^x = 2^(x*log2 e).
+__device__ __forceinline__ float fast_exp(float x) { return __expf(x); }
+
+// tanh from its exponential form tanh(y) = 1 - 2/(e^{2y}+1), odd-symmetric, saturating for large |y|.
+__device__ __forceinline__ float tanh_f32(float y)
+{
+    float a = fabsf(y);
+    float t;
+    if (a < 0.0004f) {
+        t = a;  // tanh(a) = a - a^3/3 + ..., the cubic term is below f32 resolution here
+    } else {
+        float e = fast_exp(2.0f * fminf(a, 20.0f));
+        t = 1.0f - 2.0f / (e + 1.0f);
+    }
+    return copysignf(t, y);
+}
+
+// RELU: x <= 0 -> alpha*x, else x (relu/relu.c:14-25; a negative input times alpha 0 keeps its sign).
+__device__ __forceinline__ float act_relu(float x, float alpha) { return (x <= 0.0f) ? x * alpha : x; }
+
+// SWISH: x * sigmoid(alpha*x) with sigmoid(t) = 1/(1+e^{-t}); the reference saturates the exponent
+// argument to [-87, 87] (vml_sve_la_sigmoid.h:37-47, swish/vml_sve_la_swishf.c:31-47).
+__device__ __forceinline__ float act_swish(float x, float alpha)
+{
+    float t = -alpha * x;
+    float s;
+    if (t > 87.0f) {
+        s = 0.0f;
+    } else if (t < -87.0f) {
+        s = 1.0f;
+    } else {
+        s = 1.0f / (1.0f + fast_exp(t));
+    }
+    return x * s;
+}
+
+// GELU (tanh form): 0.5*x*(1 + tanh(sqrt(2/pi)*x*(1 + 0.044715*x^2))) (gelu_tanh/vml_sve_la_gelu_tanh.h:22-39).
+__device__ __forceinline__ float act_gelu_tanh(float x)
+{
+    const float kSqrt2OverPi = 0.7978845608028654f;
+    const float kCoef = 0.044715f;
+    float y = kSqrt2OverPi * x * (1.0f + kCoef * x * x);
+    return 0.5f * x * (1.0f + tanh_f32(y));
+}
+
+// GELU (erf form): 0.5*x*(1 + erf(x/sqrt(2))) (gelu_erf/vml_sve_la_gelu_erf.h:20-28).
+__device__ __forceinline__ float act_gelu_erf(float x)
+{
+    const float kInvSqrt2 = 0.7071067811865476f;
+    return 0.5f * x * (1.0f + erff(x * kInvSqrt2));
+}
+
+__device__ __forceinline__ float apply_act(int kind, float x, float alpha)
+{
+    switch (kind) {
+        case KUDNN_ACT_RELU: return act_relu(x, alpha);
+        case KUDNN_ACT_SWISH: return act_swish(x, alpha);
+        case KUDNN_ACT_GELU_TANH: return act_gelu_tanh(x);
+        case KUDNN_ACT_GELU_ERF: return act_gelu_erf(x);
+        default: return x;
+    }
+}
+
+// Rounding of an activation output stored as dt (vml bf16 kernels truncate; f16 kernels convert RNE).
+__device__ __forceinline__ float act_round(int dt, int kind, float v)
+{
+    if (dt == KUDNN_DT_BF16) {
+        uint16_t h = (kind == KUDNN_ACT_RELU) ? f32_to_bf16_trunc_inf(v) : f32_to_bf16_trunc(v);
+        return bf16_to_f32(h);
+    }
+    if (dt == KUDNN_DT_F16) {
+        return f16_to_f32(f32_to_f16_rne(v));
+    }
+    return v;
+}
+
+// ---------------------------------------------------------------------------------------------------
+// fused epilogue
+
+// Per-batch base offsets (in elements) of the epilogue tensors for a flattened batch index.
+struct EpiBatch {
+    int64_t c, bias, src, y;
+};
+
+__device__ __forceinline__ EpiBatch epi_batch_offsets(const EpiParams &e, int64_t b)
+{
+    int64_t i2 = b % e.bdim[2];
+    int64_t t = b / e.bdim[2];
+    int64_t i1 = t % e.bdim[1];
+    int64_t i0 = t / e.bdim[1];
+    EpiBatch o;
+    o.c = i0 * e.c_bs[0] + i1 * e.c_bs[1] + i2 * e.c_bs[2];
+    o.bias = i0 * e.bias_bs[0] + i1 * e.bias_bs[1] + i2 * e.bias_bs[2];
+    o.src = i0 * e.src_bs[0] + i1 * e.src_bs[1] + i2 * e.src_bs[2];
+    o.y = i0 * e.y_bs[0] + i1 * e.y_bs[1] + i2 * e.y_bs[2];
+    return o;
+}
+
+// Applies the epilogue to one accumulator value of output element (m, n). m, n are in bounds.
+__device__ __forceinline__ void epi_apply(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, float acc)
+{
+    float v = acc * e.alpha;
+    if (e.beta != 0.0f) {
+        v += e.beta * load_elem(e.c, e.c_dt, ob.c + m * e.c_sm + n * e.c_sn);
+    }
+    if (e.bias != nullptr) {
+        v += load_elem(e.bias, e.bias_dt, ob.bias + m * e.bias_sm + n * e.bias_sn);
+    }
+    v = round_store(e.c_dt, v);
+    if (e.store_c) {
+        store_elem(e.c, e.c_dt, ob.c + m * e.c_sm + n * e.c_sn, v);
+    }
+    if (e.act != KUDNN_ACT_UNIMPLEMENTED) {
+        v = act_round(e.c_dt, e.act, apply_act(e.act, v, e.act_alpha));
+    }
+    if (e.bin != KUDNN_BINARY_NONE) {
+        float s = load_elem(e.src, e.src_dt, ob.src + m * e.src_sm + n * e.src_sn);
+        if (e.bin == KUDNN_BINARY_ADD) {
+            v = v + s;
+        } else if (e.bin == KUDNN_BINARY_EXT) {
+            v = fmaf(s, e.gamma, v);
+        } else {
+            v = v * s;
+        }
+    }
+    store_elem(e.y, e.y_dt, ob.y + m * e.y_sm + n * e.y_sn, v);
+}
+
+// Epilogue for four consecutive columns n..n+3 of row m (the MFMA output layout gives each lane runs
+// of four columns). Uses 8/16-byte accesses when the tensors are contiguous along n and aligned.
+__device__ __forceinline__ void epi_apply4(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, int64_t N,
+                                           const float acc[4])
+{
+    if (n + 3 < N && e.fast4) {
+        // fast4: y (and src / bias when present) are contiguous along n and 4-element aligned,
+        // c is not re-read (beta == 0) and not separately stored unless contiguous too.
+        float v[4];
+        float bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (e.bias != nullptr) {
+            int64_t bi = ob.bias + m * e.bias_sm + n * e.bias_sn;
+            if (e.bias_sn == 0) {
+                float b0 = load_elem(e.bias, e.bias_dt, bi);
+                bv[0] = bv[1] = bv[2] = bv[3] = b0;
+            } else if (e.bias_dt == KUDNN_DT_F32) {
+                float4 t = *reinterpret_cast<const float4 *>(static_cast<const float *>(e.bias) + bi);
+                bv[0] = t.x; bv[1] = t.y; bv[2] = t.z; bv[3] = t.w;
+            } else {
+                for (int q = 0; q < 4; ++q) bv[q] = load_elem(e.bias, e.bias_dt, bi + q);
+            }
+        }
+        for (int q = 0; q < 4; ++q) {
+            v[q] = round_store(e.c_dt, acc[q] * e.alpha + bv[q]);
+        }
+        if (e.store_c) {
+            int64_t ci = ob.c + m * e.c_sm + n;
+            if (e.c_dt == KUDNN_DT_F32) {
+                *reinterpret_cast<float4 *>(static_cast<float *>(e.c) + ci) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+                for (int q = 0; q < 4; ++q) store_elem(e.c, e.c_dt, ci + q, v[q]);
+            }
+        }
+        if (e.act != KUDNN_ACT_UNIMPLEMENTED) {
+            for (int q = 0; q < 4; ++q) v[q] = act_round(e.c_dt, e.act, apply_act(e.act, v[q], e.act_alpha));
+        }
+        if (e.bin != KUDNN_BINARY_NONE) {
+            int64_t si = ob.src + m * e.src_sm + n;
+            float s[4];
+            if (e.src_dt == KUDNN_DT_BF16) {
+                uint2 raw = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(e.src) + si);
+                s[0] = u2f(raw.x << 16); s[1] = u2f(raw.x & 0xffff0000u);
+                s[2] = u2f(raw.y << 16); s[3] = u2f(raw.y & 0xffff0000u);
+            } else if (e.src_dt == KUDNN_DT_F32) {
+                float4 t = *reinterpret_cast<const float4 *>(static_cast<const float *>(e.src) + si);
+                s[0] = t.x; s[1] = t.y; s[2] = t.z; s[3] = t.w;
+            } else {
+                for (int q = 0; q < 4; ++q) s[q] = load_elem(e.src, e.src_dt, si + q);
+            }
+            for (int q = 0; q < 4; ++q) {
+                if (e.bin == KUDNN_BINARY_ADD) {
+                    v[q] = v[q] + s[q];
+                } else if (e.bin == KUDNN_BINARY_EXT) {
+                    v[q] = fmaf(s[q], e.gamma, v[q]);
+                } else {
+                    v[q] = v[q] * s[q];
+                }
+            }
+        }
+        int64_t yi = ob.y + m * e.y_sm + n;
+        if (e.y_dt == KUDNN_DT_BF16) {
+            uint32_t lo = static_cast<uint32_t>(f32_to_bf16_rne(v[0])) | (static_cast<uint32_t>(f32_to_bf16_rne(v[1])) << 16);
+            uint32_t hi = static_cast<uint32_t>(f32_to_bf16_rne(v[2])) | (static_cast<uint32_t>(f32_to_bf16_rne(v[3])) << 16);
+            *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(e.y) + yi) = make_uint2(lo, hi);
+        } else if (e.y_dt == KUDNN_DT_F32) {
+            *reinterpret_cast<float4 *>(static_cast<float *>(e.y) + yi) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+            for (int q = 0; q < 4; ++q) store_elem(e.y, e.y_dt, yi + q, v[q]);
+        }
+        return;
+    }
+    for (int q = 0; q < 4; ++q) {
+        if (n + q < N) {
+            epi_apply(e, ob, m, n + q, acc[q]);
+        }
+    }
+}
+
+// XCD-aware block order. The hardware deals workgroups round-robin over the 8 XCDs (block b runs on
+// XCD b % 8); this maps the hardware id to a logical id such that consecutive logical ids run on the
+// same XCD and therefore share its L2.
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks)
+{
+    const int kXcds = 8;
+    int xcd = bid % kXcds;
+    int per = nblocks / kXcds;
+    int extra = nblocks % kXcds;
+    return xcd * per + (xcd < extra ? xcd : extra) + bid / kXcds;
+}
+
+// Grouped tile order: walks GROUP tile-rows at a time so that co-resident blocks share A and B panels.
+__device__ __forceinline__ void grouped_tile(int lid, int tilesM, int tilesN, int group, int &tm, int &tn)
+{
+    int perGroup = group * tilesN;
+    int g = lid / perGroup;
+    int firstM = g * group;
+    int gsize = tilesM - firstM;
+    if (gsize > group) gsize = group;
+    int r = lid % perGroup;
+    tm = firstM + r % gsize;
+    tn = r / gsize;
+}
+
+}  // namespace kudnn_dev
+
+#endif  // KUDNN_DEVICE_COMMON_H

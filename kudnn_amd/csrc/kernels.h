@@ -1,0 +1,41 @@
+// Host-side launchers of the HIP kernels (one translation unit per kernel family).
+#ifndef KUDNN_KERNELS_H
+#define KUDNN_KERNELS_H
+
+#include <hip/hip_runtime.h>
+
+#include "plan_types.h"
+
+// Tile configurations of the dispatcher (values are stable: they appear in plan descriptions).
+enum {
+    KUDNN_CFG_BF16_256x256 = 1,
+    KUDNN_CFG_BF16_256x128 = 2,
+    KUDNN_CFG_BF16_128x128 = 3,
+    KUDNN_CFG_F32_128x128 = 10,
+    KUDNN_CFG_F32_64x64 = 11,
+    KUDNN_CFG_SKINNY_BF16 = 20,
+};
+
+// Returns 0 on success, -1 if the launch failed or cfg is unknown.
+int kudnn_launch_gemm_bf16(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, hipStream_t stream);
+int kudnn_launch_gemm_f32(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, hipStream_t stream);
+// M <= 16, bf16 operands, B contiguous along K.
+int kudnn_launch_skinny_bf16(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream);
+
+// Pack: dst[b][r][k] (row pitch kp, zero for k >= cols) = convert(src element (b, r, k)) where the source
+// element sits at src + b-offset + r*s_r + k*s_k. dst dtype is KUDNN_DT_BF16 or KUDNN_DT_F32.
+struct PackArgs {
+    const void *src;
+    int src_dt;
+    int64_t rows, cols;      // logical rows (M or N) and K
+    int64_t s_r, s_k;        // source strides (elements)
+    int64_t bdim[3];
+    int64_t bs[3];           // source batch strides
+    void *dst;
+    int dst_dt;
+    int64_t kp;              // destination row pitch (elements), >= cols
+    int64_t dst_bstride;     // destination batch stride (elements)
+};
+int kudnn_launch_pack(const PackArgs &p, int64_t batches, hipStream_t stream);
+
+#endif  // KUDNN_KERNELS_H

@@ -1,0 +1,44 @@
+// Kernel argument structures shared by the host planner (capi.cpp) and the HIP kernels.
+// Plain structs passed by value as kernel arguments.
+#ifndef KUDNN_PLAN_TYPES_H
+#define KUDNN_PLAN_TYPES_H
+
+#include <stdint.h>
+
+#include "../../include/kudnn_hip.h"
+
+// Epilogue of one GEMM launch: y[m,n] = bin(act(round_c(alpha*acc + beta*c[m,n] + bias[m,n])), src[m,n]).
+// All strides are in elements; *_bs are the batch strides for the three (right-aligned) batch dims.
+struct EpiParams {
+    float alpha;
+    float beta;
+    float act_alpha;
+    float gamma;
+    int act;      // KUDNN_ACT_*, KUDNN_ACT_UNIMPLEMENTED = none
+    int bin;      // KUDNN_BINARY_*
+    int c_dt;     // dtype of C: rounding point of the GEMM stage and of the activation
+    int bias_dt;
+    int src_dt;
+    int y_dt;
+    int store_c;  // also store the GEMM-stage value to c (LinearResFWD writes C and linearRes)
+    int fast4;    // 4-wide vector epilogue allowed (host-checked contiguity and alignment)
+    void *c;              // C (read when beta != 0, written when store_c)
+    const void *bias;     // nullptr = no bias
+    const void *src;      // binary operand
+    void *y;              // final output
+    int64_t c_sm, c_sn, bias_sm, bias_sn, src_sm, src_sn, y_sm, y_sn;
+    int64_t bdim[3];      // batch dims (right-aligned), product = number of batches in grid.y
+    int64_t c_bs[3], bias_bs[3], src_bs[3], y_bs[3];
+};
+
+// Operands of the MFMA / skinny kernels: A is [M][K] with row stride lda, B is [N][K] with row stride ldb,
+// both contiguous along K ("K-major"), element type = the kernel's compute type.
+struct GemmOperands {
+    const void *a;
+    const void *b;
+    int64_t M, N, K;
+    int64_t lda, ldb;
+    int64_t a_bs[3], b_bs[3];  // batch strides (elements), same batch dims as EpiParams::bdim
+};
+
+#endif  // KUDNN_PLAN_TYPES_H

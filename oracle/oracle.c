@@ -1,0 +1,564 @@
+/*
+ * oracle.c -- CPU restatement of KuDNN's Linear/GEMM + post-op path. TEST INFRASTRUCTURE ONLY.
+ *
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this library, and only
+ * as the checker (or, for the CPU baseline, as the timed port of the reference's portable loops). The
+ * product (libkudnn_hip.so, libkudnn.so) never links or calls it.
+ *
+ * It composes the reference's stages literally, on host arrays, with the reference's storage dtype
+ * between stages:
+ *   oracle_gemm        GEMMWrapper per dtype combination (src/dnn/src/kudnn_gemm.cpp:151-241) inside the
+ *                      broadcast batch loop of BatchedExtendedGemm (:767-807), bias as in AddBias (:65-149)
+ *   oracle_activation  the vml FWD kernels: RELU (kernels/vml/relu/relu.c:14-49, 225-260),
+ *                      SWISH (swish/vml_sve_la_swishf.c:31-47, vml_sve_la_sigmoid.h:25-47),
+ *                      GELU_TANH (gelu_tanh/vml_sve_la_gelu_tanh.h:22-39), GELU_ERF (gelu_erf/vml_sve_la_gelu_erf.h:20-28);
+ *                      f32 math, bf16 results truncated (vml_sve_base.h:111-118)
+ *   oracle_res_add     AddOps (src/dnn/src/kudnn_linear_res.cpp:57-122): flat element-wise over
+ *                      linearRes's size, f32 math, RNE back to bf16
+ *   oracle_binary      the element-wise stage of the post-op chain (ADD/EXT as AddOps; MUL element-wise)
+ *
+ * Deliberate restatement choices (each also stated in DESIGN.md):
+ *   - GEMM sums are accumulated in double and rounded once to f32 (KML's f32 summation order is closed
+ *     and not restatable); fp32 parity is then judged against this correctly-rounded value.
+ *   - cblas_bgemm (bf16 C without bias) has KML-internal rounding; it is restated as RNE of the f32 value.
+ *   - bias is indexed through its own strides (the reference indexes a full [M,N] bias with C's leading
+ *     dimension, which is the same thing whenever bias and C share a layout).
+ *   - RES_EXT computes fmaf(res, gamma, c), the contraction GCC applies to `c + res * gamma` on aarch64.
+ *
+ * Pinning (tests/test_oracle.py): bf16 bit patterns, closed forms and special values of the activations,
+ * integer-valued GEMMs that are exact in f32 whatever the order, numpy float64 matmuls, and the
+ * reference gtest's own naive oracle (linear_activation_gtest.cpp:24-88) restated in numpy.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define O_F32 1
+#define O_F16 2
+#define O_BF16 3
+
+#define O_ACT_NONE 0
+#define O_ACT_RELU 5
+#define O_ACT_GELU_TANH 20
+#define O_ACT_SWISH 25
+#define O_ACT_GELU_ERF 27
+
+#define O_RES_EXT 0
+#define O_RES_MUL 1
+#define O_RES_IDENTIAL 2
+
+#define O_BIN_NONE 0
+#define O_BIN_ADD 1
+#define O_BIN_EXT 2
+#define O_BIN_MUL 3
+
+typedef struct {
+    int32_t ndims;
+    int32_t dtype;
+    int64_t dims[5];
+    int64_t strides[5]; /* logical order, 0 for size-1 dims */
+} otensor;
+
+/* ------------------------------------------------------------------------------------------------ */
+/* element conversions                                                                              */
+
+static uint32_t f2u(float f)
+{
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return u;
+}
+
+static float u2f(uint32_t u)
+{
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* Service::ConvertFp32ToBf16 / vcvth_bf16_f32: BFCVT, round to nearest even (service.cpp:48-67). */
+uint16_t oracle_f32_to_bf16_rne(float f)
+{
+    uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+        return (uint16_t)((u >> 16) | 0x0040u);
+    }
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+/* SvCvtBF16F32FullX: keep the top half of each f32 (vml_sve_base.h:111-118). */
+uint16_t oracle_f32_to_bf16_trunc(float f) { return (uint16_t)(f2u(f) >> 16); }
+
+/* SvF32CvtBf16InfSpecial then truncation (vml_sve_base.h:97-109), used by RELU's bf16 kernel. */
+uint16_t oracle_f32_to_bf16_trunc_inf(float f)
+{
+    uint32_t u = f2u(f);
+    uint32_t a = u & 0x7fffffffu;
+    if (a >= 0x7f7f8000u && a < 0x7f800000u) {
+        u = (u & 0x80000000u) | 0x7f800000u;
+    }
+    return (uint16_t)(u >> 16);
+}
+
+float oracle_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+/* IEEE binary16 <-> binary32, round to nearest even (implicit __fp16 conversions). */
+float oracle_f16_to_f32(uint16_t h)
+{
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1fu;
+    uint32_t man = h & 0x3ffu;
+    if (exp == 0) {
+        if (man == 0) {
+            return u2f(sign);
+        }
+        /* subnormal: value = man * 2^-24 */
+        float v = (float)man * 5.9604644775390625e-8f;
+        return sign ? -v : v;
+    }
+    if (exp == 31) {
+        return u2f(sign | 0x7f800000u | (man << 13));
+    }
+    return u2f(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+uint16_t oracle_f32_to_f16_rne(float f)
+{
+    uint32_t u = f2u(f);
+    uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) {
+        return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));
+    }
+    if (a >= 0x477ff000u) { /* rounds to >= 65520 -> inf */
+        return (uint16_t)(sign | 0x7c00u);
+    }
+    if (a < 0x38800000u) { /* below the smallest normal 2^-14: subnormal or zero */
+        float v = u2f(a) * 16777216.0f; /* in units of 2^-24 */
+        float r = nearbyintf(v);        /* default rounding mode: nearest even */
+        return (uint16_t)(sign | (uint16_t)r);
+    }
+    uint32_t e = (a >> 23) - 112u;
+    uint32_t m = a & 0x7fffffu;
+    uint32_t h = (e << 10) | (m >> 13);
+    uint32_t rem = m & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) {
+        h += 1u;
+    }
+    return (uint16_t)(sign | h);
+}
+
+static float ld(const void *p, int dt, int64_t i)
+{
+    switch (dt) {
+        case O_F32: return ((const float *)p)[i];
+        case O_BF16: return oracle_bf16_to_f32(((const uint16_t *)p)[i]);
+        case O_F16: return oracle_f16_to_f32(((const uint16_t *)p)[i]);
+        default: return 0.0f;
+    }
+}
+
+/* Stores with RNE (the conversion the reference applies when it writes a typed buffer). */
+static void st(void *p, int dt, int64_t i, float v)
+{
+    switch (dt) {
+        case O_F32: ((float *)p)[i] = v; break;
+        case O_BF16: ((uint16_t *)p)[i] = oracle_f32_to_bf16_rne(v); break;
+        case O_F16: ((uint16_t *)p)[i] = oracle_f32_to_f16_rne(v); break;
+        default: break;
+    }
+}
+
+static int64_t total(const otensor *t)
+{
+    int64_t n = 1;
+    if (t->ndims == 0) {
+        return 0;
+    }
+    for (int i = 0; i < t->ndims; ++i) {
+        n *= t->dims[i];
+    }
+    return n;
+}
+
+/* ------------------------------------------------------------------------------------------------ */
+/* activations (vml FWD kernels, f32 math)                                                          */
+
+/* RELU: lanes with x <= 0 are multiplied by alpha, others pass through (relu.c:14-25). */
+static float act_relu(float x, float alpha) { return (x <= 0.0f) ? x * alpha : x; }
+
+/* SWISH: x * 1/(1 + e^t) with t = -alpha*x; t > 87 gives 0, t < -87 gives 1 (vml_sve_la_sigmoid.h:37-47). */
+static float act_swish(float x, float alpha)
+{
+    float t = -alpha * x;
+    float s;
+    if (t > 87.0f) {
+        s = 0.0f;
+    } else if (t < -87.0f) {
+        s = 1.0f;
+    } else {
+        s = 1.0f / (1.0f + expf(t));
+    }
+    return x * s;
+}
+
+/* GELU_TANH: 0.5*x*(1 + tanh(sqrt(2/pi)*x*(1 + 0.044715*x^2))) (vml_sve_la_gelu_tanh.h:22-39). */
+static float act_gelu_tanh(float x)
+{
+    const float c0 = 0.7978845608028654f; /* sqrt(2/pi), 0x1.988454p-1 */
+    const float c1 = 0.044715f;           /* 0x1.6e4e26p-5 */
+    float y = (1.0f + c1 * x * x) * x * c0;
+    return (1.0f + tanhf(y)) * 0.5f * x;
+}
+
+/* GELU_ERF: s + s*erf(x/sqrt(2)) with s = x/2 (vml_sve_la_gelu_erf.h:20-28). */
+static float act_gelu_erf(float x)
+{
+    float s = x * 0.5f;
+    return s + s * erff(x * 0.70710678118654752f);
+}
+
+float oracle_act_f32(int kind, float x, float alpha)
+{
+    switch (kind) {
+        case O_ACT_RELU: return act_relu(x, alpha);
+        case O_ACT_SWISH: return act_swish(x, alpha);
+        case O_ACT_GELU_TANH: return act_gelu_tanh(x);
+        case O_ACT_GELU_ERF: return act_gelu_erf(x);
+        default: return x;
+    }
+}
+
+/* In-place activation over the tensor's elements (ActivationLayerFWD run from a copy of C back into C,
+ * kudnn_linear_activationlayer.cpp:40-56). Element-wise, so the memory walk order does not matter. */
+int oracle_activation(const otensor *t, void *p, int kind, float alpha)
+{
+    const int64_t n = total(t);
+    /* dense tensor: every element sits in [0, n) */
+    for (int64_t i = 0; i < n; ++i) {
+        float x = ld(p, t->dtype, i);
+        float y = oracle_act_f32(kind, x, alpha);
+        if (t->dtype == O_BF16) {
+            ((uint16_t *)p)[i] = (kind == O_ACT_RELU) ? oracle_f32_to_bf16_trunc_inf(y) : oracle_f32_to_bf16_trunc(y);
+        } else {
+            st(p, t->dtype, i, y);
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------------------------------ */
+/* GEMM stage                                                                                      */
+
+typedef struct {
+    otensor a, b, c, bias; /* bias.ndims == 0: no bias */
+    const void *pa, *pb, *pbias;
+    void *pc;
+    float alpha, beta;
+} ogemm;
+
+static void batch_slots(const otensor *t, int64_t dims[3], int64_t bs[3])
+{
+    int nb = t->ndims - 2;
+    for (int s = 0; s < 3; ++s) {
+        dims[s] = 1;
+        bs[s] = 0;
+    }
+    for (int d = 0; d < nb; ++d) {
+        dims[3 - nb + d] = t->dims[d];
+        bs[3 - nb + d] = t->strides[d];
+    }
+}
+
+/* Rounds alpha/beta to bf16 the way GEMMWrapper<bf16,bf16,bf16,float> does for cblas_bgemm (:222-224). */
+static float bf16_round_scalar(float f) { return oracle_bf16_to_f32(oracle_f32_to_bf16_rne(f)); }
+
+/* C = alpha * A x B + beta * C (+ bias), per the dtype rules of GEMMWrapper / ChooseImpl:
+ *  - every sum is formed in f32 (double here, rounded once);
+ *  - bf16 C with bias: f32 temp = f32(C), temp = alpha*AB + beta*temp, temp += bias, RNE (:208-221);
+ *  - bf16 C without bias: cblas_bgemm with bf16 alpha/beta, RNE (:222-226);
+ *  - f32 / f16 C: value rounded once into C's type after bias (all-f32 fallback :672-705). */
+int oracle_gemm(const ogemm *g)
+{
+    const int nd = g->a.ndims;
+    if (nd < 2 || g->b.ndims != nd || g->c.ndims != nd) {
+        return -1;
+    }
+    const int64_t M = g->a.dims[nd - 2], K = g->a.dims[nd - 1], N = g->b.dims[nd - 1];
+    const int hasBias = g->bias.ndims != 0 && total(&g->bias) != 0;
+    float alpha = g->alpha, beta = g->beta;
+    if (!hasBias && g->c.dtype == O_BF16 && g->a.dtype == O_BF16 && g->b.dtype == O_BF16) {
+        alpha = bf16_round_scalar(alpha);
+        beta = bf16_round_scalar(beta);
+    }
+    int64_t ad[3], as[3], bd[3], bs_[3], cd[3], cs[3], xd[3], xs[3] = {0, 0, 0};
+    batch_slots(&g->a, ad, as);
+    batch_slots(&g->b, bd, bs_);
+    batch_slots(&g->c, cd, cs);
+    if (hasBias) {
+        batch_slots(&g->bias, xd, xs);
+    }
+    int64_t L[3];
+    for (int s = 0; s < 3; ++s) {
+        L[s] = ad[s] > bd[s] ? ad[s] : bd[s];
+    }
+    const int64_t a_sm = g->a.strides[nd - 2], a_sk = g->a.strides[nd - 1];
+    const int64_t b_sk = g->b.strides[nd - 2], b_sn = g->b.strides[nd - 1];
+    const int64_t c_sm = g->c.strides[nd - 2], c_sn = g->c.strides[nd - 1];
+    const int64_t x_sm = hasBias ? g->bias.strides[nd - 2] : 0, x_sn = hasBias ? g->bias.strides[nd - 1] : 0;
+
+    for (int64_t i0 = 0; i0 < L[0]; ++i0) {
+        for (int64_t i1 = 0; i1 < L[1]; ++i1) {
+            for (int64_t i2 = 0; i2 < L[2]; ++i2) {
+                const int64_t ao = i0 * as[0] + i1 * as[1] + i2 * as[2];
+                const int64_t bo = i0 * bs_[0] + i1 * bs_[1] + i2 * bs_[2];
+                const int64_t co = i0 * cs[0] + i1 * cs[1] + i2 * cs[2];
+                const int64_t xo = i0 * xs[0] + i1 * xs[1] + i2 * xs[2];
+                /* B of this batch widened once to f32, [K][N] */
+                float *bf = (float *)malloc((size_t)(K * N) * sizeof(float));
+                if (bf == NULL) {
+                    return -2;
+                }
+#pragma omp parallel for schedule(static)
+                for (int64_t k = 0; k < K; ++k) {
+                    for (int64_t n = 0; n < N; ++n) {
+                        bf[k * N + n] = ld(g->pb, g->b.dtype, bo + k * b_sk + n * b_sn);
+                    }
+                }
+#pragma omp parallel for schedule(dynamic, 1)
+                for (int64_t m = 0; m < M; ++m) {
+                    double *acc = (double *)calloc((size_t)N, sizeof(double));
+                    for (int64_t k = 0; k < K; ++k) {
+                        const double av = (double)ld(g->pa, g->a.dtype, ao + m * a_sm + k * a_sk);
+                        if (av == 0.0) {
+                            continue;
+                        }
+                        const float *brow = bf + k * N;
+                        for (int64_t n = 0; n < N; ++n) {
+                            acc[n] += av * (double)brow[n];
+                        }
+                    }
+                    for (int64_t n = 0; n < N; ++n) {
+                        const int64_t ci = co + m * c_sm + n * c_sn;
+                        float v = (float)((double)alpha * acc[n]);
+                        if (beta != 0.0f) {
+                            v = v + beta * ld(g->pc, g->c.dtype, ci);
+                        }
+                        if (hasBias) {
+                            v = v + ld(g->pbias, g->bias.dtype, xo + m * x_sm + n * x_sn);
+                        }
+                        st(g->pc, g->c.dtype, ci, v);
+                    }
+                    free(acc);
+                }
+                free(bf);
+            }
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------------------------------ */
+/* residual stage                                                                                   */
+
+/* AddOps over flat arrays of linearRes's size (kudnn_linear_res.cpp:57-122). All three tensors share one
+ * dtype, as the reference's dispatch on linearRes's type assumes (:192-200). */
+int oracle_res_add(int dtype, int64_t size, const void *c, const void *res, void *out, int kind, float gamma)
+{
+    for (int64_t i = 0; i < size; ++i) {
+        float cv = ld(c, dtype, i), rv = ld(res, dtype, i);
+        float v = (kind == O_RES_IDENTIAL) ? cv + rv : fmaf(rv, gamma, cv);
+        st(out, dtype, i, v);
+    }
+    return 0;
+}
+
+/* Binary stage of the post-op chain on logical (m, n) indices of same-shaped tensors y and src. */
+int oracle_binary(const otensor *y, void *py, const otensor *src, const void *psrc, int kind, float gamma)
+{
+    const int nd = y->ndims;
+    const int64_t n = total(y);
+    for (int64_t lin = 0; lin < n; ++lin) {
+        int64_t rem = lin, yo = 0, so = 0;
+        for (int d = nd - 1; d >= 0; --d) {
+            int64_t idx = rem % y->dims[d];
+            rem /= y->dims[d];
+            yo += idx * y->strides[d];
+            so += idx * src->strides[d];
+        }
+        float v = ld(py, y->dtype, yo), s = ld(psrc, src->dtype, so);
+        float r;
+        if (kind == O_BIN_ADD) {
+            r = v + s;
+        } else if (kind == O_BIN_EXT) {
+            r = fmaf(s, gamma, v);
+        } else {
+            r = v * s;
+        }
+        st(py, y->dtype, yo, r);
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------------------------------ */
+/* composed operators                                                                              */
+
+/* LinearActivationLayerFWD::Run: GEMM (alpha 1, beta 0) into C, then the activation in place
+ * (kudnn_linear_activationlayer.cpp:40-56). */
+int oracle_linear_act(const ogemm *g, int kind, float act_alpha)
+{
+    ogemm h = *g;
+    h.alpha = 1.0f;
+    h.beta = 0.0f;
+    if (oracle_gemm(&h) != 0) {
+        return -1;
+    }
+    return oracle_activation(&g->c, g->pc, kind, act_alpha);
+}
+
+/* LinearResFWD::Run (kudnn_linear_res.cpp:184-202): GEMM into C, then RES_MUL = C x res (second GEMM) or
+ * AddOps over linearRes's size. */
+int oracle_linear_res(const ogemm *g, const otensor *res, const void *pres, const otensor *lr, void *plr, int kind,
+                      float gamma)
+{
+    ogemm h = *g;
+    h.alpha = 1.0f;
+    h.beta = 0.0f;
+    if (oracle_gemm(&h) != 0) {
+        return -1;
+    }
+    if (kind == O_RES_MUL) {
+        ogemm m2;
+        memset(&m2, 0, sizeof(m2));
+        m2.a = g->c;
+        m2.pa = g->pc;
+        m2.b = *res;
+        m2.pb = pres;
+        m2.c = *lr;
+        m2.pc = plr;
+        m2.alpha = 1.0f;
+        m2.beta = 0.0f;
+        return oracle_gemm(&m2);
+    }
+    return oracle_res_add(lr->dtype, total(lr), g->pc, pres, plr, kind, gamma);
+}
+
+/* Post-op chain: GEMM stage, optional activation stage, optional binary stage, each stored in Y's dtype. */
+int oracle_linear_postops(const ogemm *g, int act_kind, float act_alpha, int bin_kind, const otensor *src,
+                          const void *psrc, float gamma)
+{
+    ogemm h = *g;
+    h.alpha = 1.0f;
+    h.beta = 0.0f;
+    if (oracle_gemm(&h) != 0) {
+        return -1;
+    }
+    if (act_kind != O_ACT_NONE) {
+        oracle_activation(&g->c, g->pc, act_kind, act_alpha);
+    }
+    if (bin_kind != O_BIN_NONE) {
+        oracle_binary(&g->c, g->pc, src, psrc, bin_kind, gamma);
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------------------------------ */
+/* seeded inputs: SplitMix64 -> uniform / Box-Muller normal, bf16 by RNE of the f32 sample            */
+
+static uint64_t splitmix64(uint64_t *s)
+{
+    uint64_t z = (*s += 0x9e3779b97f4a7c15ull);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+/* uniform in [0,1) with 53 random bits */
+static double u01(uint64_t *s) { return (double)(splitmix64(s) >> 11) * (1.0 / 9007199254740992.0); }
+
+/* Fills n values: dist 0 = uniform[lo, hi), dist 1 = normal(mean=lo, std=hi). dtype O_F32 / O_BF16 / O_F16. */
+int oracle_fill(void *p, int dtype, int64_t n, uint64_t seed, int dist, double lo, double hi)
+{
+    uint64_t s = seed;
+    for (int64_t i = 0; i < n; ++i) {
+        double v;
+        if (dist == 0) {
+            v = lo + (hi - lo) * u01(&s);
+        } else {
+            double u1 = u01(&s), u2 = u01(&s);
+            if (u1 < 1e-300) {
+                u1 = 1e-300;
+            }
+            v = lo + hi * sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+        }
+        st(p, dtype, i, (float)v);
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------------------------------ */
+/* CPU baseline: the reference tests' portable naive loop (linear_activation_gtest.cpp:66-88, f32
+ * accumulation as in linear_res_gtest.cpp:123-160) for Y[M][N] = act(X[M][K] . W[N][K]^T + bias[N]) with an
+ * optional residual add, parallelised over output rows as MatmulRef does (matmul_gtest.cpp:112). Used only
+ * as the reported CPU baseline. */
+int oracle_cpu_baseline(int dtype, int64_t M, int64_t N, int64_t K, const void *X, const void *W, const void *bias,
+                        const void *R, void *Y, int act, float act_alpha, int threads)
+{
+#ifdef _OPENMP
+    if (threads > 0) {
+        omp_set_num_threads(threads);
+    }
+#else
+    (void)threads;
+#endif
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < M; ++i) {
+        float *xr = (float *)malloc((size_t)K * sizeof(float));
+        for (int64_t l = 0; l < K; ++l) {
+            xr[l] = ld(X, dtype, i * K + l);
+        }
+        for (int64_t j = 0; j < N; ++j) {
+            float sum = 0.0f;
+            if (dtype == O_F32) {
+                const float *wr = (const float *)W + j * K;
+                for (int64_t l = 0; l < K; ++l) {
+                    sum += xr[l] * wr[l];
+                }
+            } else {
+                const uint16_t *wr = (const uint16_t *)W + j * K;
+                for (int64_t l = 0; l < K; ++l) {
+                    sum += xr[l] * u2f((uint32_t)wr[l] << 16);
+                }
+            }
+            float v = sum + (bias ? ld(bias, dtype, j) : 0.0f);
+            if (dtype == O_BF16) {
+                v = oracle_bf16_to_f32(oracle_f32_to_bf16_rne(v));
+            }
+            v = oracle_act_f32(act, v, act_alpha);
+            if (dtype == O_BF16) {
+                v = oracle_bf16_to_f32(oracle_f32_to_bf16_trunc(v));
+            }
+            if (R) {
+                v = v + ld(R, dtype, i * N + j);
+            }
+            st(Y, dtype, i * N + j, v);
+        }
+        free(xr);
+    }
+    return 0;
+}
+
+int oracle_max_threads(void)
+{
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}

@@ -1,0 +1,239 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle on identical seeded inputs.
+
+Small problems are checked in full; the BASELINE configs C1..C5 run at full size on the GPU and are
+checked on a sample of output rows (rows of a GEMM are independent, so the oracle computes exactly those
+rows from the matching rows of X).
+"""
+import numpy as np
+import pytest
+
+import kudnn_amd as K
+import oracle as O
+from support import Case, compare, from_device, sample_rows, zeros_device
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    K.lib()  # fail loudly if the HIP library is missing
+
+
+def dense_rows(t: O.Tensor, rows) -> O.Tensor:
+    """Rows of a dense row-major tensor viewed as [rows, last dim]."""
+    last = t.dims[-1]
+    buf = t.buf.reshape(-1, last)[rows].copy().reshape(-1)
+    return O.Tensor((len(rows), last), (last, 1), t.dtype, buf)
+
+
+def as2d(t: O.Tensor) -> O.Tensor:
+    """A broadcast-batch weight/bias [1,...,r,c] as the 2-D tensor [r,c] (same buffer)."""
+    return O.Tensor(t.dims[-2:], t.strides[-2:], t.dtype, t.buf)
+
+
+# ---------------------------------------------------------------------------------------------------
+# small problems, checked in full
+
+
+@pytest.mark.parametrize("dt", [O.F32, O.BF16])
+@pytest.mark.parametrize("wlayout", ["BA", "AB"])
+@pytest.mark.parametrize("mnk", [(64, 64, 64), (100, 72, 40), (300, 260, 200), (17, 33, 24), (5, 48, 64)])
+@pytest.mark.parametrize("act", [O.ACT_RELU, O.ACT_SWISH, O.ACT_GELU_TANH, O.ACT_GELU_ERF])
+def test_linear_act_small(dt, wlayout, mnk, act):
+    M, N, Kd = mnk
+    x = Case([M, Kd], dt, "AB", seed=10)
+    w = Case([Kd, N], dt, wlayout, seed=11)
+    b = Case([1, N], dt, "AB", seed=12, lo=-0.1, hi=0.1)
+    c = Case([M, N], dt, "AB", zero=True)
+    alpha = 0.0 if act == O.ACT_RELU else 1.0
+    plan = K.LinearActivation(x.desc, w.desc, c.desc, b.desc, alpha, 0.0, act)
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc, b.device())
+    torch.cuda.synchronize()
+    ref = c.clone_empty()
+    O.linear_act(x.t, w.t, ref, b.t, act, alpha)
+    compare(from_device(dc, dt), ref.buf, dt, f"{plan.describe()}")
+
+
+@pytest.mark.parametrize("dt", [O.F32, O.BF16])
+@pytest.mark.parametrize("bias_shape", [None, "1N", "M1", "MN", "11"])
+def test_gemm_bias_kinds(dt, bias_shape):
+    M, N, Kd = 96, 80, 72
+    x = Case([M, Kd], dt, seed=20)
+    w = Case([Kd, N], dt, "BA", seed=21)
+    bdims = {"1N": [1, N], "M1": [M, 1], "MN": [M, N], "11": [1, 1]}.get(bias_shape)
+    b = Case(bdims, dt, seed=22) if bdims else None
+    c = Case([M, N], dt, seed=23)  # beta != 0 reads the old C
+    plan = K.Gemm(x.desc, w.desc, c.desc, b.desc if b else None)
+    dc = c.device()
+    plan.run(x.device(), w.device(), dc, b.device() if b else None, alpha=0.75, beta=0.5)
+    torch.cuda.synchronize()
+    ref = O.Tensor(c.t.dims, c.t.strides, dt, c.t.buf.copy())
+    O.gemm(x.t, w.t, ref, b.t if b else None, alpha=0.75, beta=0.5)
+    compare(from_device(dc, dt), ref.buf, dt, plan.describe())
+
+
+@pytest.mark.parametrize("dt", [O.F32, O.BF16])
+@pytest.mark.parametrize("layouts", [("AB", "AB", "AB"), ("BA", "BA", "AB"), ("AB", "BA", "BA"), ("BA", "AB", "BA")])
+def test_gemm_layouts(dt, layouts):
+    la, lb, lc = layouts
+    M, N, Kd = 70, 90, 56
+    x = Case([M, Kd], dt, la, seed=30)
+    w = Case([Kd, N], dt, lb, seed=31)
+    c = Case([M, N], dt, lc, zero=True)
+    plan = K.Gemm(x.desc, w.desc, c.desc)
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc)
+    torch.cuda.synchronize()
+    ref = c.clone_empty()
+    O.gemm(x.t, w.t, ref)
+    compare(from_device(dc, dt), ref.buf, dt, plan.describe())
+
+
+@pytest.mark.parametrize("dt", [O.F32, O.BF16])
+@pytest.mark.parametrize("kind", [O.RES_IDENTIAL, O.RES_EXT, O.RES_MUL])
+def test_linear_res(dt, kind):
+    M, N, Kd, L = 64, 96, 80, 48
+    x = Case([M, Kd], dt, seed=40)
+    w = Case([Kd, N], dt, "BA", seed=41)
+    b = Case([1, N], dt, seed=42, lo=-0.1, hi=0.1)
+    c = Case([M, N], dt, zero=True)
+    if kind == O.RES_MUL:
+        res = Case([N, L], dt, seed=43)
+        lr = Case([M, L], dt, zero=True)
+    else:
+        res = Case([M, N], dt, seed=43)
+        lr = Case([M, N], dt, zero=True)
+    gamma = 0.625
+    plan = K.LinearRes(x.desc, w.desc, c.desc, b.desc, res.desc, lr.desc, 1.0, 0.0, 1.0, kind)
+    dc, dlr = zeros_device(c), zeros_device(lr)
+    plan.run(x.device(), w.device(), dc, b.device(), res.device(), dlr, gamma)
+    torch.cuda.synchronize()
+    rc, rlr = c.clone_empty(), lr.clone_empty()
+    O.linear_res(x.t, w.t, rc, b.t, res.t, rlr, kind, gamma)
+    compare(from_device(dc, dt), rc.buf, dt, plan.describe() + " C")
+    compare(from_device(dlr, dt), rlr.buf, dt, plan.describe() + " linearRes")
+
+
+@pytest.mark.parametrize("dt", [O.F32, O.BF16])
+def test_batched_broadcast(dt):
+    # 4-D batch with broadcast weight over dim 1 and a bias broadcast over both batch dims
+    x = Case([3, 2, 40, 24], dt, seed=50)
+    w = Case([3, 1, 24, 56], dt, seed=51)
+    b = Case([1, 1, 1, 56], dt, seed=52, lo=-0.1, hi=0.1)
+    c = Case([3, 2, 40, 56], dt, zero=True)
+    plan = K.LinearActivation(x.desc, w.desc, c.desc, b.desc, 1.0, 0.0, K.ACT_SWISH)
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc, b.device())
+    torch.cuda.synchronize()
+    ref = c.clone_empty()
+    O.linear_act(x.t, w.t, ref, b.t, O.ACT_SWISH, 1.0)
+    compare(from_device(dc, dt), ref.buf, dt, plan.describe())
+
+
+def test_host_pointers_staged():
+    # reference-style call with host buffers: the library stages them through device memory
+    dt = O.F32
+    x = Case([110, 20], dt, seed=60)
+    w = Case([20, 200], dt, "AB", seed=61)
+    b = Case([110, 200], dt, seed=62)
+    c = Case([110, 200], dt, zero=True)
+    plan = K.LinearActivation(x.desc, w.desc, c.desc, b.desc, 0.0, 0.0, K.ACT_RELU)
+    out = c.clone_empty()
+    plan.run(x.t.buf, w.t.buf, out.buf, b.t.buf)
+    ref = c.clone_empty()
+    O.linear_act(x.t, w.t, ref, b.t, O.ACT_RELU, 0.0)
+    compare(out.buf, ref.buf, dt, plan.describe())
+
+
+# ---------------------------------------------------------------------------------------------------
+# BASELINE configs at full size
+
+
+def test_c1_fp32_relu_full():
+    x = Case([128, 1024], O.F32, seed=0)
+    w = Case([1024, 1024], O.F32, "BA", seed=1)
+    b = Case([1, 1024], O.F32, seed=2, lo=-0.1, hi=0.1)
+    c = Case([128, 1024], O.F32, zero=True)
+    plan = K.LinearActivation(x.desc, w.desc, c.desc, b.desc, 0.0, 0.0, K.ACT_RELU)
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc, b.device())
+    torch.cuda.synchronize()
+    ref = c.clone_empty()
+    O.linear_act(x.t, w.t, ref, b.t, O.ACT_RELU, 0.0)
+    compare(from_device(dc, O.F32), ref.buf, O.F32, "C1")
+
+
+def test_c2_fp32_silu_rows():
+    M, Kd, N = 2048, 4096, 4096
+    x = Case([M, Kd], O.F32, seed=0, dist="normal", lo=0.0, hi=1.0)
+    w = Case([Kd, N], O.F32, "BA", seed=1, dist="normal", lo=0.0, hi=1.0 / 64)
+    b = Case([1, N], O.F32, seed=2, dist="normal", lo=0.0, hi=0.02)
+    c = Case([M, N], O.F32, zero=True)
+    plan = K.LinearActivation(x.desc, w.desc, c.desc, b.desc, 1.0, 0.0, K.ACT_SWISH)
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc, b.device())
+    torch.cuda.synchronize()
+    got = from_device(dc, O.F32).reshape(M, N)
+    rows = sample_rows(M, 24)
+    ref = O.empty((len(rows), N), (N, 1), O.F32)
+    O.linear_act(dense_rows(x.t, rows), w.t, ref, b.t, O.ACT_SWISH, 1.0)
+    compare(got[rows].reshape(-1), ref.buf, O.F32, "C2 " + plan.describe())
+
+
+def test_c3_bf16_gelu_residual_rows():
+    M, Kd, N = 4096, 4096, 11008
+    x = Case([M, Kd], O.BF16, seed=0, dist="normal", lo=0.0, hi=1.0)
+    w = Case([Kd, N], O.BF16, "BA", seed=1, dist="normal", lo=0.0, hi=0.02)
+    b = Case([1, N], O.BF16, zero=True)
+    r = Case([M, N], O.BF16, seed=3, dist="normal", lo=0.0, hi=1.0)
+    y = Case([M, N], O.BF16, zero=True)
+    plan = K.LinearPostOps(x.desc, w.desc, y.desc, b.desc, act=K.ACT_GELU_TANH, binary=K.BIN_ADD, src=r.desc)
+    dy = zeros_device(y)
+    plan.run(x.device(), w.device(), dy, b.device(), r.device())
+    torch.cuda.synchronize()
+    got = from_device(dy, O.BF16).reshape(M, N)
+    rows = sample_rows(M, 24)
+    ref = O.empty((len(rows), N), (N, 1), O.BF16)
+    O.linear_postops(dense_rows(x.t, rows), w.t, ref, b.t, O.ACT_GELU_TANH, 0.0, O.BIN_ADD, dense_rows(r.t, rows))
+    maxnorm, exact = compare(got[rows].reshape(-1), ref.buf, O.BF16, "C3 " + plan.describe())
+    print(f"C3 max-normalised error {maxnorm:.3e}, bit-exact fraction {exact:.5f}")
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+@pytest.mark.parametrize("N", [4096, 14336])
+def test_c4_skinny_mul(M, N):
+    Kd = 4096
+    x = Case([M, Kd], O.BF16, seed=0, dist="normal", lo=0.0, hi=1.0)
+    w = Case([Kd, N], O.BF16, "BA", seed=1, dist="normal", lo=0.0, hi=0.02)
+    m2 = Case([M, N], O.BF16, seed=3, lo=0.5, hi=1.5)
+    y = Case([M, N], O.BF16, zero=True)
+    plan = K.LinearPostOps(x.desc, w.desc, y.desc, binary=K.BIN_MUL, src=m2.desc)
+    assert plan.describe().startswith("skinny")
+    dy = zeros_device(y)
+    plan.run(x.device(), w.device(), dy, None, m2.device())
+    torch.cuda.synchronize()
+    ref = y.clone_empty()
+    O.linear_postops(x.t, w.t, ref, None, O.ACT_NONE, 0.0, O.BIN_MUL, m2.t)
+    compare(from_device(dy, O.BF16), ref.buf, O.BF16, f"C4 M={M} N={N}")
+
+
+def test_c5_bf16_3d_silu_kmajor_rows():
+    B, S, Kd, N = 8, 2048, 5120, 13824
+    x = Case([B, S, Kd], O.BF16, "ABC", seed=0, dist="normal", lo=0.0, hi=1.0)
+    w = Case([1, Kd, N], O.BF16, "ABC", seed=1, dist="normal", lo=0.0, hi=0.014)
+    b = Case([1, 1, N], O.BF16, "ABC", seed=2, dist="normal", lo=0.0, hi=0.02)
+    y = Case([B, S, N], O.BF16, "ABC", zero=True)
+    plan = K.LinearActivation(x.desc, w.desc, y.desc, b.desc, 1.0, 0.0, K.ACT_SWISH)
+    dy = zeros_device(y)
+    plan.run(x.device(), w.device(), dy, b.device())
+    torch.cuda.synchronize()
+    got = from_device(dy, O.BF16).reshape(B * S, N)
+    rows = sample_rows(B * S, 24)
+    ref = O.empty((len(rows), N), (N, 1), O.BF16)
+    O.linear_act(dense_rows(x.t, rows), as2d(w.t), ref, as2d(b.t), O.ACT_SWISH, 1.0)
+    compare(got[rows].reshape(-1), ref.buf, O.BF16, "C5 " + plan.describe())
