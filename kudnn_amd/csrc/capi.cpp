@@ -463,8 +463,12 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
     // Operands the MFMA kernels cannot read in place: wrong dtype, not contiguous along K, or rows /
     // batches not aligned to 16-byte chunks.
     const int epc = ElemsPerChunk(core.computeDt);
+    const int64_t bk = core.computeDt == KUDNN_DT_F32 ? 32 : 64;
+    // The MFMA kernels need K to be a whole number of k-tiles (a padded pack provides it); the skinny
+    // kernel masks its K tail itself.
+    const bool kTiles = core.M <= 16 && core.computeDt == KUDNN_DT_BF16 ? true : (core.K % bk == 0);
     auto needsPack = [&](const OperandSpec &o) {
-        bool direct = o.dt == core.computeDt && (o.s_k == 1) && (core.K % epc == 0) && (o.s_r % epc == 0);
+        bool direct = o.dt == core.computeDt && (o.s_k == 1) && (core.K % epc == 0) && (o.s_r % epc == 0) && kTiles;
         for (int s = 0; s < 3; ++s) {
             direct = direct && (o.bs[s] % epc == 0);
         }
@@ -472,7 +476,6 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
     };
     core.A.staticPack = needsPack(core.A);
     core.B.staticPack = needsPack(core.B);
-    const int64_t bk = core.computeDt == KUDNN_DT_F32 ? 32 : 64;
     core.kp = (core.K + bk - 1) / bk * bk;
 
     // engine and tile configuration
@@ -590,7 +593,9 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
     GemmOperands op{};
     op.M = core.M;
     op.N = core.N;
-    op.K = core.K;
+    // MFMA kernels run whole k-tiles: when K is not a multiple of the tile both operands were packed with
+    // zero padding up to kp (and kp == K otherwise). The skinny kernel masks its own K tail.
+    op.K = core.engine == ENGINE_SKINNY_BF16 ? core.K : core.kp;
     auto setupOperand = [&](const OperandSpec &o, const void *ptr, bool pack, void *dst, const void *&outPtr,
                             int64_t &ld, int64_t outBs[3]) -> int {
         if (!pack) {
@@ -690,6 +695,22 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
         fast = fast && Vec4Ok(src, x.Src.dt, x.Src, false);
     }
     ep.fast4 = fast ? 1 : 0;
+    // 8-wide: 16-byte vector accesses on y / src / bf16 bias, rows and batches 8-element aligned
+    auto vec8 = [](const void *p, const TensorSpec &t) {
+        if (t.sn != 1 || t.sm % 8 != 0) return false;
+        for (int s = 0; s < 3; ++s) {
+            if (t.bs[s] % 8 != 0) return false;
+        }
+        return Aligned(p, 16);
+    };
+    bool fast8 = fast && vec8(ep.y, Y);
+    if (x.hasSrc) {
+        fast8 = fast8 && vec8(src, x.Src);
+    }
+    if (core.hasBias && core.Bias.sn != 0) {
+        fast8 = fast8 && vec8(bias, core.Bias);
+    }
+    ep.fast8 = fast8 ? 1 : 0;
 
     int lrc = 0;
     if (core.engine == ENGINE_SKINNY_BF16) {

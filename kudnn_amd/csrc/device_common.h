@@ -297,6 +297,103 @@ __device__ __forceinline__ void epi_apply4(const EpiParams &e, const EpiBatch &o
     }
 }
 
+// Epilogue for eight consecutive columns n..n+7 of row m (n a multiple of 8): one 16-byte bf16 (or two
+// 16-byte f32) store per call when the output rows are contiguous and 8-element aligned (fast8).
+__device__ __forceinline__ void epi_apply8(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, int64_t N,
+                                           const float acc[8])
+{
+    if (n + 7 < N && e.fast8) {
+        float v[8];
+        float bv[8];
+        if (e.bias != nullptr) {
+            const int64_t bi = ob.bias + m * e.bias_sm + n * e.bias_sn;
+            if (e.bias_sn == 0) {
+                const float b0 = load_elem(e.bias, e.bias_dt, bi);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) bv[q] = b0;
+            } else if (e.bias_dt == KUDNN_DT_BF16) {
+                const uint4 raw = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(e.bias) + bi);
+                const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    bv[2 * q] = u2f(w[q] << 16);
+                    bv[2 * q + 1] = u2f(w[q] & 0xffff0000u);
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 8; ++q) bv[q] = load_elem(e.bias, e.bias_dt, bi + q);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) bv[q] = 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            v[q] = round_store(e.c_dt, acc[q] * e.alpha + bv[q]);
+        }
+        if (e.store_c) {
+            const int64_t ci = ob.c + m * e.c_sm + n;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) store_elem(e.c, e.c_dt, ci + q, v[q]);
+        }
+        if (e.act != KUDNN_ACT_UNIMPLEMENTED) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) v[q] = act_round(e.c_dt, e.act, apply_act(e.act, v[q], e.act_alpha));
+        }
+        if (e.bin != KUDNN_BINARY_NONE) {
+            const int64_t si = ob.src + m * e.src_sm + n;
+            float sv[8];
+            if (e.src_dt == KUDNN_DT_BF16) {
+                const uint4 raw = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(e.src) + si);
+                const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    sv[2 * q] = u2f(w[q] << 16);
+                    sv[2 * q + 1] = u2f(w[q] & 0xffff0000u);
+                }
+            } else if (e.src_dt == KUDNN_DT_F32) {
+                const float4 t0 = *reinterpret_cast<const float4 *>(static_cast<const float *>(e.src) + si);
+                const float4 t1 = *reinterpret_cast<const float4 *>(static_cast<const float *>(e.src) + si + 4);
+                sv[0] = t0.x; sv[1] = t0.y; sv[2] = t0.z; sv[3] = t0.w;
+                sv[4] = t1.x; sv[5] = t1.y; sv[6] = t1.z; sv[7] = t1.w;
+            } else {
+#pragma unroll
+                for (int q = 0; q < 8; ++q) sv[q] = load_elem(e.src, e.src_dt, si + q);
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                if (e.bin == KUDNN_BINARY_ADD) {
+                    v[q] = v[q] + sv[q];
+                } else if (e.bin == KUDNN_BINARY_EXT) {
+                    v[q] = fmaf(sv[q], e.gamma, v[q]);
+                } else {
+                    v[q] = v[q] * sv[q];
+                }
+            }
+        }
+        const int64_t yi = ob.y + m * e.y_sm + n;
+        if (e.y_dt == KUDNN_DT_BF16) {
+            uint32_t w[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                w[q] = static_cast<uint32_t>(f32_to_bf16_rne(v[2 * q])) |
+                       (static_cast<uint32_t>(f32_to_bf16_rne(v[2 * q + 1])) << 16);
+            }
+            *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(e.y) + yi) = make_uint4(w[0], w[1], w[2], w[3]);
+        } else if (e.y_dt == KUDNN_DT_F32) {
+            float *yp = static_cast<float *>(e.y) + yi;
+            *reinterpret_cast<float4 *>(yp) = make_float4(v[0], v[1], v[2], v[3]);
+            *reinterpret_cast<float4 *>(yp + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) store_elem(e.y, e.y_dt, yi + q, v[q]);
+        }
+        return;
+    }
+    epi_apply4(e, ob, m, n, N, acc);
+    epi_apply4(e, ob, m, n + 4, N, acc + 4);
+}
+
 // XCD-aware block order. The hardware deals workgroups round-robin over the 8 XCDs (block b runs on
 // XCD b % 8); this maps the hardware id to a logical id such that consecutive logical ids run on the
 // same XCD and therefore share its L2.

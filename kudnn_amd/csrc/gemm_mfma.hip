@@ -5,19 +5,26 @@
 // cblas_bgemm (bf16) and cblas_sgemm (fp32) in the reference (src/dnn/src/kudnn_gemm.cpp:157-241) plus
 // its post-op passes.
 //
-// Design (one workgroup per BM x BN output tile, 4 waves as 2 x 2):
-//  - A and B k-tiles of 128 bytes per row (64 bf16 / 32 fp32) are staged global -> registers -> LDS,
-//    double buffered: the global loads of tile k+1 are in flight while the MFMAs of tile k run; one
-//    barrier per k-tile.
-//  - LDS rows are 128 B with the 16-byte chunk index XOR-swizzled by (row & 7), so the ds_read_b128 of
-//    32 consecutive rows at one k-chunk hits every bank once.
+// Design (one workgroup of 4 waves per BM x BN output tile, waves arranged 2 x 2):
+//  - k-tiles of 128 bytes per row (64 bf16 / 32 fp32) go straight from global memory into LDS with
+//    gfx950's global_load_lds_dwordx4 (no staging registers), double buffered: the loads of tile k+1 are
+//    issued right after the barrier that opens tile k and land while tile k's MFMAs run.
+//  - A wave's LDS DMA instruction fills 8 rows x 128 bytes; lane l writes 16-byte slot l, and fetches the
+//    global chunk that the XOR swizzle (chunk ^ (row & 7)) assigns to that slot, so the ds_read_b128 of
+//    32 consecutive rows at one logical k-chunk hits every bank once.
+//  - MFMA fragments of k16-substep s+1 are read from LDS while substep s's MFMAs issue.
 //  - bf16: v_mfma_f32_32x32x16_bf16; fp32: v_mfma_f32_32x32x2f32 fed from one 16-byte LDS read per lane
 //    (four k values; MFMA q consumes element q of both lane halves, which covers every k exactly once).
 //  - The operands are swapped (weight tile as the first MFMA operand): each lane then owns, per 32x32
-//    sub-tile, one output row m and four runs of four consecutive columns n, so the epilogue issues
-//    8-byte (bf16) / 16-byte (f32) stores and residual loads.
+//    sub-tile, one output row m and four runs of four consecutive columns n.
+//  - Epilogue: the accumulators pass through LDS, one 32-column strip per wave at a time, and are read
+//    back row-major so each lane applies bias / activation / residual to 8 consecutive columns and
+//    writes them with one 16-byte store (a wave writes 16 rows x 64 contiguous bytes per instruction).
 //  - Blocks are remapped so consecutive tiles run on the same XCD and walked in groups of tile-rows.
+// Requirements (the dispatcher packs operands otherwise): K a multiple of the k-tile, rows 16-byte
+// aligned. Rows past M / N are clamped (read but never stored).
 #include <type_traits>
+#include <utility>
 
 #include "device_common.h"
 #include "kernels.h"
@@ -29,29 +36,49 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kChunks = 8;   // 16-byte chunks per 128-byte LDS row
+constexpr int kStagePitch = 36;  // epilogue staging row pitch in floats (32 columns + 4 pad)
+// s_waitcnt immediate for vmcnt(0) with expcnt/lgkmcnt left unconstrained (gfx9 encoding: vmcnt[3:0] and
+// [15:14], expcnt[6:4], lgkmcnt[11:8]).
+constexpr int kWaitVmcnt0 = 0x0F70;
 
 __device__ __forceinline__ int swz(int row, int chunk) { return (chunk ^ (row & 7)); }
 
-template <bool F32, int BM, int BN, int WM, int WN, bool KTAIL>
+// Calls f(std::integral_constant<int, I>) for I = 0 .. N-1 (a loop whose index is a compile-time constant).
+template <int... I, typename F>
+__device__ __forceinline__ void static_for_impl(std::integer_sequence<int, I...>, F &&f)
+{
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f)
+{
+    static_for_impl(std::make_integer_sequence<int, N>{}, f);
+}
+
+template <bool F32, int BM, int BN, int WM, int WN>
 __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands op, EpiParams ep, int tilesM,
                                                                   int tilesN, int group)
 {
     using T = typename std::conditional<F32, float, uint16_t>::type;
     constexpr int EPC = 16 / static_cast<int>(sizeof(T));  // elements per 16-byte chunk
     constexpr int kBK = kChunks * EPC;                      // k-tile in elements
-    constexpr int NT = WM * WN * 64;
+    constexpr int NW = WM * WN;                             // waves
     constexpr int TM = BM / WM;   // wave tile rows (m)
     constexpr int TN = BN / WN;   // wave tile cols (n)
     constexpr int FM = TM / 32;   // 32x32 sub-tiles per wave along m
     constexpr int FN = TN / 32;   // ... along n
-    constexpr int CA = BM * kChunks / NT;  // 16-byte chunks per thread per A tile
-    constexpr int CB = BN * kChunks / NT;
-    constexpr int ROWS_PER_PASS = NT / kChunks;
+    constexpr int GA = BM / 8 / NW;  // 8-row LDS DMA groups per wave per A tile
+    constexpr int GB = BN / 8 / NW;
+    static_assert(GA >= 1 && GB >= 1, "tile too small for the wave count");
+    static_assert(NW * TM * kStagePitch * 4 <= (BM + BN) * kChunks * 16 * 2, "epilogue staging exceeds LDS");
 
-    __shared__ uint4 sA[2][BM * kChunks];
-    __shared__ uint4 sB[2][BN * kChunks];
+    // one LDS array: two A stages, then two B stages; reused as epilogue staging after the k-loop
+    __shared__ uint4 lds[2 * (BM + BN) * kChunks];
+    uint4(*sA)[BM * kChunks] = reinterpret_cast<uint4(*)[BM * kChunks]>(lds);
+    uint4(*sB)[BN * kChunks] = reinterpret_cast<uint4(*)[BN * kChunks]>(lds + 2 * BM * kChunks);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -72,46 +99,35 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
     const T *B = static_cast<const T *>(op.b) + i0 * op.b_bs[0] + i1 * op.b_bs[1] + i2 * op.b_bs[2];
     const int64_t M = op.M, N = op.N, K = op.K;
 
-    // Per-thread global source rows (clamped into range; out-of-range rows are never stored).
-    const int chunk = tid & (kChunks - 1);
-    const int rowBase = tid / kChunks;
-    const T *pa[CA];
-    const T *pb[CB];
+    // This lane's source in every DMA group: row (8-row group base) + lane/8, logical chunk chosen so that
+    // LDS slot (lane % 8) of the row holds swizzled chunk (lane % 8).
+    const int lrow8 = lane >> 3;
+    const int lchunk = (lane & 7) ^ lrow8;
+    const T *pa[GA];
+    const T *pb[GB];
 #pragma unroll
-    for (int j = 0; j < CA; ++j) {
-        int64_t r = m0 + rowBase + j * ROWS_PER_PASS;
+    for (int j = 0; j < GA; ++j) {
+        int64_t r = m0 + (wave * GA + j) * 8 + lrow8;
         r = r < M ? r : M - 1;
-        pa[j] = A + r * op.lda + chunk * EPC;
+        pa[j] = A + r * op.lda + lchunk * EPC;
     }
 #pragma unroll
-    for (int j = 0; j < CB; ++j) {
-        int64_t r = n0 + rowBase + j * ROWS_PER_PASS;
+    for (int j = 0; j < GB; ++j) {
+        int64_t r = n0 + (wave * GB + j) * 8 + lrow8;
         r = r < N ? r : N - 1;
-        pb[j] = B + r * op.ldb + chunk * EPC;
+        pb[j] = B + r * op.ldb + lchunk * EPC;
     }
 
-    uint4 ra[CA], rb[CB];
-    auto load_tile = [&](int64_t k0) {
-        const bool inK = !KTAIL || (k0 + chunk * EPC < K);
+    auto issue_tile = [&](int buf, int64_t k0) {
 #pragma unroll
-        for (int j = 0; j < CA; ++j) {
-            ra[j] = inK ? *reinterpret_cast<const uint4 *>(pa[j] + k0) : make_uint4(0, 0, 0, 0);
+        for (int j = 0; j < GA; ++j) {
+            __builtin_amdgcn_global_load_lds(static_cast<const void *>(pa[j] + k0),
+                                             (lds_void *)(&sA[buf][(wave * GA + j) * 64]), 16, 0, 0);
         }
 #pragma unroll
-        for (int j = 0; j < CB; ++j) {
-            rb[j] = inK ? *reinterpret_cast<const uint4 *>(pb[j] + k0) : make_uint4(0, 0, 0, 0);
-        }
-    };
-    auto store_tile = [&](int buf) {
-#pragma unroll
-        for (int j = 0; j < CA; ++j) {
-            int row = rowBase + j * ROWS_PER_PASS;
-            sA[buf][row * kChunks + swz(row, chunk)] = ra[j];
-        }
-#pragma unroll
-        for (int j = 0; j < CB; ++j) {
-            int row = rowBase + j * ROWS_PER_PASS;
-            sB[buf][row * kChunks + swz(row, chunk)] = rb[j];
+        for (int j = 0; j < GB; ++j) {
+            __builtin_amdgcn_global_load_lds(static_cast<const void *>(pb[j] + k0),
+                                             (lds_void *)(&sB[buf][(wave * GB + j) * 64]), 16, 0, 0);
         }
     };
 
@@ -125,33 +141,44 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
         }
     }
 
-    const int KT = static_cast<int>((K + kBK - 1) / kBK);
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
-
     const int lrow = lane & 31;
     const int lhalf = lane >> 5;
+    const int KT = static_cast<int>(K / kBK);
+
+    issue_tile(0, 0);
     for (int kt = 0; kt < KT; ++kt) {
         const int cur = kt & 1;
+        // Wait for this thread's DMA of tile kt (vmcnt(0)); the barrier then makes every wave's tile kt
+        // visible and guarantees every wave finished reading buffer cur ^ 1 (tile kt - 1).
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __syncthreads();
         if (kt + 1 < KT) {
-            load_tile(static_cast<int64_t>(kt + 1) * kBK);
+            issue_tile(cur ^ 1, static_cast<int64_t>(kt + 1) * kBK);
         }
-#pragma unroll
-        for (int s = 0; s < kChunks / 2; ++s) {
-            // lane half h reads 16-byte chunk 2s+h of its row
-            const int c = s * 2 + lhalf;
-            uint4 va[FM], vb[FN];
+        uint4 va[2][FM], vb[2][FN];
+        auto read_frags = [&](int slot, int s) {
+            const int c = s * 2 + lhalf;  // lane half h reads 16-byte chunk 2s+h of its row
 #pragma unroll
             for (int i = 0; i < FM; ++i) {
-                int row = wm * TM + i * 32 + lrow;
-                va[i] = sA[cur][row * kChunks + swz(row, c)];
+                const int row = wm * TM + i * 32 + lrow;
+                va[slot][i] = sA[cur][row * kChunks + swz(row, c)];
             }
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
-                int row = wn * TN + j * 32 + lrow;
-                vb[j] = sB[cur][row * kChunks + swz(row, c)];
+                const int row = wn * TN + j * 32 + lrow;
+                vb[slot][j] = sB[cur][row * kChunks + swz(row, c)];
             }
+        };
+        read_frags(0, 0);
+#pragma unroll
+        for (int s = 0; s < kChunks / 2; ++s) {
+            if (s + 1 < kChunks / 2) {
+                read_frags((s + 1) & 1, s + 1);
+            }
+            // Keep the next substep's LDS reads ahead of this substep's MFMAs (the scheduler would
+            // otherwise sink them next to their uses and expose the LDS latency every few MFMAs).
+            __builtin_amdgcn_sched_barrier(0);
+            const int sl = s & 1;
             if constexpr (F32) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -159,8 +186,8 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
                     for (int j = 0; j < FN; ++j) {
 #pragma unroll
                         for (int i = 0; i < FM; ++i) {
-                            f32x4_t a4 = __builtin_bit_cast(f32x4_t, va[i]);
-                            f32x4_t b4 = __builtin_bit_cast(f32x4_t, vb[j]);
+                            const f32x4_t a4 = __builtin_bit_cast(f32x4_t, va[sl][i]);
+                            const f32x4_t b4 = __builtin_bit_cast(f32x4_t, vb[sl][j]);
                             acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x2f32(b4[q], a4[q], acc[j][i], 0, 0, 0);
                         }
                     }
@@ -170,54 +197,61 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
                 for (int j = 0; j < FN; ++j) {
 #pragma unroll
                     for (int i = 0; i < FM; ++i) {
-                        acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vb[j]),
-                                                                            __builtin_bit_cast(bf16x8_t, va[i]),
+                        acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vb[sl][j]),
+                                                                            __builtin_bit_cast(bf16x8_t, va[sl][i]),
                                                                             acc[j][i], 0, 0, 0);
                     }
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        if (kt + 1 < KT) {
-            store_tile(cur ^ 1);
-        }
-        __syncthreads();
     }
 
-    // Epilogue. Sub-tile (j, i): lane holds output row m = ... + (lane & 31) and, for register group g,
-    // columns n = ... + 8g + 4*(lane >> 5) + {0,1,2,3}.
+    // Epilogue through LDS, one 32-column strip of each wave tile at a time. The strip index is a
+    // compile-time constant (static_for) so the accumulators stay in registers.
+    float *stage = reinterpret_cast<float *>(lds) + wave * (TM * kStagePitch);
     const EpiBatch ob = epi_batch_offsets(ep, batch);
+    static_for<FN>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        __syncthreads();  // previous strip fully read back (and, for j = 0, the k-loop's last LDS reads done)
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-        const int64_t m = m0 + wm * TM + i * 32 + lrow;
-        if (m >= M) continue;
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
+        for (int i = 0; i < FM; ++i) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const int64_t n = n0 + wn * TN + j * 32 + g * 8 + lhalf * 4;
-                if (n >= N) continue;
-                float v[4] = {acc[j][i][4 * g + 0], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2], acc[j][i][4 * g + 3]};
-                epi_apply4(ep, ob, m, n, N, v);
+                float *dst = stage + (i * 32 + lrow) * kStagePitch + g * 8 + lhalf * 4;
+                *reinterpret_cast<float4 *>(dst) =
+                    make_float4(acc[j][i][4 * g + 0], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2], acc[j][i][4 * g + 3]);
             }
         }
-    }
+        __syncthreads();
+        // row-major read back: 4 lanes per row, 8 columns per lane, 16 rows per pass
+        const int col8 = (lane & 3) * 8;
+        for (int r = lane >> 2; r < TM; r += 16) {
+            const int64_t m = m0 + wm * TM + r;
+            const int64_t n = n0 + wn * TN + j * 32 + col8;
+            if (m < M && n < N) {
+                const float *src = stage + r * kStagePitch + col8;
+                const float4 lo = *reinterpret_cast<const float4 *>(src);
+                const float4 hi = *reinterpret_cast<const float4 *>(src + 4);
+                const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                epi_apply8(ep, ob, m, n, N, v);
+            }
+        }
+    });
 }
 
 template <bool F32, int BM, int BN, int WM, int WN>
 int launch_cfg(const GemmOperands &op, const EpiParams &ep, int64_t batches, int group, hipStream_t stream)
 {
     constexpr int kBK = F32 ? 32 : 64;
+    if (op.K % kBK != 0) {
+        return -1;  // the dispatcher pads K by packing
+    }
     int tilesM = static_cast<int>((op.M + BM - 1) / BM);
     int tilesN = static_cast<int>((op.N + BN - 1) / BN);
     dim3 grid(static_cast<unsigned>(tilesM * tilesN), static_cast<unsigned>(batches));
     dim3 block(WM * WN * 64);
-    if (op.K % kBK == 0) {
-        hipLaunchKernelGGL((gemm_mfma_kernel<F32, BM, BN, WM, WN, false>), grid, block, 0, stream, op, ep, tilesM,
-                           tilesN, group);
-    } else {
-        hipLaunchKernelGGL((gemm_mfma_kernel<F32, BM, BN, WM, WN, true>), grid, block, 0, stream, op, ep, tilesM,
-                           tilesN, group);
-    }
+    hipLaunchKernelGGL((gemm_mfma_kernel<F32, BM, BN, WM, WN>), grid, block, 0, stream, op, ep, tilesM, tilesN, group);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -22,6 +22,7 @@ struct EpiParams {
     int y_dt;
     int store_c;  // also store the GEMM-stage value to c (LinearResFWD writes C and linearRes)
     int fast4;    // 4-wide vector epilogue allowed (host-checked contiguity and alignment)
+    int fast8;    // 8-wide vector epilogue allowed
     void *c;              // C (read when beta != 0, written when store_c)
     const void *bias;     // nullptr = no bias
     const void *src;      // binary operand

@@ -97,7 +97,7 @@ __global__ __launch_bounds__(KW * 64) void skinny_bf16_kernel(GemmOperands op, E
         return;
     }
     const EpiBatch ob = epi_batch_offsets(ep, batch);
-    float v[4] = {sum[0], sum[1], sum[2], sum[3]};
+    const float v[4] = {sum[0], sum[1], sum[2], sum[3]};
     epi_apply4(ep, ob, r16, n, N, v);
 }
 
