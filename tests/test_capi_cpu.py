@@ -1,0 +1,157 @@
+"""C ABI checks that need no GPU: the library loads and exports every entry point include/kudnn_hip.h
+declares, descriptors get KuDNN's strides, validation follows KuDNN's rules, and the dispatcher picks the
+intended kernel family for each BASELINE config. (Plan creation makes no HIP calls.)"""
+import re
+from pathlib import Path
+
+import pytest
+
+import kudnn_amd as K
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def declared_symbols():
+    text = (ROOT / "include" / "kudnn_hip.h").read_text()
+    return sorted(set(re.findall(r"KUDNN_HIP_API\s+[\w\s\*]+?\b(kudnn_\w+)\s*\(", text)))
+
+
+def test_header_declares_what_the_binding_binds():
+    decl = declared_symbols()
+    assert len(decl) >= 30
+    assert sorted(K.exported_symbols()) == decl
+
+
+def test_library_exports_every_declared_symbol():
+    lib = K.lib()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert K.lib().kudnn_version().decode().startswith("kudnn-mi355x")
+
+
+def test_cpp_library_exports_kudnn_classes():
+    import ctypes
+    import subprocess
+
+    so = K.LIB_DIR / "libkudnn.so"
+    ctypes.CDLL(str(so))
+    out = subprocess.run(["nm", "-DC", "--defined-only", str(so)], capture_output=True, text=True, check=True).stdout
+    for sym in ("KuDNN::Gemm::Gemm(", "KuDNN::Gemm::Run(", "KuDNN::LinearActivationLayerFWD::Run(",
+                "KuDNN::LinearResFWD::Run(", "KuDNN::LinearPostOpsFWD::Run(", "KuDNN::Threading::GetMaxNumThreads()",
+                "KuDNN::TensorInfo::ValidateLayout<false>", "KuDNN::Service::AlignedAlloc("):
+        assert sym in out, sym
+
+
+@pytest.mark.parametrize("layout,dims,strides", [
+    ("AB", [3, 4], (4, 1)),
+    ("BA", [3, 4], (1, 3)),
+    ("AB", [1, 4], (0, 1)),
+    ("ABC", [2, 3, 4], (12, 4, 1)),
+    ("ACB", [2, 3, 4], (12, 1, 3)),
+    ("CAB", [2, 3, 4], (3, 1, 6)),
+    ("ABCED", [2, 3, 4, 5, 6], (360, 120, 30, 1, 5)),
+    ("DECAB", [2, 3, 4, 5, 6], (3, 1, 6, 144, 24)),
+])
+def test_descriptor_min_strides(layout, dims, strides):
+    d = K.desc(dims, K.F32, layout)
+    assert d.stride() == strides
+    assert K.lib().kudnn_tensor_desc_is_dense(d) == 1
+
+
+def test_descriptor_errors():
+    with pytest.raises(K.KudnnError) as e:
+        K.desc([2, 3], K.F32, "ABC")
+    assert e.value.status == K.BAD_ARGUMENTS
+    with pytest.raises(K.KudnnError):
+        K.desc([2, 3], K.DT_UNDEFINED, "AB")
+    with pytest.raises(K.KudnnError):
+        K.desc([4, 5], K.F32, "AB", strides=[4, 1])  # below the minimum stride
+    d = K.desc([4, 5], K.F32, "AB", strides=[8, 1])
+    assert K.lib().kudnn_tensor_desc_is_dense(d) == 0
+
+
+def validate(a, b, c, bias=None, nt=0):
+    return K.lib().kudnn_gemm_validate(a, b, c, bias, nt)
+
+
+def test_gemm_validation_rules():
+    F = K.F32
+    a, b, c = K.desc([5, 6], F), K.desc([6, 7], F, "BA"), K.desc([5, 7], F)
+    assert validate(a, b, c) == K.SUCCESS
+    assert validate(a, K.desc([7, 7], F), c) == K.BAD_ARGUMENTS                    # K mismatch
+    assert validate(a, b, K.desc([5, 8], F)) == K.BAD_ARGUMENTS                    # N mismatch
+    assert validate(K.desc([5, 6], K.S32), b, c) == K.UNSUPPORTED                  # S32 source
+    assert validate(a, b, K.desc([5, 7], F, "AB", strides=[8, 1])) == K.UNSUPPORTED  # strided destination
+    assert validate(a, b, c, K.desc([2, 7], F)) == K.BAD_ARGUMENTS                 # bias rows neither 1 nor M
+    assert validate(a, b, c, K.desc([5, 1], F)) == K.SUCCESS
+    assert validate(a, b, c, K.desc([1, 1, 7], F)) == K.BAD_ARGUMENTS             # bias rank differs
+    assert validate(a, b, c, nt=-1) == K.BAD_ARGUMENTS
+    assert validate(a, b, c, nt=K.lib().kudnn_threading_get_max_num_threads() + 1) == K.BAD_ARGUMENTS
+    assert validate(K.desc([1, 6], F), K.desc([6, 7], F), K.desc([1, 7], F)) == K.SUCCESS
+    assert validate(K.desc([0, 6], F), b, K.desc([0, 7], F)) == K.UNSUPPORTED      # zero-size
+    # batch dims: equal or 1
+    a3, b3 = K.desc([4, 5, 6], F), K.desc([1, 6, 7], F)
+    assert validate(a3, b3, K.desc([4, 5, 7], F)) == K.SUCCESS
+    assert validate(a3, K.desc([3, 6, 7], F), K.desc([4, 5, 7], F)) == K.BAD_ARGUMENTS
+
+
+def test_linear_act_validation_and_kinds():
+    F = K.F32
+    a, b, c = K.desc([5, 6], F), K.desc([6, 7], F), K.desc([5, 7], F)
+    v = lambda kind, alpha=0.0, beta=0.0, cc=c: K.lib().kudnn_linear_act_validate(a, b, cc, None, alpha, beta, kind, 0)
+    assert v(K.ACT_RELU) == K.SUCCESS
+    assert v(K.ACT_TANH) == K.SUCCESS              # KuDNN's eltwise accepts it ...
+    with pytest.raises(K.KudnnError) as e:        # ... but it is not a fused epilogue here
+        K.LinearActivation(a, b, c, None, 0.0, 0.0, K.ACT_TANH)
+    assert e.value.status == K.UNSUPPORTED
+    assert v(K.ACT_UNIMPLEMENTED) == K.UNSUPPORTED
+    assert v(K.ACT_CLIP, 2.0, 1.0) == K.UNSUPPORTED  # alpha > beta
+    assert v(K.ACT_SRELU, 0.0) == K.UNSUPPORTED
+    assert v(K.ACT_SWISH, cc=K.desc([5, 7], K.S8)) == K.UNSUPPORTED
+
+
+def test_linear_res_validation():
+    F = K.F32
+    a, b, c = K.desc([5, 6], F), K.desc([6, 7], F), K.desc([5, 7], F)
+    v = lambda res, lr, kind: K.lib().kudnn_linear_res_validate(a, b, c, None, res, lr, kind, 0)
+    assert v(K.desc([5, 7], F), K.desc([5, 7], F), K.RES_IDENTIAL) == K.SUCCESS
+    assert v(K.desc([7, 3], F), K.desc([5, 3], F), K.RES_MUL) == K.SUCCESS
+    assert v(K.desc([7, 3], K.S32), K.desc([5, 3], F), K.RES_MUL) == K.UNSUPPORTED
+    assert v(K.desc([6, 7], F), K.desc([5, 7], F), K.RES_EXT) == K.BAD_ARGUMENTS
+    assert v(K.desc([5, 7], F), K.desc([5, 7], F), 7) == K.UNSUPPORTED
+
+
+def plan_of(M, Kd, N, dt=K.BF16, wl="BA", **kw):
+    return K.LinearPostOps(K.desc([M, Kd], dt), K.desc([Kd, N], dt, wl), K.desc([M, N], dt), **kw)
+
+
+def test_dispatcher_choices():
+    assert plan_of(4096, 4096, 11008).describe().startswith("mfma_bf16_256x256 M=4096 N=11008 K=4096")
+    for M in (1, 4, 16):
+        for N in (4096, 14336):
+            assert plan_of(M, 4096, N).describe().startswith("skinny_bf16")
+    assert plan_of(17, 4096, 4096).describe().startswith("mfma_bf16")
+    assert plan_of(2048, 4096, 4096, K.F32).describe().startswith("mfma_f32_128x128")
+    assert plan_of(128, 1024, 1024, K.F32).describe().startswith("mfma_f32_64x64")
+    # C5: 3-D input with a batch-broadcast K-major weight folds into one M=16384 GEMM
+    p = K.LinearActivation(K.desc([8, 2048, 5120], K.BF16, "ABC"), K.desc([1, 5120, 13824], K.BF16, "ABC"),
+                           K.desc([8, 2048, 13824], K.BF16, "ABC"), K.desc([1, 1, 13824], K.BF16, "ABC"), 1.0, 0.0,
+                           K.ACT_SWISH)
+    assert p.describe().startswith("mfma_bf16_256x256 M=16384 N=13824 K=5120 batches=1")
+    # a K not a multiple of the k-tile is packed (zero-padded)
+    assert "packA" in plan_of(300, 200, 260).describe()
+
+
+def test_run_rejects_null_pointers_without_gpu():
+    p = plan_of(64, 64, 64)
+    with pytest.raises(K.KudnnError) as e:
+        p.run(None, None, None)
+    assert e.value.status == K.NULL_POINTER
+
+
+def test_threading_api_contract():
+    lib = K.lib()
+    mx = lib.kudnn_threading_get_max_num_threads()
+    assert mx >= 1
+    assert lib.kudnn_threading_set_max_num_threads(0) == mx          # ignored, old value returned
+    assert lib.kudnn_threading_get_max_num_threads() == mx
