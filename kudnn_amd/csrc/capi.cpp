@@ -488,7 +488,7 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
             core.engine = ENGINE_MFMA_BF16;
             auto tiles = [&](int64_t bm, int64_t bn) { return (core.M + bm - 1) / bm * ((core.N + bn - 1) / bn) * batches; };
             if (tiles(256, 256) >= 256) {
-                core.cfg = KUDNN_CFG_BF16_256x256;
+                core.cfg = KUDNN_CFG_BF16_PINGPONG_256x256;
             } else if (tiles(256, 128) >= 256) {
                 core.cfg = KUDNN_CFG_BF16_256x128;
             } else {
@@ -504,6 +504,7 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
         int f = std::atoi(force);
         bool okBf16 = core.computeDt == KUDNN_DT_BF16 &&
                       (f == KUDNN_CFG_BF16_256x256 || f == KUDNN_CFG_BF16_256x128 || f == KUDNN_CFG_BF16_128x128 ||
+                       (f == KUDNN_CFG_BF16_PINGPONG_256x256 && core.M > 16) ||
                        (f == KUDNN_CFG_SKINNY_BF16 && core.M <= 16));
         bool okF32 = core.computeDt == KUDNN_DT_F32 && (f == KUDNN_CFG_F32_128x128 || f == KUDNN_CFG_F32_64x64);
         if (okBf16 || okF32) {
@@ -521,6 +522,7 @@ const char *CfgName(int cfg)
         case KUDNN_CFG_BF16_256x256: return "mfma_bf16_256x256";
         case KUDNN_CFG_BF16_256x128: return "mfma_bf16_256x128";
         case KUDNN_CFG_BF16_128x128: return "mfma_bf16_128x128";
+        case KUDNN_CFG_BF16_PINGPONG_256x256: return "mfma_bf16_pingpong_256x256";
         case KUDNN_CFG_F32_128x128: return "mfma_f32_128x128";
         case KUDNN_CFG_F32_64x64: return "mfma_f32_64x64";
         case KUDNN_CFG_SKINNY_BF16: return "skinny_bf16_16xK";
@@ -716,7 +718,13 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
     if (core.engine == ENGINE_SKINNY_BF16) {
         lrc = kudnn_launch_skinny_bf16(op, ep, batches, stream);
     } else if (core.engine == ENGINE_MFMA_BF16) {
-        lrc = kudnn_launch_gemm_bf16(op, ep, batches, core.cfg, stream);
+        if (core.cfg == KUDNN_CFG_BF16_PINGPONG_256x256 && kudnn_pingpong_eligible(op)) {
+            lrc = kudnn_launch_gemm_bf16_pingpong(op, ep, batches, stream);
+        } else {
+            // operands the ping-pong kernel cannot address (e.g. offsets beyond 2 GiB) use the 4-wave kernel
+            const int cfg = core.cfg == KUDNN_CFG_BF16_PINGPONG_256x256 ? KUDNN_CFG_BF16_256x256 : core.cfg;
+            lrc = kudnn_launch_gemm_bf16(op, ep, batches, cfg, stream);
+        }
     } else {
         lrc = kudnn_launch_gemm_f32(op, ep, batches, core.cfg, stream);
     }

@@ -103,7 +103,7 @@ __device__ __forceinline__ float tanh_f32(float y)
         t = a;  // tanh(a) = a - a^3/3 + ..., the cubic term is below f32 resolution here
     } else {
         float e = fast_exp(2.0f * fminf(a, 20.0f));
-        t = 1.0f - 2.0f / (e + 1.0f);
+        t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
     }
     return copysignf(t, y);
 }
@@ -122,7 +122,7 @@ __device__ __forceinline__ float act_swish(float x, float alpha)
     } else if (t < -87.0f) {
         s = 1.0f;
     } else {
-        s = 1.0f / (1.0f + fast_exp(t));
+        s = __builtin_amdgcn_rcpf(1.0f + fast_exp(t));
     }
     return x * s;
 }
@@ -299,8 +299,46 @@ __device__ __forceinline__ void epi_apply4(const EpiParams &e, const EpiBatch &o
 
 // Epilogue for eight consecutive columns n..n+7 of row m (n a multiple of 8): one 16-byte bf16 (or two
 // 16-byte f32) store per call when the output rows are contiguous and 8-element aligned (fast8).
+// Binary operand of epi_apply8's fast path (8 consecutive columns of one row), loaded ahead of use: one 16-byte
+// load for bf16, two for f32; zero when the fast path does not apply (the epilogue then loads the operand itself).
+struct Src8 {
+    uint4 lo, hi;
+};
+
+__device__ __forceinline__ Src8 epi_load_src8(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, int64_t M,
+                                              int64_t N)
+{
+    Src8 r{make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
+    if (e.bin != KUDNN_BINARY_NONE && e.fast8 && m < M && n + 7 < N) {
+        const int64_t si = ob.src + m * e.src_sm + n;
+        if (e.src_dt == KUDNN_DT_BF16) {
+            r.lo = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(e.src) + si);
+        } else if (e.src_dt == KUDNN_DT_F32) {
+            r.lo = *reinterpret_cast<const uint4 *>(static_cast<const float *>(e.src) + si);
+            r.hi = *reinterpret_cast<const uint4 *>(static_cast<const float *>(e.src) + si + 4);
+        }
+    }
+    return r;
+}
+
+__device__ __forceinline__ void epi_apply8_core(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, int64_t N,
+                                                const float acc[8], const Src8 *pre);
+
 __device__ __forceinline__ void epi_apply8(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, int64_t N,
                                            const float acc[8])
+{
+    epi_apply8_core(e, ob, m, n, N, acc, nullptr);
+}
+
+// epi_apply8 with the binary operand already loaded by epi_load_src8 (bf16 and f32 operands).
+__device__ __forceinline__ void epi_apply8_pre(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, int64_t N,
+                                               const float acc[8], const Src8 &pre)
+{
+    epi_apply8_core(e, ob, m, n, N, acc, &pre);
+}
+
+__device__ __forceinline__ void epi_apply8_core(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, int64_t N,
+                                                const float acc[8], const Src8 *pre)
 {
     if (n + 7 < N && e.fast8) {
         float v[8];
@@ -344,7 +382,7 @@ __device__ __forceinline__ void epi_apply8(const EpiParams &e, const EpiBatch &o
             const int64_t si = ob.src + m * e.src_sm + n;
             float sv[8];
             if (e.src_dt == KUDNN_DT_BF16) {
-                const uint4 raw = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(e.src) + si);
+                const uint4 raw = pre ? pre->lo : *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(e.src) + si);
                 const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -352,8 +390,10 @@ __device__ __forceinline__ void epi_apply8(const EpiParams &e, const EpiBatch &o
                     sv[2 * q + 1] = u2f(w[q] & 0xffff0000u);
                 }
             } else if (e.src_dt == KUDNN_DT_F32) {
-                const float4 t0 = *reinterpret_cast<const float4 *>(static_cast<const float *>(e.src) + si);
-                const float4 t1 = *reinterpret_cast<const float4 *>(static_cast<const float *>(e.src) + si + 4);
+                const float4 t0 = pre ? __builtin_bit_cast(float4, pre->lo)
+                                      : *reinterpret_cast<const float4 *>(static_cast<const float *>(e.src) + si);
+                const float4 t1 = pre ? __builtin_bit_cast(float4, pre->hi)
+                                      : *reinterpret_cast<const float4 *>(static_cast<const float *>(e.src) + si + 4);
                 sv[0] = t0.x; sv[1] = t0.y; sv[2] = t0.z; sv[3] = t0.w;
                 sv[4] = t1.x; sv[5] = t1.y; sv[6] = t1.z; sv[7] = t1.w;
             } else {

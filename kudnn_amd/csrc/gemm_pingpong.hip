@@ -1,0 +1,306 @@
+// bf16 GEMM on gfx950 MFMA, 8-wave ping-pong schedule, 256 x 256 output tile, k-tile 64, fused epilogue.
+//
+// This is the kernel behind cblas_sbgemm / cblas_bgemm in the reference (src/dnn/src/kudnn_gemm.cpp:208-241)
+// for large M: Y = epilogue(A[M][K] x B[N][K]^T), both operands contiguous along K.
+//
+// Why this schedule. On gfx950 a wave that issues a global->LDS copy (buffer_load ... lds) stalls until the
+// texture-address unit accepts it, about 22 cycles per 1 KB instruction per CU (measured; the cost is per 128-byte
+// cache line, so k-tiles of 64 bf16 = full lines are used). A 256x256x64 tile needs 64 such instructions
+// (~1400 cycles) against 2048 cycles of MFMA per SIMD, so the copies must never sit in front of the MFMAs.
+// Eight waves run as two groups on the four SIMDs (wave w: group g = w/4, SIMD p = w%4) and alternate phases
+// separated by s_barrier, group 1 one phase behind group 0:
+//   memory phase M(t): read this wave's A fragments of k-tile t from LDS, issue its share of the next copies
+//                      (group 0: A(t+1), group 1: B(t+2)), read the B fragments of the first k16 step;
+//   compute phase C(t): 32 v_mfma_f32_32x32x16_bf16, B fragments of step s+1 read while step s issues.
+// While one wave of a SIMD is in its memory phase the other issues MFMAs.
+//
+// LDS (160 KB): A tiles double-buffered, B tiles triple-buffered (5 x 32 KB). A(t) is read in phases 2t, 2t+1 and
+// rewritten by A(t+2) from phase 2t+2; B(t) is read in phases 2t .. 2t+2 and rewritten by B(t+3) at phase 2t+3.
+// Each buffer is its own __shared__ array and the loop is unrolled by 6 so every access names its buffer at compile
+// time; the compiler can then tell that the copies and the fragment reads never alias and does not insert a full
+// vmcnt(0) wait in front of every LDS read.
+//
+// Rows are 128 bytes per k-tile with a XOR swizzle (chunk ^ ((row >> 1) & 7)) so the 16 lanes of a ds_read_b128
+// quarter-wave hit 16 distinct 16-byte slots of the 64 LDS banks. Copies use raw buffer resources: the per-lane part
+// of the source offset (row within an 8-row block, chunk) is one VGPR and the resource itself starts at the block, so
+// rows past the end of the operand fall outside the resource's range and read as zero. Wave-uniform values are made
+// explicit with readfirstlane.
+//
+// Epilogue: the accumulators pass through LDS one 32-column strip at a time and are read back row-major, 8
+// consecutive columns per lane, so bias / activation / residual run on 8 values and the result is one 16-byte store;
+// the binary operand of strip j+1 is loaded while strip j is processed.
+#include <utility>
+
+#include "device_common.h"
+#include "kernels.h"
+
+using namespace kudnn_dev;
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kBM = 256, kBN = 256, kKC = 8, kBK = 64;
+constexpr int kTile = 256 * kKC;        // uint4 per A or B tile buffer (32 KB)
+constexpr int kPitch = 36;              // epilogue staging pitch in floats (32 columns + 4)
+
+template <int... I, typename F>
+__device__ __forceinline__ void sfor_impl(std::integer_sequence<int, I...>, F &&f)
+{
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void sfor(F &&f)
+{
+    sfor_impl(std::make_integer_sequence<int, N>{}, f);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    // s_waitcnt: vmcnt[3:0] bits 3:0, vmcnt[5:4] bits 15:14; expcnt (7) and lgkmcnt (15) left unconstrained
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// One 1 KB copy global -> LDS of an 8-row block through a raw buffer resource. The resource starts at the block's
+// first element (wave-uniform `elemOff` from `base`) and covers the bytes of the operand that remain after it, so the
+// hardware range check, which applies to the per-lane offset `voff` only, turns rows past the end of the operand
+// into zeros instead of reads outside the allocation.
+__device__ __forceinline__ void copy_block(const uint16_t *base, uint32_t totalBytes, uint32_t elemOff, uint32_t voff, uint4 *dst)
+{
+    const uint32_t off = elemOff * 2u;
+    const uint32_t remain = off < totalBytes ? totalBytes - off : 0u;
+    __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)(base + elemOff), (short)0, (int)remain, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)dst, 16, voff, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(512, 1) void gemm_bf16_pingpong_kernel(GemmOperands op, EpiParams ep, int tilesM,
+                                                                     int tilesN, int group)
+{
+    __shared__ uint4 a0[kTile], a1[kTile], b0[kTile], b1[kTile], b2[kTile];
+    auto abuf = [&](auto ic) __attribute__((always_inline)) -> uint4 * {
+        if constexpr (decltype(ic)::value % 2 == 0) return a0; else return a1;
+    };
+    auto bbuf = [&](auto ic) __attribute__((always_inline)) -> uint4 * {
+        constexpr int I = decltype(ic)::value % 3;
+        if constexpr (I == 0) return b0; else if constexpr (I == 1) return b1; else return b2;
+    };
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = wave >> 2, p = wave & 3;
+    int tm, tn;
+    grouped_tile(xcd_remap(blockIdx.x, gridDim.x), tilesM, tilesN, group, tm, tn);
+    const int m0 = tm * kBM, n0 = tn * kBN;
+    const int M = static_cast<int>(op.M), N = static_cast<int>(op.N), K = static_cast<int>(op.K);
+
+    const int64_t batch = blockIdx.y;
+    const int64_t i2 = batch % ep.bdim[2];
+    const int64_t i1 = (batch / ep.bdim[2]) % ep.bdim[1];
+    const int64_t i0 = batch / (ep.bdim[2] * ep.bdim[1]);
+    const uint16_t *A = static_cast<const uint16_t *>(op.a) + i0 * op.a_bs[0] + i1 * op.a_bs[1] + i2 * op.a_bs[2];
+    const uint16_t *B = static_cast<const uint16_t *>(op.b) + i0 * op.b_bs[0] + i1 * op.b_bs[1] + i2 * op.b_bs[2];
+    const uint32_t lda = static_cast<uint32_t>(op.lda), ldb = static_cast<uint32_t>(op.ldb);
+    const uint32_t bytesA = static_cast<uint32_t>(op.M) * lda * 2u, bytesB = static_cast<uint32_t>(op.N) * ldb * 2u;
+
+    // copy addressing: a 1 KB copy covers an 8-row block q (rows 8q .. 8q+7 of the tile); lane -> row lr, LDS slot ls,
+    // source chunk ls ^ ((row >> 1) & 7) = ls ^ (4 * (q & 1) + (lr >> 1))
+    const int lr = lane >> 3, ls = lane & 7;
+    const uint32_t loA0 = lr * lda * 2u + static_cast<uint32_t>((ls ^ (lr >> 1)) * 16);
+    const uint32_t loA1 = lr * lda * 2u + static_cast<uint32_t>((ls ^ (4 + (lr >> 1))) * 16);
+    const uint32_t loB0 = lr * ldb * 2u + static_cast<uint32_t>((ls ^ (lr >> 1)) * 16);
+    const uint32_t loB1 = lr * ldb * 2u + static_cast<uint32_t>((ls ^ (4 + (lr >> 1))) * 16);
+    auto copyA = [&](int q, int t, uint4 *dst) __attribute__((always_inline)) {
+        copy_block(A, bytesA, static_cast<uint32_t>(m0 + q * 8) * lda + static_cast<uint32_t>(t * kBK), (q & 1) ? loA1 : loA0,
+                   dst + q * 8 * kKC);
+    };
+    auto copyB = [&](int q, int t, uint4 *dst) __attribute__((always_inline)) {
+        copy_block(B, bytesB, static_cast<uint32_t>(n0 + q * 8) * ldb + static_cast<uint32_t>(t * kBK), (q & 1) ? loB1 : loB0,
+                   dst + q * 8 * kKC);
+    };
+    // the operand this wave streams inside the loop, selected once by value (group 0: A, group 1: B)
+    const uint16_t *sX = g == 0 ? A : B;
+    const uint32_t sBytes = g == 0 ? bytesA : bytesB;
+    const uint32_t sLd = g == 0 ? lda : ldb;
+    const uint32_t sLo0 = g == 0 ? loA0 : loB0, sLo1 = g == 0 ? loA1 : loB1;
+    const int sR0 = g == 0 ? m0 : n0;
+
+    // fragment addressing: rows of a 32-row block start at multiples of 32, so the swizzle term depends on lrow only
+    const int lrow = lane & 31, lh = lane >> 5;
+    const int fsw = (lrow >> 1) & 7;
+    const int offA = (p * 64 + lrow) * kKC, offB = (g * 128 + lrow) * kKC;
+
+    f32x16_t acc[4][2];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.0f;
+        }
+    }
+    uint4 fa[4][2], fb[2][4];
+    const int KT = K / kBK;
+
+    // prologue: A(0), B(0), B(1); wave w copies 8-row blocks 4w .. 4w+3 of each
+#pragma unroll
+    for (int j = 0; j < 4; ++j) copyA(wave * 4 + j, 0, a0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) copyB(wave * 4 + j, 0, b0);
+    if (KT > 1) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) copyB(wave * 4 + j, 1, b1);
+        wait_vmcnt<4>();
+    } else {
+        wait_vmcnt<0>();
+    }
+    __builtin_amdgcn_s_barrier();
+    if (g == 1) {
+        __builtin_amdgcn_s_barrier();  // group 1 runs one phase behind
+    }
+
+    auto readB = [&](const uint4 *bt, auto slotc, auto stepc) __attribute__((always_inline)) {
+        constexpr int slot = decltype(slotc)::value, s = decltype(stepc)::value;
+        const int sl = (2 * s + lh) ^ fsw;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) fb[slot][j] = bt[offB + j * 32 * kKC + sl];
+    };
+    auto step = [&](auto ic, int t) __attribute__((always_inline)) {
+        constexpr int I = decltype(ic)::value;
+        const uint4 *at = abuf(ic);
+        const uint4 *bt = bbuf(ic);
+        // ---- memory phase
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int sl = (2 * s + lh) ^ fsw;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) fa[s][i] = at[offA + i * 32 * kKC + sl];
+        }
+        {
+            const int tt = t + 1 + g;  // group 0 copies A(t+1), group 1 copies B(t+2)
+            uint4 *dst = g == 0 ? abuf(std::integral_constant<int, I + 1>{}) : bbuf(std::integral_constant<int, I + 2>{});
+            if (tt < KT) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int q = p * 8 + j;
+                    copy_block(sX, sBytes, static_cast<uint32_t>(sR0 + q * 8) * sLd + static_cast<uint32_t>(tt * kBK),
+                               (q & 1) ? sLo1 : sLo0, dst + q * 8 * kKC);
+                }
+            }
+        }
+        readB(bt, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+        wait_lgkmcnt0();
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        // ---- compute phase
+        sfor<4>([&](auto sc) __attribute__((always_inline)) {
+            constexpr int s = decltype(sc)::value;
+            if constexpr (s + 1 < 4) {
+                readB(bt, std::integral_constant<int, (s + 1) & 1>{}, std::integral_constant<int, s + 1>{});
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fb[s & 1][j]),
+                                                                        __builtin_bit_cast(bf16x8_t, fa[s][i]), acc[j][i], 0, 0, 0);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        // copies that the next phase boundary needs: group 0's A(t+1) (its only copies in flight);
+        // group 1's B(t+1) (B(t+2) may stay in flight)
+        if (g == 0) {
+            wait_vmcnt<0>();
+        } else if (t + 2 < KT) {
+            wait_vmcnt<8>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int t = 0; t < KT; t += 6) {
+        sfor<6>([&](auto ic) __attribute__((always_inline)) {
+            if (t + decltype(ic)::value < KT) step(ic, t + decltype(ic)::value);
+        });
+    }
+    if (g == 0) {
+        __builtin_amdgcn_s_barrier();  // matches group 1's extra barrier at the start
+    }
+
+    // ---- epilogue: wave (p, g) owns rows p*64 .. +64, columns g*128 .. +128; 4 strips of 32 columns
+    wait_vmcnt<0>();
+    __syncthreads();  // every wave is done with the tile buffers that the staging area reuses
+    // 64 x 36 floats (9 KB) per wave: waves 0-2 stage in a0, 3-5 in a1, 6-7 in b0
+    float *stage = reinterpret_cast<float *>(wave < 3 ? a0 : (wave < 6 ? a1 : b0)) + (wave % 3) * (64 * kPitch);
+    const EpiBatch ob = epi_batch_offsets(ep, batch);
+    const int col8 = (lane & 3) * 8;
+    const int rlane = lane >> 2;
+    const int64_t nBase = n0 + g * 128 + col8;
+    const int64_t mBase = m0 + p * 64 + rlane;
+    sfor<4>([&](auto jc) __attribute__((always_inline)) {
+        constexpr int j = decltype(jc)::value;
+        // binary operand of this strip, loaded before the staging round trip so its latency overlaps it
+        Src8 pre[4];
+        sfor<4>([&](auto pc) __attribute__((always_inline)) {
+            constexpr int ps = decltype(pc)::value;
+            pre[ps] = epi_load_src8(ep, ob, mBase + ps * 16, nBase + j * 32, M, N);
+        });
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                float *dst = stage + (i * 32 + lrow) * kPitch + q4 * 8 + lh * 4;
+                *reinterpret_cast<float4 *>(dst) =
+                    make_float4(acc[j][i][4 * q4 + 0], acc[j][i][4 * q4 + 1], acc[j][i][4 * q4 + 2], acc[j][i][4 * q4 + 3]);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        sfor<4>([&](auto pc) __attribute__((always_inline)) {
+            constexpr int ps = decltype(pc)::value;
+            const int r = rlane + ps * 16;
+            const int64_t m = m0 + p * 64 + r;
+            const int64_t n = nBase + j * 32;
+            if (m < M && n < N) {
+                const float *src = stage + r * kPitch + col8;
+                const float4 lo = *reinterpret_cast<const float4 *>(src);
+                const float4 hi = *reinterpret_cast<const float4 *>(src + 4);
+                const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                epi_apply8_pre(ep, ob, m, n, N, v, pre[ps]);
+            }
+        });
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    });
+}
+
+}  // namespace
+
+bool kudnn_pingpong_eligible(const GemmOperands &op)
+{
+    // whole k-tiles, 16-byte aligned rows, 32-bit buffer offsets
+    return op.K % kBK == 0 && op.lda % 8 == 0 && op.ldb % 8 == 0 && op.M * op.lda * 2 < (int64_t(1) << 31) &&
+           op.N * op.ldb * 2 < (int64_t(1) << 31) && op.K > 0;
+}
+
+int kudnn_launch_gemm_bf16_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream)
+{
+    if (!kudnn_pingpong_eligible(op)) {
+        return -1;
+    }
+    const int tilesM = static_cast<int>((op.M + kBM - 1) / kBM);
+    const int tilesN = static_cast<int>((op.N + kBN - 1) / kBN);
+    dim3 grid(static_cast<unsigned>(tilesM * tilesN), static_cast<unsigned>(batches));
+    hipLaunchKernelGGL(gemm_bf16_pingpong_kernel, grid, dim3(512), 0, stream, op, ep, tilesM, tilesN, 8);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}

@@ -11,6 +11,7 @@ enum {
     KUDNN_CFG_BF16_256x256 = 1,
     KUDNN_CFG_BF16_256x128 = 2,
     KUDNN_CFG_BF16_128x128 = 3,
+    KUDNN_CFG_BF16_PINGPONG_256x256 = 4,
     KUDNN_CFG_F32_128x128 = 10,
     KUDNN_CFG_F32_64x64 = 11,
     KUDNN_CFG_SKINNY_BF16 = 20,
@@ -18,6 +19,10 @@ enum {
 
 // Returns 0 on success, -1 if the launch failed or cfg is unknown.
 int kudnn_launch_gemm_bf16(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, hipStream_t stream);
+// 8-wave ping-pong schedule, 256x256 tile (gemm_pingpong.hip). Needs K a multiple of 64, 16-byte aligned rows and
+// 32-bit operand offsets; kudnn_pingpong_eligible says whether `op` qualifies.
+bool kudnn_pingpong_eligible(const GemmOperands &op);
+int kudnn_launch_gemm_bf16_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream);
 int kudnn_launch_gemm_f32(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, hipStream_t stream);
 // M <= 16, bf16 operands, B contiguous along K.
 int kudnn_launch_skinny_bf16(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream);

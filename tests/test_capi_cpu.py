@@ -126,7 +126,7 @@ def plan_of(M, Kd, N, dt=K.BF16, wl="BA", **kw):
 
 
 def test_dispatcher_choices():
-    assert plan_of(4096, 4096, 11008).describe().startswith("mfma_bf16_256x256 M=4096 N=11008 K=4096")
+    assert plan_of(4096, 4096, 11008).describe().startswith("mfma_bf16_pingpong_256x256 M=4096 N=11008 K=4096")
     for M in (1, 4, 16):
         for N in (4096, 14336):
             assert plan_of(M, 4096, N).describe().startswith("skinny_bf16")
@@ -137,7 +137,7 @@ def test_dispatcher_choices():
     p = K.LinearActivation(K.desc([8, 2048, 5120], K.BF16, "ABC"), K.desc([1, 5120, 13824], K.BF16, "ABC"),
                            K.desc([8, 2048, 13824], K.BF16, "ABC"), K.desc([1, 1, 13824], K.BF16, "ABC"), 1.0, 0.0,
                            K.ACT_SWISH)
-    assert p.describe().startswith("mfma_bf16_256x256 M=16384 N=13824 K=5120 batches=1")
+    assert p.describe().startswith("mfma_bf16_pingpong_256x256 M=16384 N=13824 K=5120 batches=1")
     # a K not a multiple of the k-tile is packed (zero-padded)
     assert "packA" in plan_of(300, 200, 260).describe()
 

@@ -237,3 +237,61 @@ def test_c5_bf16_3d_silu_kmajor_rows():
     ref = O.empty((len(rows), N), (N, 1), O.BF16)
     O.linear_act(dense_rows(x.t, rows), as2d(w.t), ref, as2d(b.t), O.ACT_SWISH, 1.0)
     compare(got[rows].reshape(-1), ref.buf, O.BF16, "C5 " + plan.describe())
+
+
+# ---------------------------------------------------------------------------------------------------
+# the 8-wave ping-pong kernel (chosen for large bf16 problems) on shapes that exercise its edges:
+# partial 256-row / 256-column tiles (rows past the end read as zero), a single k-tile, many k-tiles,
+# batches, and every epilogue kind
+
+
+@pytest.fixture
+def force_pingpong(monkeypatch):
+    monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "4")
+
+
+@pytest.mark.parametrize("mnk", [(256, 256, 64), (300, 520, 192), (257, 255, 64), (512, 768, 1024), (40, 600, 128)])
+@pytest.mark.parametrize("post", ["none", "bias_gelu_add", "swish", "mul", "relu_ext"])
+def test_pingpong_shapes_and_epilogues(force_pingpong, mnk, post):
+    M, N, Kd = mnk
+    dt = O.BF16
+    x = Case([M, Kd], dt, seed=70, dist="normal", lo=0.0, hi=1.0)
+    w = Case([Kd, N], dt, "BA", seed=71, dist="normal", lo=0.0, hi=0.05)
+    y = Case([M, N], dt, zero=True)
+    b = Case([1, N], dt, seed=72, lo=-0.1, hi=0.1) if post in ("bias_gelu_add", "relu_ext") else None
+    s = Case([M, N], dt, seed=73, lo=0.5, hi=1.5) if post in ("bias_gelu_add", "mul", "relu_ext") else None
+    act, aa, binary = {"none": (O.ACT_NONE, 0.0, O.BIN_NONE), "bias_gelu_add": (O.ACT_GELU_TANH, 0.0, O.BIN_ADD),
+                       "swish": (O.ACT_SWISH, 1.0, O.BIN_NONE), "mul": (O.ACT_NONE, 0.0, O.BIN_MUL),
+                       "relu_ext": (O.ACT_RELU, 0.0, O.BIN_EXT)}[post]
+    plan = K.LinearPostOps(x.desc, w.desc, y.desc, b.desc if b else None, act=act, act_alpha=aa, binary=binary,
+                           src=s.desc if s else None)
+    assert "pingpong" in plan.describe()
+    dy = zeros_device(y)
+    plan.run(x.device(), w.device(), dy, b.device() if b else None, s.device() if s else None, gamma=0.75)
+    torch.cuda.synchronize()
+    ref = y.clone_empty()
+    O.linear_postops(x.t, w.t, ref, b.t if b else None, act, aa, binary, s.t if s else None, 0.75)
+    compare(from_device(dy, dt), ref.buf, dt, f"{plan.describe()} {post}")
+
+
+def test_pingpong_batched_and_strided_weight(force_pingpong):
+    # 3 batches, K-major weight (packed to [N][K] by the pack kernel), bias per batch row
+    dt = O.BF16
+    x = Case([3, 300, 128], dt, "ABC", seed=80, dist="normal", lo=0.0, hi=1.0)
+    w = Case([3, 128, 280], dt, "ABC", seed=81, dist="normal", lo=0.0, hi=0.05)
+    b = Case([3, 1, 280], dt, "ABC", seed=82, lo=-0.1, hi=0.1)
+    c = Case([3, 300, 280], dt, "ABC", zero=True)
+    plan = K.LinearActivation(x.desc, w.desc, c.desc, b.desc, 1.0, 0.0, K.ACT_SWISH)
+    assert "pingpong" in plan.describe()
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc, b.device())
+    torch.cuda.synchronize()
+    ref = c.clone_empty()
+    O.linear_act(x.t, w.t, ref, b.t, O.ACT_SWISH, 1.0)
+    compare(from_device(dc, dt), ref.buf, dt, plan.describe())
+
+
+def test_c3_plan_uses_pingpong():
+    dx, dw, dy = K.desc([4096, 4096], K.BF16), K.desc([4096, 11008], K.BF16, "BA"), K.desc([4096, 11008], K.BF16)
+    plan = K.LinearPostOps(dx, dw, dy, K.desc([1, 11008], K.BF16), act=K.ACT_GELU_TANH, binary=K.BIN_ADD, src=dy)
+    assert plan.describe().startswith("mfma_bf16_pingpong_256x256")
