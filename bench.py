@@ -9,7 +9,15 @@ Also reported (not `value`): the decode-shaped skinny Linear at M=1, K=4096, N i
 cannot serve the weight stream, and the CPU baseline (the reference tests' portable naive loop, timed
 on a bounded row sample of the same workload on this host's cores).
 
-Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10]
+Before the W counted warmup steps, the step is also run untimed for --prewarm-ms of wall time (default 300 ms):
+the GPU raises its clocks over the first ~100 ms of sustained load, and a timed region that starts on a cold GPU
+reports the ramp rather than the kernel (a 25 ms region read 475 us per step cold against 412 us warm).
+
+For profiling, --only c3 runs just the C3 step (JSON line without decode or CPU baseline), and --only copy runs an
+elementwise copy-like kernel (y = -x, 512 MiB bf16 in, 512 MiB out) whose known traffic calibrates the
+FETCH_SIZE / WRITE_SIZE counters against which the C3 kernel's HBM traffic is read.
+
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--prewarm-ms 300] [--only c3|copy]
 """
 from __future__ import annotations
 
@@ -33,13 +41,20 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--prewarm-ms", type=float, default=300.0, help="untimed run time before warmup (clock ramp)")
+    p.add_argument("--only", choices=["c3", "copy"], default=None, help="profiling modes (see module docstring)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU-baseline sample time")
     return p.parse_args()
 
 
-def time_launches(fn, steps, warmup, torch, stream):
+def time_launches(fn, steps, warmup, torch, stream, prewarm_ms=0.0):
+    t_end = time.perf_counter() + prewarm_ms * 1e-3
+    while time.perf_counter() < t_end:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -76,7 +91,7 @@ def bench_c3(args, torch, K):
     def step(i=0):
         plan.run(x, w, y, bias, r, stream=stream)
 
-    ms_kernel, ms_wall = time_launches(step, args.steps, args.warmup, torch, stream)
+    ms_kernel, ms_wall = time_launches(step, args.steps, args.warmup, torch, stream, args.prewarm_ms)
     flops = 2.0 * M * N * Kd
     alg_bytes = 2 * (M * Kd + N * Kd + N + M * N + M * N)
     tflops = flops / (ms_kernel * 1e-3) / 1e12
@@ -109,7 +124,7 @@ def bench_decode(args, torch, K, N):
         plan.run(x, ws[i % copies], y, None, m2, stream=stream)
 
     steps = max(args.steps, 4 * copies)
-    ms, ms_wall = time_launches(step, steps, max(args.warmup, copies), torch, stream)
+    ms, ms_wall = time_launches(step, steps, max(args.warmup, copies), torch, stream, args.prewarm_ms)
     alg_bytes = 2 * (N * Kd + M * Kd + 2 * M * N)
     gbs = alg_bytes / (ms * 1e-3) / 1e9
     return {"N": N, "M": M, "K": Kd, "plan": plan.describe(), "us": ms * 1e3, "us_wall": ms_wall * 1e3,
@@ -163,9 +178,20 @@ def main():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
 
+    if args.only == "copy":
+        n = 256 << 20  # bf16 elements: 512 MiB read + 512 MiB written per launch
+        x = torch.ones(n, device="cuda", dtype=torch.bfloat16)
+        y = torch.empty_like(x)
+        stream = torch.cuda.current_stream()
+        ms, _ = time_launches(lambda i=0: torch.neg(x, out=y), args.steps, args.warmup, torch, stream, 0.0)
+        print(json.dumps({"kernel": "copy-like elementwise (torch.neg, bf16)", "bytes_read": 2 * n,
+                          "bytes_written": 2 * n, "ms": round(ms, 4), "GB/s": round(4 * n / (ms * 1e-3) / 1e9, 1)}))
+        return
+
     c3 = bench_c3(args, torch, K)
-    decode = [] if args.no_decode else [bench_decode(args, torch, K, n) for n in (4096, 14336)]
-    cpu = None if args.no_cpu_baseline else cpu_baseline(args, np)
+    only = args.only == "c3"
+    decode = [] if (args.no_decode or only) else [bench_decode(args, torch, K, n) for n in (4096, 14336)]
+    cpu = None if (args.no_cpu_baseline or only) else cpu_baseline(args, np)
 
     traffic = None
     tf = ROOT / "profiles" / "traffic_c3.json"
@@ -182,6 +208,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "prewarm_ms": args.prewarm_ms,
         "ms_per_step": round(c3["ms_wall"], 4),
         "higher_is_better": True,
         "scaling": "weak",

@@ -27,15 +27,14 @@ __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return u2f(static_cast<uint32_t>(h) << 16); }
 
-// Round-to-nearest-even f32 -> bf16 (NaN kept quiet).
+// Round-to-nearest-even f32 -> bf16 (NaN kept quiet). Both results are computed and one is selected, so the
+// conversion is straight-line code.
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f)
 {
-    uint32_t u = f2u(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) {
-        return static_cast<uint16_t>((u >> 16) | 0x0040u);
-    }
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return static_cast<uint16_t>(u >> 16);
+    const uint32_t u = f2u(f);
+    const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    const uint32_t quiet = (u >> 16) | 0x0040u;
+    return static_cast<uint16_t>((u & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
 }
 
 // Truncating f32 -> bf16 (keep the top 16 bits).
@@ -44,12 +43,10 @@ __device__ __forceinline__ uint16_t f32_to_bf16_trunc(float f) { return static_c
 // RELU's bf16 store: finite values at or above the largest bf16 (0x7f7f8000) become +-Inf, then truncate.
 __device__ __forceinline__ uint16_t f32_to_bf16_trunc_inf(float f)
 {
-    uint32_t u = f2u(f);
-    uint32_t a = u & 0x7fffffffu;
-    if (a >= 0x7f7f8000u && a < 0x7f800000u) {
-        u = (u & 0x80000000u) | 0x7f800000u;
-    }
-    return static_cast<uint16_t>(u >> 16);
+    const uint32_t u = f2u(f);
+    const uint32_t a = u & 0x7fffffffu;
+    const uint32_t inf = (u & 0x80000000u) | 0x7f800000u;
+    return static_cast<uint16_t>(((a >= 0x7f7f8000u && a < 0x7f800000u) ? inf : u) >> 16);
 }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
@@ -299,46 +296,8 @@ __device__ __forceinline__ void epi_apply4(const EpiParams &e, const EpiBatch &o
 
 // Epilogue for eight consecutive columns n..n+7 of row m (n a multiple of 8): one 16-byte bf16 (or two
 // 16-byte f32) store per call when the output rows are contiguous and 8-element aligned (fast8).
-// Binary operand of epi_apply8's fast path (8 consecutive columns of one row), loaded ahead of use: one 16-byte
-// load for bf16, two for f32; zero when the fast path does not apply (the epilogue then loads the operand itself).
-struct Src8 {
-    uint4 lo, hi;
-};
-
-__device__ __forceinline__ Src8 epi_load_src8(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, int64_t M,
-                                              int64_t N)
-{
-    Src8 r{make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
-    if (e.bin != KUDNN_BINARY_NONE && e.fast8 && m < M && n + 7 < N) {
-        const int64_t si = ob.src + m * e.src_sm + n;
-        if (e.src_dt == KUDNN_DT_BF16) {
-            r.lo = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(e.src) + si);
-        } else if (e.src_dt == KUDNN_DT_F32) {
-            r.lo = *reinterpret_cast<const uint4 *>(static_cast<const float *>(e.src) + si);
-            r.hi = *reinterpret_cast<const uint4 *>(static_cast<const float *>(e.src) + si + 4);
-        }
-    }
-    return r;
-}
-
-__device__ __forceinline__ void epi_apply8_core(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, int64_t N,
-                                                const float acc[8], const Src8 *pre);
-
 __device__ __forceinline__ void epi_apply8(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, int64_t N,
                                            const float acc[8])
-{
-    epi_apply8_core(e, ob, m, n, N, acc, nullptr);
-}
-
-// epi_apply8 with the binary operand already loaded by epi_load_src8 (bf16 and f32 operands).
-__device__ __forceinline__ void epi_apply8_pre(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, int64_t N,
-                                               const float acc[8], const Src8 &pre)
-{
-    epi_apply8_core(e, ob, m, n, N, acc, &pre);
-}
-
-__device__ __forceinline__ void epi_apply8_core(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, int64_t N,
-                                                const float acc[8], const Src8 *pre)
 {
     if (n + 7 < N && e.fast8) {
         float v[8];
@@ -382,7 +341,7 @@ __device__ __forceinline__ void epi_apply8_core(const EpiParams &e, const EpiBat
             const int64_t si = ob.src + m * e.src_sm + n;
             float sv[8];
             if (e.src_dt == KUDNN_DT_BF16) {
-                const uint4 raw = pre ? pre->lo : *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(e.src) + si);
+                const uint4 raw = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(e.src) + si);
                 const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -390,10 +349,8 @@ __device__ __forceinline__ void epi_apply8_core(const EpiParams &e, const EpiBat
                     sv[2 * q + 1] = u2f(w[q] & 0xffff0000u);
                 }
             } else if (e.src_dt == KUDNN_DT_F32) {
-                const float4 t0 = pre ? __builtin_bit_cast(float4, pre->lo)
-                                      : *reinterpret_cast<const float4 *>(static_cast<const float *>(e.src) + si);
-                const float4 t1 = pre ? __builtin_bit_cast(float4, pre->hi)
-                                      : *reinterpret_cast<const float4 *>(static_cast<const float *>(e.src) + si + 4);
+                const float4 t0 = *reinterpret_cast<const float4 *>(static_cast<const float *>(e.src) + si);
+                const float4 t1 = *reinterpret_cast<const float4 *>(static_cast<const float *>(e.src) + si + 4);
                 sv[0] = t0.x; sv[1] = t0.y; sv[2] = t0.z; sv[3] = t0.w;
                 sv[4] = t1.x; sv[5] = t1.y; sv[6] = t1.z; sv[7] = t1.w;
             } else {
@@ -432,6 +389,192 @@ __device__ __forceinline__ void epi_apply8_core(const EpiParams &e, const EpiBat
     }
     epi_apply4(e, ob, m, n, N, acc);
     epi_apply4(e, ob, m, n + 4, N, acc + 4);
+}
+
+// ---------------------------------------------------------------------------------------------------
+// Epilogue with the activation and the tensor types fixed at compile time.
+//
+// The generic epilogue above dispatches every option at run time; inlined at the many call sites of an unrolled
+// epilogue that is megabytes of code, and the jumps over the unused parts miss the instruction cache on every pass.
+// A "form" fixes the types of every epilogue tensor: EPI_FORM_BF16 (C rounding, bias, binary operand and output all
+// bf16) or EPI_FORM_F32 (all f32), in both cases with C not stored separately, beta == 0 and fast8 (output and binary
+// operand contiguous along n, 16-byte aligned 8-column groups). Anything else is EPI_FORM_GENERIC and goes through
+// epi_apply. Arithmetic and rounding are those of epi_apply.
+
+enum { EPI_FORM_BF16 = 0, EPI_FORM_F32 = 1, EPI_FORM_GENERIC = 2 };
+
+// Host-side choice of the form for an epilogue.
+inline int epi_form(const EpiParams &e)
+{
+    if (!e.fast8 || e.store_c || e.beta != 0.0f) {
+        return EPI_FORM_GENERIC;
+    }
+    const int dt = e.y_dt;
+    if ((dt != KUDNN_DT_BF16 && dt != KUDNN_DT_F32) || e.c_dt != dt || (e.bin != KUDNN_BINARY_NONE && e.src_dt != dt) ||
+        (e.bias != nullptr && e.bias_dt != dt)) {
+        return EPI_FORM_GENERIC;
+    }
+    return dt == KUDNN_DT_BF16 ? EPI_FORM_BF16 : EPI_FORM_F32;
+}
+
+template <int FORM>
+constexpr int form_dt()
+{
+    return FORM == EPI_FORM_BF16 ? KUDNN_DT_BF16 : KUDNN_DT_F32;
+}
+
+template <int ACT>
+__device__ __forceinline__ float act_fixed(float x, float alpha)
+{
+    if constexpr (ACT == KUDNN_ACT_RELU) {
+        return act_relu(x, alpha);
+    } else if constexpr (ACT == KUDNN_ACT_SWISH) {
+        return act_swish(x, alpha);
+    } else if constexpr (ACT == KUDNN_ACT_GELU_TANH) {
+        return act_gelu_tanh(x);
+    } else if constexpr (ACT == KUDNN_ACT_GELU_ERF) {
+        return act_gelu_erf(x);
+    } else {
+        return x;
+    }
+}
+
+// Raw bits of 8 consecutive elements: one 16-byte word for bf16, two for f32.
+struct Raw8 {
+    uint4 lo, hi;
+};
+
+// Bias and binary operand of one 8-column group, as loaded by epi_prefetch8.
+struct Pre8 {
+    Raw8 src, bias;
+};
+
+template <int FORM>
+__device__ __forceinline__ Raw8 load_raw8(const void *p, int64_t idx)
+{
+    Raw8 r{make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
+    if constexpr (FORM == EPI_FORM_BF16) {
+        r.lo = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p) + idx);
+    } else {
+        const uint4 *q = reinterpret_cast<const uint4 *>(static_cast<const float *>(p) + idx);
+        r.lo = q[0];
+        r.hi = q[1];
+    }
+    return r;
+}
+
+template <int FORM>
+__device__ __forceinline__ void unpack_raw8(const Raw8 &r, float v[8])
+{
+    const uint32_t w[8] = {r.lo.x, r.lo.y, r.lo.z, r.lo.w, r.hi.x, r.hi.y, r.hi.z, r.hi.w};
+    if constexpr (FORM == EPI_FORM_BF16) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            v[2 * q] = u2f(w[q] << 16);
+            v[2 * q + 1] = u2f(w[q] & 0xffff0000u);
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = u2f(w[q]);
+    }
+}
+
+// Loads the binary operand and the bias of group (m, n .. n+7). A bias broadcast along n (bias_sn == 0) is one
+// value, kept as f32 bits in bias.lo.x.
+template <int FORM>
+__device__ __forceinline__ Pre8 epi_prefetch8(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n)
+{
+    Pre8 p{};
+    if (e.bin != KUDNN_BINARY_NONE) {
+        p.src = load_raw8<FORM>(e.src, ob.src + m * e.src_sm + n);
+    }
+    if (e.bias != nullptr) {
+        if (e.bias_sn == 0) {
+            p.bias.lo.x = f2u(load_elem(e.bias, form_dt<FORM>(), ob.bias + m * e.bias_sm));
+        } else {
+            p.bias = load_raw8<FORM>(e.bias, ob.bias + m * e.bias_sm + n);
+        }
+    }
+    return p;
+}
+
+// Epilogue of the 8-column group (m, n .. n+7), all in bounds, operands from epi_prefetch8.
+template <int ACT, int FORM>
+__device__ __forceinline__ void epi_fast8(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, const float acc[8],
+                                          const Pre8 &pre)
+{
+    constexpr int DT = form_dt<FORM>();
+    float v[8];
+    float bv[8];
+    if (e.bias == nullptr) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) bv[q] = 0.0f;
+    } else if (e.bias_sn == 0) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) bv[q] = u2f(pre.bias.lo.x);
+    } else {
+        unpack_raw8<FORM>(pre.bias, bv);
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v[q] = round_store(DT, acc[q] * e.alpha + bv[q]);
+    if constexpr (ACT != KUDNN_ACT_UNIMPLEMENTED) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = act_round(DT, ACT, act_fixed<ACT>(v[q], e.act_alpha));
+    }
+    if (e.bin != KUDNN_BINARY_NONE) {
+        float sv[8];
+        unpack_raw8<FORM>(pre.src, sv);
+        if (e.bin == KUDNN_BINARY_ADD) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) v[q] = v[q] + sv[q];
+        } else if (e.bin == KUDNN_BINARY_EXT) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) v[q] = fmaf(sv[q], e.gamma, v[q]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) v[q] = v[q] * sv[q];
+        }
+    }
+    const int64_t yi = ob.y + m * e.y_sm + n;
+    if constexpr (FORM == EPI_FORM_BF16) {
+        uint32_t w[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            w[q] = static_cast<uint32_t>(f32_to_bf16_rne(v[2 * q])) |
+                   (static_cast<uint32_t>(f32_to_bf16_rne(v[2 * q + 1])) << 16);
+        }
+        *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(e.y) + yi) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+        float *yp = static_cast<float *>(e.y) + yi;
+        *reinterpret_cast<float4 *>(yp) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4 *>(yp + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+}
+
+// Epilogue of one in-bounds element (m, n) in a fixed form (used at the matrix edge).
+template <int ACT, int FORM>
+__device__ __forceinline__ void epi_elem(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, float acc)
+{
+    constexpr int DT = form_dt<FORM>();
+    float v = acc * e.alpha;
+    if (e.bias != nullptr) {
+        v += load_elem(e.bias, DT, ob.bias + m * e.bias_sm + n * e.bias_sn);
+    }
+    v = round_store(DT, v);
+    if constexpr (ACT != KUDNN_ACT_UNIMPLEMENTED) {
+        v = act_round(DT, ACT, act_fixed<ACT>(v, e.act_alpha));
+    }
+    if (e.bin != KUDNN_BINARY_NONE) {
+        const float sv = load_elem(e.src, DT, ob.src + m * e.src_sm + n);
+        if (e.bin == KUDNN_BINARY_ADD) {
+            v = v + sv;
+        } else if (e.bin == KUDNN_BINARY_EXT) {
+            v = fmaf(sv, e.gamma, v);
+        } else {
+            v = v * sv;
+        }
+    }
+    store_elem(e.y, DT, ob.y + m * e.y_sm + n, v);
 }
 
 // XCD-aware block order. The hardware deals workgroups round-robin over the 8 XCDs (block b runs on

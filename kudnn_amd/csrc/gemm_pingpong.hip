@@ -28,7 +28,10 @@
 //
 // Epilogue: the accumulators pass through LDS one 32-column strip at a time and are read back row-major, 8
 // consecutive columns per lane, so bias / activation / residual run on 8 values and the result is one 16-byte store;
-// the binary operand of strip j+1 is loaded while strip j is processed.
+// the bias and binary operand of a strip are loaded before its staging round trip. The activation is a template
+// argument of the kernel and the all-bf16 case has its own code, so the epilogue of a full tile is short straight-line
+// code (an epilogue that dispatched every option at run time at each of its 16 call sites made the kernel 2.2 MB and
+// spent most of its time in instruction-cache misses). Tiles that cross the matrix edge take a rolled per-element loop.
 #include <utility>
 
 #include "device_common.h"
@@ -77,6 +80,124 @@ __device__ __forceinline__ void copy_block(const uint16_t *base, uint32_t totalB
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)dst, 16, voff, 0, 0, 0);
 }
 
+// Writes strip j of a wave's accumulators (64 rows x 32 columns) to its staging area, row pitch kPitch floats.
+__device__ __forceinline__ void stage_strip(const f32x16_t (&accj)[2], float *stage, int lrow, int lh)
+{
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            float *dst = stage + (i * 32 + lrow) * kPitch + q4 * 8 + lh * 4;
+            *reinterpret_cast<float4 *>(dst) =
+                make_float4(accj[i][4 * q4 + 0], accj[i][4 * q4 + 1], accj[i][4 * q4 + 2], accj[i][4 * q4 + 3]);
+        }
+    }
+}
+
+// The staging area is private to the wave: ordering its LDS writes and reads needs a wave barrier only.
+__device__ __forceinline__ void wave_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Epilogue of a full tile (all rows and columns in bounds) in a fixed form: lane -> row rl + 16 * pass, columns
+// col8 .. +8 of each strip.
+template <int ACT, int FORM>
+__device__ __forceinline__ void epilogue_full(const EpiParams &ep, const EpiBatch &ob, const f32x16_t (&acc)[4][2],
+                                              float *stage, int lane, int64_t mW, int64_t nW)
+{
+    const int lrow = lane & 31, lh = lane >> 5;
+    const int col8 = (lane & 3) * 8, rl = lane >> 2;
+    sfor<4>([&](auto jc) __attribute__((always_inline)) {
+        constexpr int j = decltype(jc)::value;
+        const int64_t n = nW + j * 32 + col8;
+        Pre8 pre[4];
+        sfor<4>([&](auto pc) __attribute__((always_inline)) {
+            constexpr int ps = decltype(pc)::value;
+            pre[ps] = epi_prefetch8<FORM>(ep, ob, mW + rl + ps * 16, n);
+        });
+        stage_strip(acc[j], stage, lrow, lh);
+        wave_sync();
+        sfor<4>([&](auto pc) __attribute__((always_inline)) {
+            constexpr int ps = decltype(pc)::value;
+            const int r = rl + ps * 16;
+            const float *src = stage + r * kPitch + col8;
+            const float4 lo = *reinterpret_cast<const float4 *>(src);
+            const float4 hi = *reinterpret_cast<const float4 *>(src + 4);
+            const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            epi_fast8<ACT, FORM>(ep, ob, mW + r, n, v, pre[ps]);
+        });
+        wave_sync();
+    });
+}
+
+// Epilogue of a tile that crosses the matrix edge, in a fixed form: whole 8-column groups as in a full tile, the
+// last partial group of a row one element at a time; rolled loops keep the code small.
+template <int ACT, int FORM>
+__device__ __forceinline__ void epilogue_edge(const EpiParams &ep, const EpiBatch &ob, const f32x16_t (&acc)[4][2],
+                                              float *stage, int lane, int64_t mW, int64_t nW, int64_t M, int64_t N)
+{
+    const int lrow = lane & 31, lh = lane >> 5;
+    const int col8 = (lane & 3) * 8, rl = lane >> 2;
+    sfor<4>([&](auto jc) __attribute__((always_inline)) {
+        constexpr int j = decltype(jc)::value;
+        const int64_t n = nW + j * 32 + col8;
+        stage_strip(acc[j], stage, lrow, lh);
+        wave_sync();
+#pragma unroll 1
+        for (int ps = 0; ps < 4; ++ps) {
+            const int r = rl + ps * 16;
+            const int64_t m = mW + r;
+            const float *src = stage + r * kPitch + col8;
+            if (m < M && n + 7 < N) {
+                const float4 lo = *reinterpret_cast<const float4 *>(src);
+                const float4 hi = *reinterpret_cast<const float4 *>(src + 4);
+                const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                epi_fast8<ACT, FORM>(ep, ob, m, n, v, epi_prefetch8<FORM>(ep, ob, m, n));
+            } else if (m < M) {
+#pragma unroll 1
+                for (int q = 0; q < 8; ++q) {
+                    if (n + q < N) {
+                        epi_elem<ACT, FORM>(ep, ob, m, n + q, src[q]);
+                    }
+                }
+            }
+        }
+        wave_sync();
+    });
+}
+
+// Epilogue of any tile in the generic form: one element at a time through epi_apply (activation read at run time).
+__device__ __forceinline__ void epilogue_generic(const EpiParams &ep, const EpiBatch &ob, const f32x16_t (&acc)[4][2],
+                                                 float *stage, int lane, int64_t mW, int64_t nW, int64_t M, int64_t N)
+{
+    const int lrow = lane & 31, lh = lane >> 5;
+    const int col8 = (lane & 3) * 8, rl = lane >> 2;
+    sfor<4>([&](auto jc) __attribute__((always_inline)) {
+        constexpr int j = decltype(jc)::value;
+        const int64_t n = nW + j * 32 + col8;
+        stage_strip(acc[j], stage, lrow, lh);
+        wave_sync();
+#pragma unroll 1
+        for (int ps = 0; ps < 4; ++ps) {
+            const int r = rl + ps * 16;
+            const int64_t m = mW + r;
+            if (m < M) {
+#pragma unroll 1
+                for (int q = 0; q < 8; ++q) {
+                    if (n + q < N) {
+                        epi_apply(ep, ob, m, n + q, stage[r * kPitch + col8 + q]);
+                    }
+                }
+            }
+        }
+        wave_sync();
+    });
+}
+
+template <int ACT, int FORM>
 __global__ __launch_bounds__(512, 1) void gemm_bf16_pingpong_kernel(GemmOperands op, EpiParams ep, int tilesM,
                                                                      int tilesN, int group)
 {
@@ -241,47 +362,14 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_pingpong_kernel(GemmOperands
     // 64 x 36 floats (9 KB) per wave: waves 0-2 stage in a0, 3-5 in a1, 6-7 in b0
     float *stage = reinterpret_cast<float *>(wave < 3 ? a0 : (wave < 6 ? a1 : b0)) + (wave % 3) * (64 * kPitch);
     const EpiBatch ob = epi_batch_offsets(ep, batch);
-    const int col8 = (lane & 3) * 8;
-    const int rlane = lane >> 2;
-    const int64_t nBase = n0 + g * 128 + col8;
-    const int64_t mBase = m0 + p * 64 + rlane;
-    sfor<4>([&](auto jc) __attribute__((always_inline)) {
-        constexpr int j = decltype(jc)::value;
-        // binary operand of this strip, loaded before the staging round trip so its latency overlaps it
-        Src8 pre[4];
-        sfor<4>([&](auto pc) __attribute__((always_inline)) {
-            constexpr int ps = decltype(pc)::value;
-            pre[ps] = epi_load_src8(ep, ob, mBase + ps * 16, nBase + j * 32, M, N);
-        });
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-#pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-                float *dst = stage + (i * 32 + lrow) * kPitch + q4 * 8 + lh * 4;
-                *reinterpret_cast<float4 *>(dst) =
-                    make_float4(acc[j][i][4 * q4 + 0], acc[j][i][4 * q4 + 1], acc[j][i][4 * q4 + 2], acc[j][i][4 * q4 + 3]);
-            }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        sfor<4>([&](auto pc) __attribute__((always_inline)) {
-            constexpr int ps = decltype(pc)::value;
-            const int r = rlane + ps * 16;
-            const int64_t m = m0 + p * 64 + r;
-            const int64_t n = nBase + j * 32;
-            if (m < M && n < N) {
-                const float *src = stage + r * kPitch + col8;
-                const float4 lo = *reinterpret_cast<const float4 *>(src);
-                const float4 hi = *reinterpret_cast<const float4 *>(src + 4);
-                const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-                epi_apply8_pre(ep, ob, m, n, N, v, pre[ps]);
-            }
-        });
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    });
+    const int64_t mW = m0 + p * 64, nW = n0 + g * 128;
+    if constexpr (FORM == EPI_FORM_GENERIC) {
+        epilogue_generic(ep, ob, acc, stage, lane, mW, nW, M, N);
+    } else if (m0 + kBM <= M && n0 + kBN <= N) {
+        epilogue_full<ACT, FORM>(ep, ob, acc, stage, lane, mW, nW);
+    } else {
+        epilogue_edge<ACT, FORM>(ep, ob, acc, stage, lane, mW, nW, M, N);
+    }
 }
 
 }  // namespace
@@ -301,6 +389,30 @@ int kudnn_launch_gemm_bf16_pingpong(const GemmOperands &op, const EpiParams &ep,
     const int tilesM = static_cast<int>((op.M + kBM - 1) / kBM);
     const int tilesN = static_cast<int>((op.N + kBN - 1) / kBN);
     dim3 grid(static_cast<unsigned>(tilesM * tilesN), static_cast<unsigned>(batches));
-    hipLaunchKernelGGL(gemm_bf16_pingpong_kernel, grid, dim3(512), 0, stream, op, ep, tilesM, tilesN, 8);
+    // the activation and the tensor types of the epilogue select one of the compiled variants
+    decltype(&gemm_bf16_pingpong_kernel<0, EPI_FORM_GENERIC>) kernel = nullptr;
+    const int form = epi_form(ep);
+    auto pick = [&](auto formc) {
+        constexpr int F = decltype(formc)::value;
+        switch (ep.act) {
+            case KUDNN_ACT_UNIMPLEMENTED: kernel = gemm_bf16_pingpong_kernel<KUDNN_ACT_UNIMPLEMENTED, F>; break;
+            case KUDNN_ACT_RELU: kernel = gemm_bf16_pingpong_kernel<KUDNN_ACT_RELU, F>; break;
+            case KUDNN_ACT_SWISH: kernel = gemm_bf16_pingpong_kernel<KUDNN_ACT_SWISH, F>; break;
+            case KUDNN_ACT_GELU_TANH: kernel = gemm_bf16_pingpong_kernel<KUDNN_ACT_GELU_TANH, F>; break;
+            case KUDNN_ACT_GELU_ERF: kernel = gemm_bf16_pingpong_kernel<KUDNN_ACT_GELU_ERF, F>; break;
+            default: break;
+        }
+    };
+    if (form == EPI_FORM_BF16) {
+        pick(std::integral_constant<int, EPI_FORM_BF16>{});
+    } else if (form == EPI_FORM_F32) {
+        pick(std::integral_constant<int, EPI_FORM_F32>{});
+    } else {
+        kernel = gemm_bf16_pingpong_kernel<0, EPI_FORM_GENERIC>;  // reads the activation at run time
+    }
+    if (kernel == nullptr) {
+        return -1;  // not a fused activation
+    }
+    hipLaunchKernelGGL(kernel, grid, dim3(512), 0, stream, op, ep, tilesM, tilesN, 8);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

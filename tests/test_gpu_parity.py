@@ -274,6 +274,49 @@ def test_pingpong_shapes_and_epilogues(force_pingpong, mnk, post):
     compare(from_device(dy, dt), ref.buf, dt, f"{plan.describe()} {post}")
 
 
+@pytest.mark.parametrize("mnk", [(512, 512, 128), (300, 520, 192)])
+@pytest.mark.parametrize("ydt", [O.F32, O.F16, O.BF16])
+@pytest.mark.parametrize("bias_rows", [False, True])
+def test_pingpong_epilogue_forms(force_pingpong, mnk, ydt, bias_rows):
+    # bf16 operands with f32 / f16 / bf16 outputs: the kernel's fixed-type forms (bf16, f32) and its generic form
+    # (f16); a bias per column ([1, N]) or per row ([M, 1]); full tiles and tiles at the matrix edge
+    M, N, Kd = mnk
+    x = Case([M, Kd], O.BF16, seed=90, dist="normal", lo=0.0, hi=1.0)
+    w = Case([Kd, N], O.BF16, "BA", seed=91, dist="normal", lo=0.0, hi=0.05)
+    y = Case([M, N], ydt, zero=True)
+    b = Case([M, 1] if bias_rows else [1, N], ydt, seed=92, lo=-0.2, hi=0.2)
+    s = Case([M, N], ydt, seed=93, lo=-1.0, hi=1.0)
+    plan = K.LinearPostOps(x.desc, w.desc, y.desc, b.desc, act=K.ACT_GELU_ERF, binary=K.BIN_ADD, src=s.desc)
+    assert "pingpong" in plan.describe()
+    dy = zeros_device(y)
+    plan.run(x.device(), w.device(), dy, b.device(), s.device())
+    torch.cuda.synchronize()
+    ref = y.clone_empty()
+    O.linear_postops(x.t, w.t, ref, b.t, O.ACT_GELU_ERF, 0.0, O.BIN_ADD, s.t, 1.0)
+    compare(from_device(dy, ydt), ref.buf, ydt, f"{plan.describe()} ydt={ydt} bias_rows={bias_rows}")
+
+
+@pytest.mark.parametrize("kind", [O.RES_IDENTIAL, O.RES_EXT])
+def test_pingpong_linear_res_stores_c(force_pingpong, kind):
+    # LinearResFWD writes C and linearRes from one launch (the generic form of the epilogue)
+    M, N, Kd = 300, 264, 128
+    x = Case([M, Kd], O.BF16, seed=94, dist="normal", lo=0.0, hi=1.0)
+    w = Case([Kd, N], O.BF16, "BA", seed=95, dist="normal", lo=0.0, hi=0.05)
+    b = Case([1, N], O.BF16, seed=96, lo=-0.1, hi=0.1)
+    c = Case([M, N], O.BF16, zero=True)
+    res = Case([M, N], O.BF16, seed=97)
+    lr = Case([M, N], O.BF16, zero=True)
+    plan = K.LinearRes(x.desc, w.desc, c.desc, b.desc, res.desc, lr.desc, 1.0, 0.0, 1.0, kind)
+    assert "pingpong" in plan.describe()
+    dc, dlr = zeros_device(c), zeros_device(lr)
+    plan.run(x.device(), w.device(), dc, b.device(), res.device(), dlr, 0.625)
+    torch.cuda.synchronize()
+    rc, rlr = c.clone_empty(), lr.clone_empty()
+    O.linear_res(x.t, w.t, rc, b.t, res.t, rlr, kind, 0.625)
+    compare(from_device(dc, O.BF16), rc.buf, O.BF16, plan.describe() + " C")
+    compare(from_device(dlr, O.BF16), rlr.buf, O.BF16, plan.describe() + " linearRes")
+
+
 def test_pingpong_batched_and_strided_weight(force_pingpong):
     # 3 batches, K-major weight (packed to [N][K] by the pack kernel), bias per batch row
     dt = O.BF16
