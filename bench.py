@@ -4,9 +4,9 @@ Workload ("C3"): bf16 Linear + GELU(tanh) + residual a
 X[4096,4096] x W[11008,4096]^T, zero bias, residual R[4096,11008], fp32 accumulate, bf16 out. One step
 is one call of the fused Linear post-op chain through the C ABI on inputs already resident in HBM.
 
-Also reported (not `value`): the decode-shaped skinny Linear at M=1, K=4096, N in {4096, 14336}
-(configs[3]) in GB/s, timed over rotating weight copies (>= 512 MB) so that the 256 MB Infinity Cache
-cannot serve the weight stream, and the CPU baseline (the reference tests' portable naive loop, timed
+Also reported (not `value`): the decode-shaped skinny Linear at M in {1, 4, 16}, K=4096, N in {4096, 14336}
+(configs[3], Linear then element-wise multiply) in GB/s, timed over rotating weight copies (>= 512 MB) so that the 256 MB Infinity Cache
+cannot serve the weight stream; C1, C2 and C5 in TFLOP/s; and the CPU baseline (the reference tests' portable naive loop, timed
 on a bounded row sample of the same workload on this host's cores).
 
 Before the W counted warmup steps, the step is also run untimed for --prewarm-ms of wall time (default 300 ms):
@@ -34,6 +34,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "Linear+postop TFLOP/s (% MFMA peak) at 4096x4096x11008; M=1 GB/s (% HBM)"
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+PEAK_F32_TFLOPS = 157.3    # MI355X dense fp32 MFMA
 
 
 def parse():
@@ -45,6 +46,7 @@ def parse():
     p.add_argument("--only", choices=["c3", "copy"], default=None, help="profiling modes (see module docstring)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-decode", action="store_true")
+    p.add_argument("--no-others", action="store_true", help="skip the informational C1 / C2 / C5 lines")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU-baseline sample time")
     return p.parse_args()
 
@@ -105,8 +107,8 @@ def bench_c3(args, torch, K):
     }
 
 
-def bench_decode(args, torch, K, N):
-    M, Kd = 1, 4096
+def bench_decode(args, torch, K, N, M=1):
+    Kd = 4096
     dev = "cuda"
     wbytes = N * Kd * 2
     copies = max(2, -(-512 * 2**20 // wbytes))  # >= 512 MB of distinct weights
@@ -129,6 +131,45 @@ def bench_decode(args, torch, K, N):
     gbs = alg_bytes / (ms * 1e-3) / 1e9
     return {"N": N, "M": M, "K": Kd, "plan": plan.describe(), "us": ms * 1e3, "us_wall": ms_wall * 1e3,
             "GB/s": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "weight_copies": copies, "alg_bytes": alg_bytes}
+
+
+def bench_config(args, torch, K, name):
+    """The other configurations (informational, not `value`): C1, C2 (fp32) and C5 (bf16 3-D, K-major weight).
+
+    C2's inputs are rotated over 4 copies (>= 512 MB) so that the Infinity Cache does not hold them; C1's 5 MB working
+    set is cache-resident whatever is done, and C5's 760 MB footprint exceeds the cache by itself."""
+    dev = "cuda"
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    if name == "C1":
+        M, Kd, N, dt, kind, alpha, copies = 128, 1024, 1024, torch.float32, K.ACT_RELU, 0.0, 1
+    elif name == "C2":
+        M, Kd, N, dt, kind, alpha, copies = 2048, 4096, 4096, torch.float32, K.ACT_SWISH, 1.0, 4
+    else:
+        M, Kd, N, dt, kind, alpha, copies = 16384, 5120, 13824, torch.bfloat16, K.ACT_SWISH, 1.0, 1
+    kdt = K.F32 if dt == torch.float32 else K.BF16
+    xs = [torch.randn(M, Kd, device=dev, generator=g).to(dt) for _ in range(copies)]
+    if name == "C5":  # W{1,5120,13824} ABC: K-major [K][N], broadcast over the batch of 8
+        ws = [(torch.randn(Kd, N, device=dev, generator=g) * 0.014).to(dt)]
+        da, db, dc = K.desc([8, 2048, Kd], kdt, "ABC"), K.desc([1, Kd, N], kdt, "ABC"), K.desc([8, 2048, N], kdt, "ABC")
+        dbias = K.desc([1, 1, N], kdt, "ABC")
+    else:  # nn.Linear weight [N][K] (logical [K,N], layout BA)
+        ws = [(torch.randn(N, Kd, device=dev, generator=g) * (1.0 / 64)).to(dt) for _ in range(copies)]
+        da, db, dc, dbias = K.desc([M, Kd], kdt), K.desc([Kd, N], kdt, "BA"), K.desc([M, N], kdt), K.desc([1, N], kdt)
+    bias = (torch.randn(1, N, device=dev, generator=g) * 0.02).to(dt)
+    y = torch.empty(M, N, device=dev, dtype=dt)
+    plan = K.LinearActivation(da, db, dc, dbias, alpha, 0.0, kind)
+    stream = torch.cuda.current_stream()
+
+    def step(i=0):
+        plan.run(xs[i % copies], ws[i % copies], y, bias, stream=stream)
+
+    ms, _ = time_launches(step, args.steps, max(args.warmup, copies), torch, stream, args.prewarm_ms)
+    flops = 2.0 * M * N * Kd
+    tflops = flops / (ms * 1e-3) / 1e12
+    peak = PEAK_F32_TFLOPS if dt == torch.float32 else PEAK_BF16_TFLOPS
+    return {"config": name, "M": M, "K": Kd, "N": N, "plan": plan.describe(), "us": ms * 1e3, "TFLOP/s": tflops,
+            "frac_peak": tflops / peak, "input_copies": copies}
 
 
 def cpu_baseline(args, np):
@@ -190,7 +231,9 @@ def main():
 
     c3 = bench_c3(args, torch, K)
     only = args.only == "c3"
-    decode = [] if (args.no_decode or only) else [bench_decode(args, torch, K, n) for n in (4096, 14336)]
+    decode = [] if (args.no_decode or only) else [bench_decode(args, torch, K, n, m) for n in (4096, 14336)
+                                                  for m in (1, 4, 16)]
+    others = [] if (args.no_others or only) else [bench_config(args, torch, K, c) for c in ("C1", "C2", "C5")]
     cpu = None if (args.no_cpu_baseline or only) else cpu_baseline(args, np)
 
     traffic = None
@@ -222,6 +265,7 @@ def main():
                      "kernel_ms": round(c3["ms"], 4), "alg_flops": c3["flops"], "alg_bytes": c3["alg_bytes"]},
         "cpu_baseline": cpu,
         "decode": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()} for d in decode],
+        "other_configs": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()} for d in others],
     }
     print(json.dumps(out))
 
