@@ -13,7 +13,8 @@ Before the W counted warmup steps, the step is also run untimed for --prewarm-ms
 the GPU raises its clocks over the first ~100 ms of sustained load, and a timed region that starts on a cold GPU
 reports the ramp rather than the kernel (a 25 ms region read 475 us per step cold against 412 us warm).
 
-For profiling, --only c3 runs just the C3 step (JSON line without decode or CPU baseline), and --only copy runs an
+For profiling, --only c3 runs just the C3 step (JSON line without decode or CPU baseline), --only decode just the
+decode lines, and --only copy runs an
 elementwise copy-like kernel (y = -x, 512 MiB bf16 in, 512 MiB out) whose known traffic calibrates the
 FETCH_SIZE / WRITE_SIZE counters against which the C3 kernel's HBM traffic is read.
 
@@ -43,7 +44,8 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--prewarm-ms", type=float, default=300.0, help="untimed run time before warmup (clock ramp)")
-    p.add_argument("--only", choices=["c3", "copy"], default=None, help="profiling modes (see module docstring)")
+    p.add_argument("--only", choices=["c3", "copy", "decode"], default=None,
+                   help="profiling modes (see module docstring)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--no-others", action="store_true", help="skip the informational C1 / C2 / C5 lines")
@@ -227,6 +229,12 @@ def main():
         ms, _ = time_launches(lambda i=0: torch.neg(x, out=y), args.steps, args.warmup, torch, stream, 0.0)
         print(json.dumps({"kernel": "copy-like elementwise (torch.neg, bf16)", "bytes_read": 2 * n,
                           "bytes_written": 2 * n, "ms": round(ms, 4), "GB/s": round(4 * n / (ms * 1e-3) / 1e9, 1)}))
+        return
+
+    if args.only == "decode":
+        decode = [bench_decode(args, torch, K, n, m) for n in (4096, 14336) for m in (1, 4, 16)]
+        print(json.dumps({"decode": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}
+                                     for d in decode]}))
         return
 
     c3 = bench_c3(args, torch, K)

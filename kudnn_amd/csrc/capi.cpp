@@ -483,7 +483,7 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
     if (core.computeDt == KUDNN_DT_BF16) {
         if (core.M <= 16) {
             core.engine = ENGINE_SKINNY_BF16;
-            core.cfg = KUDNN_CFG_SKINNY_BF16;
+            core.cfg = core.M == 1 ? KUDNN_CFG_GEMV_BF16 : KUDNN_CFG_SKINNY_BF16;
         } else {
             core.engine = ENGINE_MFMA_BF16;
             auto tiles = [&](int64_t bm, int64_t bn) { return (core.M + bm - 1) / bm * ((core.N + bn - 1) / bn) * batches; };
@@ -526,6 +526,7 @@ const char *CfgName(int cfg)
         case KUDNN_CFG_F32_128x128: return "mfma_f32_128x128";
         case KUDNN_CFG_F32_64x64: return "mfma_f32_64x64";
         case KUDNN_CFG_SKINNY_BF16: return "skinny_bf16_16xK";
+        case KUDNN_CFG_GEMV_BF16: return "skinny_bf16_gemv_row";
         default: return "unknown";
     }
 }

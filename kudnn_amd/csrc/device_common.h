@@ -186,15 +186,37 @@ __device__ __forceinline__ EpiBatch epi_batch_offsets(const EpiParams &e, int64_
     return o;
 }
 
-// Applies the epilogue to one accumulator value of output element (m, n). m, n are in bounds.
-__device__ __forceinline__ void epi_apply(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, float acc)
+// Epilogue operands of one output element (C when beta != 0, bias, binary operand), loadable ahead of the
+// accumulator so that their latency overlaps the main loop.
+struct EpiPre1 {
+    float c, bias, src;
+};
+
+__device__ __forceinline__ EpiPre1 epi_prefetch1(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n)
+{
+    EpiPre1 p{0.0f, 0.0f, 0.0f};
+    if (e.beta != 0.0f) {
+        p.c = load_elem(e.c, e.c_dt, ob.c + m * e.c_sm + n * e.c_sn);
+    }
+    if (e.bias != nullptr) {
+        p.bias = load_elem(e.bias, e.bias_dt, ob.bias + m * e.bias_sm + n * e.bias_sn);
+    }
+    if (e.bin != KUDNN_BINARY_NONE) {
+        p.src = load_elem(e.src, e.src_dt, ob.src + m * e.src_sm + n * e.src_sn);
+    }
+    return p;
+}
+
+// Applies the epilogue to one accumulator value of output element (m, n), with its operands from epi_prefetch1.
+__device__ __forceinline__ void epi_apply_pre(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, float acc,
+                                              const EpiPre1 &p)
 {
     float v = acc * e.alpha;
     if (e.beta != 0.0f) {
-        v += e.beta * load_elem(e.c, e.c_dt, ob.c + m * e.c_sm + n * e.c_sn);
+        v += e.beta * p.c;
     }
     if (e.bias != nullptr) {
-        v += load_elem(e.bias, e.bias_dt, ob.bias + m * e.bias_sm + n * e.bias_sn);
+        v += p.bias;
     }
     v = round_store(e.c_dt, v);
     if (e.store_c) {
@@ -204,16 +226,21 @@ __device__ __forceinline__ void epi_apply(const EpiParams &e, const EpiBatch &ob
         v = act_round(e.c_dt, e.act, apply_act(e.act, v, e.act_alpha));
     }
     if (e.bin != KUDNN_BINARY_NONE) {
-        float s = load_elem(e.src, e.src_dt, ob.src + m * e.src_sm + n * e.src_sn);
         if (e.bin == KUDNN_BINARY_ADD) {
-            v = v + s;
+            v = v + p.src;
         } else if (e.bin == KUDNN_BINARY_EXT) {
-            v = fmaf(s, e.gamma, v);
+            v = fmaf(p.src, e.gamma, v);
         } else {
-            v = v * s;
+            v = v * p.src;
         }
     }
     store_elem(e.y, e.y_dt, ob.y + m * e.y_sm + n * e.y_sn, v);
+}
+
+// Applies the epilogue to one accumulator value of output element (m, n). m, n are in bounds.
+__device__ __forceinline__ void epi_apply(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, float acc)
+{
+    epi_apply_pre(e, ob, m, n, acc, epi_prefetch1(e, ob, m, n));
 }
 
 // Epilogue for four consecutive columns n..n+3 of row m (the MFMA output layout gives each lane runs
@@ -403,10 +430,11 @@ __device__ __forceinline__ void epi_apply8(const EpiParams &e, const EpiBatch &o
 
 enum { EPI_FORM_BF16 = 0, EPI_FORM_F32 = 1, EPI_FORM_GENERIC = 2 };
 
-// Host-side choice of the form for an epilogue.
-inline int epi_form(const EpiParams &e)
+// Host-side choice of the form for an epilogue. need8: the kernel stores 8-column groups with 16-byte accesses
+// (fast8 must hold); a kernel that stores single elements passes false.
+inline int epi_form(const EpiParams &e, bool need8 = true)
 {
-    if (!e.fast8 || e.store_c || e.beta != 0.0f) {
+    if ((need8 && !e.fast8) || e.store_c || e.beta != 0.0f) {
         return EPI_FORM_GENERIC;
     }
     const int dt = e.y_dt;
@@ -549,6 +577,32 @@ __device__ __forceinline__ void epi_fast8(const EpiParams &e, const EpiBatch &ob
         *reinterpret_cast<float4 *>(yp) = make_float4(v[0], v[1], v[2], v[3]);
         *reinterpret_cast<float4 *>(yp + 4) = make_float4(v[4], v[5], v[6], v[7]);
     }
+}
+
+// Epilogue of one element (m, n) in a fixed form, its bias and binary operand from epi_prefetch1.
+template <int ACT, int FORM>
+__device__ __forceinline__ void epi_elem_pre(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, float acc,
+                                             const EpiPre1 &p)
+{
+    constexpr int DT = form_dt<FORM>();
+    float v = acc * e.alpha;
+    if (e.bias != nullptr) {
+        v += p.bias;
+    }
+    v = round_store(DT, v);
+    if constexpr (ACT != KUDNN_ACT_UNIMPLEMENTED) {
+        v = act_round(DT, ACT, act_fixed<ACT>(v, e.act_alpha));
+    }
+    if (e.bin != KUDNN_BINARY_NONE) {
+        if (e.bin == KUDNN_BINARY_ADD) {
+            v = v + p.src;
+        } else if (e.bin == KUDNN_BINARY_EXT) {
+            v = fmaf(p.src, e.gamma, v);
+        } else {
+            v = v * p.src;
+        }
+    }
+    store_elem(e.y, DT, ob.y + m * e.y_sm + n * e.y_sn, v);
 }
 
 // Epilogue of one in-bounds element (m, n) in a fixed form (used at the matrix edge).

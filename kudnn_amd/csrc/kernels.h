@@ -15,6 +15,7 @@ enum {
     KUDNN_CFG_F32_128x128 = 10,
     KUDNN_CFG_F32_64x64 = 11,
     KUDNN_CFG_SKINNY_BF16 = 20,
+    KUDNN_CFG_GEMV_BF16 = 21,  // M == 1: one wave per weight row (skinny engine)
 };
 
 // Returns 0 on success, -1 if the launch failed or cfg is unknown.
@@ -24,7 +25,7 @@ int kudnn_launch_gemm_bf16(const GemmOperands &op, const EpiParams &ep, int64_t 
 bool kudnn_pingpong_eligible(const GemmOperands &op);
 int kudnn_launch_gemm_bf16_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream);
 int kudnn_launch_gemm_f32(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, hipStream_t stream);
-// M <= 16, bf16 operands, B contiguous along K.
+// M <= 16, bf16 operands, B contiguous along K (M == 1: row-per-wave GEMV, otherwise 16-row MFMA tiles).
 int kudnn_launch_skinny_bf16(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream);
 
 // Pack: dst[b][r][k] (row pitch kp, zero for k >= cols) = convert(src element (b, r, k)) where the source

@@ -9,6 +9,8 @@
 //    contiguous bytes), UNR k-steps are issued back to back to keep enough bytes in flight;
 //  - X rows (m < M, tiny and cache-resident) form the second MFMA operand; lanes with m >= M feed zeros;
 //  - the KW partial 16x16 tiles are summed through LDS and wave 0 runs the fused epilogue.
+#include <utility>
+
 #include "device_common.h"
 #include "kernels.h"
 
@@ -101,6 +103,129 @@ __global__ __launch_bounds__(KW * 64) void skinny_bf16_kernel(GemmOperands op, E
     epi_apply4(ep, ob, r16, n, N, v);
 }
 
+// M = 1: one wave per weight row. Lane l reads 16-byte chunks l, l + 64, ... of the row, so every load instruction of
+// a wave reads 1 KB of one row contiguously. (The MFMA operand layout of the kernel above reads 16 rows x 64 bytes per
+// instruction; at M = 1, where the multiply is negligible, the memory system serves that pattern at about 4.9 TB/s
+// against 6.4 TB/s for whole rows, measured on MI355X with the weight streamed from HBM.) K is walked in blocks of
+// 4096 (512 chunks, 8 per lane): X's chunks of the block are loaded first, then the row's, all in flight together;
+// products are summed in f32 with FMA per lane, then across the wave. Lane 0 runs the epilogue, whose operands are
+// loaded during the row. The activation and the epilogue's tensor types are template arguments (as in the MFMA
+// kernels) so the kernel's tail is short; batch indices are only decomposed when there is more than one batch.
+constexpr int kGemvCh = 8;  // chunks per lane per K block
+
+template <bool FULL>
+__device__ __forceinline__ float gemv_block(const uint16_t *X, const uint16_t *W, int c0, int chunks, int lane)
+{
+    typedef uint32_t v4 __attribute__((ext_vector_type(4)));
+    const v4 zero = {0u, 0u, 0u, 0u};
+    v4 xv[kGemvCh], wv[kGemvCh];
+#pragma unroll
+    for (int c = 0; c < kGemvCh; ++c) {
+        const int ch = c0 + c * 64 + lane;
+        xv[c] = (FULL || ch < chunks) ? *reinterpret_cast<const v4 *>(X + static_cast<int64_t>(ch) * 8) : zero;
+    }
+#pragma unroll
+    for (int c = 0; c < kGemvCh; ++c) {
+        const int ch = c0 + c * 64 + lane;
+        wv[c] = (FULL || ch < chunks) ? __builtin_nontemporal_load(reinterpret_cast<const v4 *>(W + static_cast<int64_t>(ch) * 8))
+                                      : zero;
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kGemvCh; ++c) {
+        const uint32_t w[4] = {wv[c][0], wv[c][1], wv[c][2], wv[c][3]};
+        const uint32_t x[4] = {xv[c][0], xv[c][1], xv[c][2], xv[c][3]};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            sum = fmaf(u2f(w[j] << 16), u2f(x[j] << 16), sum);
+            sum = fmaf(u2f(w[j] & 0xffff0000u), u2f(x[j] & 0xffff0000u), sum);
+        }
+    }
+    return sum;
+}
+
+template <int ACT, int FORM>
+__global__ __launch_bounds__(256) void gemv_bf16_kernel(GemmOperands op, EpiParams ep)
+{
+    const int lane = threadIdx.x & 63;
+    const int n = static_cast<int>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (n >= op.N) {
+        return;  // no barrier or LDS below: a wave past the last row just ends
+    }
+    int64_t aoff = 0, boff = 0;
+    EpiBatch ob{0, 0, 0, 0};
+    if (gridDim.y > 1) {
+        const int64_t batch = blockIdx.y;
+        const int64_t i2 = batch % ep.bdim[2];
+        const int64_t i1 = (batch / ep.bdim[2]) % ep.bdim[1];
+        const int64_t i0 = batch / (ep.bdim[2] * ep.bdim[1]);
+        aoff = i0 * op.a_bs[0] + i1 * op.a_bs[1] + i2 * op.a_bs[2];
+        boff = i0 * op.b_bs[0] + i1 * op.b_bs[1] + i2 * op.b_bs[2];
+        ob = epi_batch_offsets(ep, batch);
+    }
+    const uint16_t *X = static_cast<const uint16_t *>(op.a) + aoff;
+    const uint16_t *W = static_cast<const uint16_t *>(op.b) + boff + static_cast<int64_t>(n) * op.ldb;
+    // rows are 16-byte aligned with a zero-padded or exact multiple-of-8 length (the planner packs otherwise), so whole
+    // 16-byte chunks up to ceil(K / 8) are in bounds; the launcher guarantees ceil(K / 8) < 2^31
+    const int chunks = static_cast<int>((op.K + 7) / 8);
+    const EpiPre1 pre = epi_prefetch1(ep, ob, 0, n);
+    float sum = 0.0f;
+    int c0 = 0;
+    for (; c0 + kGemvCh * 64 <= chunks; c0 += kGemvCh * 64) {
+        sum += gemv_block<true>(X, W, c0, chunks, lane);
+    }
+    if (c0 < chunks) {
+        sum += gemv_block<false>(X, W, c0, chunks, lane);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        sum += __shfl_xor(sum, o);
+    }
+    if (lane == 0) {
+        if constexpr (FORM == EPI_FORM_GENERIC) {
+            epi_apply_pre(ep, ob, 0, n, sum, pre);
+        } else {
+            epi_elem_pre<ACT, FORM>(ep, ob, 0, n, sum, pre);
+        }
+    }
+}
+
+// 32-bit row and chunk indices
+bool gemv_eligible(const GemmOperands &op)
+{
+    return op.M == 1 && op.N < (int64_t(1) << 31) / 4 && (op.K + 7) / 8 < (int64_t(1) << 31);
+}
+
+int launch_gemv(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream)
+{
+    decltype(&gemv_bf16_kernel<0, EPI_FORM_GENERIC>) kernel = nullptr;
+    const int form = epi_form(ep, false);
+    auto pick = [&](auto formc) {
+        constexpr int F = decltype(formc)::value;
+        switch (ep.act) {
+            case KUDNN_ACT_UNIMPLEMENTED: kernel = gemv_bf16_kernel<KUDNN_ACT_UNIMPLEMENTED, F>; break;
+            case KUDNN_ACT_RELU: kernel = gemv_bf16_kernel<KUDNN_ACT_RELU, F>; break;
+            case KUDNN_ACT_SWISH: kernel = gemv_bf16_kernel<KUDNN_ACT_SWISH, F>; break;
+            case KUDNN_ACT_GELU_TANH: kernel = gemv_bf16_kernel<KUDNN_ACT_GELU_TANH, F>; break;
+            case KUDNN_ACT_GELU_ERF: kernel = gemv_bf16_kernel<KUDNN_ACT_GELU_ERF, F>; break;
+            default: break;
+        }
+    };
+    if (form == EPI_FORM_BF16) {
+        pick(std::integral_constant<int, EPI_FORM_BF16>{});
+    } else if (form == EPI_FORM_F32) {
+        pick(std::integral_constant<int, EPI_FORM_F32>{});
+    } else {
+        kernel = gemv_bf16_kernel<0, EPI_FORM_GENERIC>;  // reads the activation at run time
+    }
+    if (kernel == nullptr) {
+        return -1;
+    }
+    dim3 grid(static_cast<unsigned>((op.N + 3) / 4), static_cast<unsigned>(batches));
+    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, op, ep);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 template <int KW, int UNR>
 int launch(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream)
 {
@@ -120,6 +245,9 @@ int kudnn_launch_skinny_bf16(const GemmOperands &op, const EpiParams &ep, int64_
 {
     if (op.M > 16) {
         return -1;
+    }
+    if (gemv_eligible(op)) {
+        return launch_gemv(op, ep, batches, stream);
     }
     // Few weight row-groups: split K over 8 waves per workgroup to keep more loads in flight.
     const int64_t groups = (op.N + 15) / 16 * batches;

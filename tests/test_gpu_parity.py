@@ -222,6 +222,53 @@ def test_c4_skinny_mul(M, N):
     compare(from_device(dy, O.BF16), ref.buf, O.BF16, f"C4 M={M} N={N}")
 
 
+@pytest.mark.parametrize("Kd", [40, 1001, 1024, 2048, 4096, 9000])
+@pytest.mark.parametrize("post", ["bias_gelu_add", "swish_f32", "gemm_beta"])
+def test_m1_row_gemv(Kd, post):
+    # M = 1 takes the row-per-wave GEMV: K blocks of 512 chunks, a K tail (K % 8 != 0 packs the operands with zero
+    # padding), every epilogue option through the generic per-element path
+    N = 300
+    ydt = O.F32 if post in ("swish_f32", "gemm_beta") else O.BF16
+    x = Case([1, Kd], O.BF16, seed=200, dist="normal", lo=0.0, hi=1.0)
+    w = Case([Kd, N], O.BF16, "BA", seed=201, dist="normal", lo=0.0, hi=0.05)
+    b = Case([1, N], ydt, seed=202, lo=-0.2, hi=0.2)
+    y = Case([1, N], ydt, seed=203, lo=-1.0, hi=1.0) if post == "gemm_beta" else Case([1, N], ydt, zero=True)
+    dy = torch.from_numpy(y.t.buf.view(np.int16).copy() if ydt != O.F32 else y.t.buf.copy()).cuda()
+    ref = O.Tensor(y.t.dims, y.t.strides, ydt, y.t.buf.copy())
+    if post == "bias_gelu_add":
+        s = Case([1, N], ydt, seed=204, lo=-1.0, hi=1.0)
+        plan = K.LinearPostOps(x.desc, w.desc, y.desc, b.desc, act=K.ACT_GELU_TANH, binary=K.BIN_ADD, src=s.desc)
+        plan.run(x.device(), w.device(), dy, b.device(), s.device())
+        O.linear_postops(x.t, w.t, ref, b.t, O.ACT_GELU_TANH, 0.0, O.BIN_ADD, s.t)
+    elif post == "swish_f32":
+        plan = K.LinearActivation(x.desc, w.desc, y.desc, b.desc, 1.0, 0.0, K.ACT_SWISH)
+        plan.run(x.device(), w.device(), dy, b.device())
+        O.linear_act(x.t, w.t, ref, b.t, O.ACT_SWISH, 1.0)
+    else:
+        plan = K.Gemm(x.desc, w.desc, y.desc, b.desc)
+        plan.run(x.device(), w.device(), dy, b.device(), alpha=0.5, beta=0.25)
+        O.gemm(x.t, w.t, ref, b.t, 0.5, 0.25)
+    assert plan.describe().startswith("skinny")
+    torch.cuda.synchronize()
+    compare(from_device(dy, ydt), ref.buf, ydt, f"M=1 K={Kd} {post} {plan.describe()}")
+
+
+def test_m1_row_gemv_batched_broadcast_weight():
+    # 3 batches of one row each against one K-major weight (packed once, batch stride 0)
+    Kd, N = 640, 200
+    x = Case([3, 1, Kd], O.BF16, "ABC", seed=210, dist="normal", lo=0.0, hi=1.0)
+    w = Case([1, Kd, N], O.BF16, "ABC", seed=211, dist="normal", lo=0.0, hi=0.05)
+    b = Case([1, 1, N], O.BF16, "ABC", seed=212, lo=-0.1, hi=0.1)
+    c = Case([3, 1, N], O.BF16, "ABC", zero=True)
+    plan = K.LinearActivation(x.desc, w.desc, c.desc, b.desc, 0.0, 0.0, K.ACT_RELU)
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc, b.device())
+    torch.cuda.synchronize()
+    ref = c.clone_empty()
+    O.linear_act(x.t, w.t, ref, b.t, O.ACT_RELU, 0.0)
+    compare(from_device(dc, O.BF16), ref.buf, O.BF16, plan.describe())
+
+
 def test_c5_bf16_3d_silu_kmajor_rows():
     B, S, Kd, N = 8, 2048, 5120, 13824
     x = Case([B, S, Kd], O.BF16, "ABC", seed=0, dist="normal", lo=0.0, hi=1.0)
