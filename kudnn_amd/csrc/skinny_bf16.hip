@@ -226,6 +226,117 @@ int launch_gemv(const GemmOperands &op, const EpiParams &ep, int64_t batches, hi
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+// 2 <= M <= 16: 16 weight rows per workgroup, KW waves splitting K into blocks of 256 (block b goes to wave b % KW).
+// A wave loads a block of all 16 rows two rows per instruction (lanes 0-31 one row, 32-63 the next: 512 contiguous
+// bytes per row, whole cache lines; the MFMA operand layout would read 16 rows x 64 bytes per instruction, which the
+// memory system streams at about 4.9 TB/s against 6.4 TB/s for whole rows, measured at M = 1), writes it to a
+// per-wave LDS tile (16 rows x 32 chunks of 16 bytes, row pitch 33 chunks: the row-wise writes and the reads of 16 rows
+// at one chunk both touch every bank once, and every access is a per-lane base plus an immediate offset), and reads
+// it back in the operand layout of v_mfma_f32_16x16x32_bf16, weight rows first, X (rows m < M, cache-resident) second.
+// Loads go through buffer resources and are issued by every lane: a lane with nothing to load (a chunk past K, an X
+// row m >= M) gets an offset past the resource's range, which reads zero, so no branch separates the loads of a block.
+// The KW partial 16 x 16 tiles are summed through LDS and wave 0 runs the epilogue on runs of 4 consecutive columns.
+template <int KW>
+__global__ __launch_bounds__(KW * 64) void skinny_rows_kernel(GemmOperands op, EpiParams ep)
+{
+    constexpr int kPitch = 33;  // chunks per LDS row
+    __shared__ u32x4_t tile[KW][16 * kPitch];
+    __shared__ f32x4_t part[KW][64];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t M = op.M, N = op.N;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
+    int64_t aoff = 0, boff = 0;
+    const int64_t batch = blockIdx.y;
+    if (gridDim.y > 1) {
+        const int64_t i2 = batch % ep.bdim[2];
+        const int64_t i1 = (batch / ep.bdim[2]) % ep.bdim[1];
+        const int64_t i0 = batch / (ep.bdim[2] * ep.bdim[1]);
+        aoff = i0 * op.a_bs[0] + i1 * op.a_bs[1] + i2 * op.a_bs[2];
+        boff = i0 * op.b_bs[0] + i1 * op.b_bs[1] + i2 * op.b_bs[2];
+    }
+    const uint16_t *X = static_cast<const uint16_t *>(op.a) + aoff;
+    const uint16_t *W = static_cast<const uint16_t *>(op.b) + boff;
+    const int r16 = lane & 15;
+    const int q = lane >> 4;
+    const int half = lane >> 5, c32 = lane & 31;
+    // rows are 16-byte aligned with a zero-padded or exact multiple-of-8 length (the planner packs otherwise), so whole
+    // chunks up to ceil(K / 8) are in bounds; the launcher guarantees N * ldb * 2 < 2^31 and M * lda * 2 < 2^31
+    const int chunks = static_cast<int>((op.K + 7) / 8);
+    const int blocks = (chunks + 31) / 32;
+    constexpr uint32_t kOut = 0xFFFFFFF0u;  // past any range below
+    const __amdgpu_buffer_rsrc_t wrs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)W, (short)0, static_cast<int>(N * op.ldb * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t xrs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)X, (short)0, static_cast<int>(M * op.lda * 2), 0x00020000);
+    const uint32_t rowBytes = static_cast<uint32_t>(op.ldb) * 2u;
+    const uint32_t xrow = static_cast<uint32_t>(r16) * static_cast<uint32_t>(op.lda) * 2u;
+    // byte offset of this lane's row within instruction i (rows 2i, 2i+1; rows past N load row N-1, never stored)
+    uint32_t wrow[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int64_t row = n0 + 2 * i + half;
+        wrow[i] = static_cast<uint32_t>(row < N ? row : N - 1) * rowBytes;
+    }
+    u32x4_t *tw = tile[wave];
+
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int b = wave; b < blocks; b += KW) {
+        const int c0 = b * 32;
+        const bool win = c0 + c32 < chunks;
+        u32x4_t wv[8], xv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            wv[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, win ? wrow[i] + static_cast<uint32_t>(c0 + c32) * 16u : kOut, 0, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {  // k-step k of the block: chunk c0 + 4k + q
+            const int kc = c0 + 4 * k + q;
+            const bool in = r16 < M && kc < chunks;
+            xv[k] = __builtin_amdgcn_raw_buffer_load_b128(xrs, in ? xrow + static_cast<uint32_t>(kc) * 16u : kOut, 0, 0);
+        }
+        // the previous block's tile reads have returned (their MFMAs consumed them); order the rewrite after them
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int i = 0; i < 8; ++i) tw[(2 * i + half) * kPitch + c32] = wv[i];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const u32x4_t wf = tw[r16 * kPitch + 4 * k + q];
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, wf), __builtin_bit_cast(bf16x8_t, xv[k]),
+                                                          acc, 0, 0, 0);
+        }
+    }
+
+    part[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0) {
+        return;
+    }
+    f32x4_t sum = part[0][lane];
+#pragma unroll
+    for (int w = 1; w < KW; ++w) {
+        const f32x4_t p = part[w][lane];
+        sum[0] += p[0];
+        sum[1] += p[1];
+        sum[2] += p[2];
+        sum[3] += p[3];
+    }
+    // lane holds D[n = n0 + 4q + i][m = r16], i = 0..3
+    const int64_t n = n0 + 4 * q;
+    if (r16 >= M || n >= N) {
+        return;
+    }
+    const EpiBatch ob = epi_batch_offsets(ep, batch);
+    const float v[4] = {sum[0], sum[1], sum[2], sum[3]};
+    epi_apply4(ep, ob, r16, n, N, v);
+}
+
 template <int KW, int UNR>
 int launch(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream)
 {
@@ -248,6 +359,17 @@ int kudnn_launch_skinny_bf16(const GemmOperands &op, const EpiParams &ep, int64_
     }
     if (gemv_eligible(op)) {
         return launch_gemv(op, ep, batches, stream);
+    }
+    if (op.N * op.ldb * 2 < (int64_t(1) << 31) && op.M * op.lda * 2 < (int64_t(1) << 31)) {
+        // fewer than 2 row groups per CU: split K over 16 waves (one workgroup per CU); otherwise 8 (two per CU)
+        const int64_t groups = (op.N + 15) / 16 * batches;
+        dim3 grid(static_cast<unsigned>((op.N + 15) / 16), static_cast<unsigned>(batches));
+        if (groups < 512) {
+            hipLaunchKernelGGL(skinny_rows_kernel<16>, grid, dim3(16 * 64), 0, stream, op, ep);
+        } else {
+            hipLaunchKernelGGL(skinny_rows_kernel<8>, grid, dim3(8 * 64), 0, stream, op, ep);
+        }
+        return hipGetLastError() == hipSuccess ? 0 : -1;
     }
     // Few weight row-groups: split K over 8 waves per workgroup to keep more loads in flight.
     const int64_t groups = (op.N + 15) / 16 * batches;
