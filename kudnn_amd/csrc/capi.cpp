@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <thread>
@@ -569,9 +570,93 @@ bool Vec4Ok(const void *p, int dt, const TensorSpec &t, bool needAlign16)
     return Aligned(p, align);
 }
 
+// Device workspace owned by a plan: packed operands and split-K partial tiles. It grows on demand (hipMalloc, which
+// happens on the first runs only) and is used in stream order. A run on another stream than the previous one first
+// waits for an event recorded after that run, so overlapping runs of one plan on several streams stay correct
+// (they are serialised on the workspace); runs on one stream add no wait. A copy of a plan gets its own workspace.
+class Workspace {
+public:
+    Workspace() = default;
+    Workspace(const Workspace &) {}
+    Workspace &operator=(const Workspace &) { return *this; }
+    ~Workspace()
+    {
+        if (ptr_ != nullptr) {
+            (void)hipFree(ptr_);  // waits for work that still uses it
+        }
+        if (done_ != nullptr) {
+            (void)hipEventDestroy(done_);
+        }
+    }
+
+    // Locks the workspace and returns at least `bytes` of device memory ordered after its previous use, or nullptr
+    // with `rc` set. Every successful Acquire is paired with one Release on the same stream.
+    void *Acquire(size_t bytes, hipStream_t stream, int &rc)
+    {
+        rc = KUDNN_STATUS_SUCCESS;
+        m_.lock();
+        if (bytes > bytes_) {
+            if (ptr_ != nullptr) {
+                (void)hipFree(ptr_);
+                ptr_ = nullptr;
+                bytes_ = 0;
+            }
+            const size_t want = (bytes + (size_t(2) << 20) - 1) / (size_t(2) << 20) * (size_t(2) << 20);
+            hipError_t e = hipMalloc(&ptr_, want);
+            if (e != hipSuccess) {
+                ptr_ = nullptr;
+                m_.unlock();
+                rc = Fail(KUDNN_STATUS_ALLOC_FAILED, std::string("workspace allocation failed: ") + hipGetErrorString(e));
+                return nullptr;
+            }
+            bytes_ = want;
+            used_ = false;  // fresh memory: nothing to wait for
+        }
+        if (done_ == nullptr) {
+            hipError_t e = hipEventCreateWithFlags(&done_, hipEventDisableTiming);
+            if (e != hipSuccess) {
+                done_ = nullptr;
+                m_.unlock();
+                rc = HipFail(e, "workspace event");
+                return nullptr;
+            }
+        }
+        if (used_ && last_ != stream) {
+            hipError_t e = hipStreamWaitEvent(stream, done_, 0);
+            if (e != hipSuccess) {
+                m_.unlock();
+                rc = HipFail(e, "workspace ordering");
+                return nullptr;
+            }
+        }
+        return ptr_;
+    }
+
+    void Release(hipStream_t stream)
+    {
+        if (hipEventRecord(done_, stream) == hipSuccess) {
+            last_ = stream;
+            used_ = true;
+        } else {
+            (void)hipGetLastError();
+            (void)hipDeviceSynchronize();  // no event: make the next user safe the slow way
+            used_ = false;
+        }
+        m_.unlock();
+    }
+
+private:
+    std::mutex m_;
+    void *ptr_ = nullptr;
+    size_t bytes_ = 0;
+    hipEvent_t done_ = nullptr;
+    hipStream_t last_ = nullptr;
+    bool used_ = false;
+};
+
 // Launches one GEMM core. Pointers are device pointers.
 int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const void *b, void *c, const void *bias,
-               const void *src, void *y, float alpha, float beta, float gamma, hipStream_t stream)
+               const void *src, void *y, float alpha, float beta, float gamma, Workspace &wsp, hipStream_t stream)
 {
     const int es = DtSize(core.computeDt);
     const bool packA = core.A.staticPack || !Aligned(a, 16);
@@ -583,15 +668,9 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
         int64_t copies = allBroadcast(o) ? 1 : batches;
         return copies * o.rows * core.kp * es;
     };
-    size_t wsA = packA ? static_cast<size_t>(packedBytes(core.A)) : 0;
-    size_t wsB = packB ? static_cast<size_t>(packedBytes(core.B)) : 0;
-    void *ws = nullptr;
-    if (wsA + wsB > 0) {
-        hipError_t e = hipMallocAsync(&ws, wsA + wsB, stream);
-        if (e != hipSuccess) {
-            return Fail(KUDNN_STATUS_ALLOC_FAILED, std::string("workspace allocation failed: ") + hipGetErrorString(e));
-        }
-    }
+    auto align256 = [](size_t v) { return (v + 255) / 256 * 256; };
+    size_t wsA = packA ? align256(static_cast<size_t>(packedBytes(core.A))) : 0;
+    size_t wsB = packB ? align256(static_cast<size_t>(packedBytes(core.B))) : 0;
 
     GemmOperands op{};
     op.M = core.M;
@@ -641,12 +720,39 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
         }
         return 0;
     };
+    // workspace: packed A, packed B, split-K partials of the 4-wave kernels
+    GemmOperands shape{};
+    shape.M = core.M;
+    shape.N = core.N;
+    shape.K = core.kp;
+    const bool mfma4 = core.engine == ENGINE_MFMA_F32 ||
+                       (core.engine == ENGINE_MFMA_BF16 && core.cfg != KUDNN_CFG_BF16_PINGPONG_256x256);
+    const size_t wsS = mfma4 ? align256(kudnn_gemm_workspace_bytes(shape, batches, core.cfg)) : 0;
+    void *ws = nullptr;
+    bool acquired = false;
+    if (wsA + wsB + wsS > 0) {
+        int arc = KUDNN_STATUS_SUCCESS;
+        ws = wsp.Acquire(wsA + wsB + wsS, stream, arc);
+        if (ws == nullptr) {
+            return arc;
+        }
+        acquired = true;
+    }
+    struct ReleaseGuard {
+        Workspace &w;
+        hipStream_t s;
+        bool on;
+        ~ReleaseGuard()
+        {
+            if (on) w.Release(s);
+        }
+    } guard{wsp, stream, acquired};
+    void *splitWs = wsS > 0 ? static_cast<char *>(ws) + wsA + wsB : nullptr;
     int rc = setupOperand(core.A, a, packA, ws, op.a, op.lda, op.a_bs);
     if (rc == 0) {
         rc = setupOperand(core.B, b, packB, static_cast<char *>(ws) + wsA, op.b, op.ldb, op.b_bs);
     }
     if (rc != 0) {
-        if (ws) (void)hipFreeAsync(ws, stream);
         return HipFail(hipGetLastError(), "pack launch");
     }
 
@@ -723,16 +829,14 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
             lrc = kudnn_launch_gemm_bf16_pingpong(op, ep, batches, stream);
         } else {
             // operands the ping-pong kernel cannot address (e.g. offsets beyond 2 GiB) use the 4-wave kernel
+            // (no split-K workspace was reserved for the ping-pong configuration: runs unsplit)
             const int cfg = core.cfg == KUDNN_CFG_BF16_PINGPONG_256x256 ? KUDNN_CFG_BF16_256x256 : core.cfg;
-            lrc = kudnn_launch_gemm_bf16(op, ep, batches, cfg, stream);
+            lrc = kudnn_launch_gemm_bf16(op, ep, batches, cfg, splitWs, stream);
         }
     } else {
-        lrc = kudnn_launch_gemm_f32(op, ep, batches, core.cfg, stream);
+        lrc = kudnn_launch_gemm_f32(op, ep, batches, core.cfg, splitWs, stream);
     }
     hipError_t le = hipGetLastError();
-    if (ws) {
-        (void)hipFreeAsync(ws, stream);
-    }
     if (lrc != 0 || le != hipSuccess) {
         return HipFail(le, "GEMM launch");
     }
@@ -742,10 +846,10 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
 // Runs a core, batch by batch in order when C is broadcast over a looped batch dim (the reference's
 // sequential batch loop, kudnn_gemm.cpp:783-807, then leaves the last batch's result).
 int RunCore(const GemmCore &core, const EpiExtras &x, const void *a, const void *b, void *c, const void *bias,
-            const void *src, void *y, float alpha, float beta, float gamma, hipStream_t stream)
+            const void *src, void *y, float alpha, float beta, float gamma, Workspace &wsp, hipStream_t stream)
 {
     if (!core.serial) {
-        return LaunchCore(core, x, a, b, c, bias, src, y, alpha, beta, gamma, stream);
+        return LaunchCore(core, x, a, b, c, bias, src, y, alpha, beta, gamma, wsp, stream);
     }
     GemmCore one = core;
     one.serial = false;
@@ -762,7 +866,7 @@ int RunCore(const GemmCore &core, const EpiExtras &x, const void *a, const void 
                 const char *pbias = core.hasBias ? static_cast<const char *>(bias) + off(core.Bias.bs, core.Bias.dt) : nullptr;
                 const char *psrc = x.hasSrc ? static_cast<const char *>(src) + off(x.Src.bs, x.Src.dt) : nullptr;
                 char *py = x.hasY ? static_cast<char *>(y) + off(x.Y.bs, x.Y.dt) : nullptr;
-                int rc = LaunchCore(one, x, pa, pb, pc, pbias, psrc, py, alpha, beta, gamma, stream);
+                int rc = LaunchCore(one, x, pa, pb, pc, pbias, psrc, py, alpha, beta, gamma, wsp, stream);
                 if (rc != KUDNN_STATUS_SUCCESS) {
                     return rc;
                 }
@@ -879,6 +983,7 @@ struct kudnn_gemm_plan : PlanBase {
     kudnn_gemm_plan() : PlanBase(PLAN_GEMM) {}
     kudnn_tensor_desc a{}, b{}, c{}, bias{};
     GemmCore core;
+    mutable Workspace ws;
 };
 
 struct kudnn_linear_act_plan : PlanBase {
@@ -886,6 +991,7 @@ struct kudnn_linear_act_plan : PlanBase {
     kudnn_tensor_desc a{}, b{}, c{}, bias{};
     GemmCore core;
     EpiExtras x;
+    mutable Workspace ws;
 };
 
 struct kudnn_linear_res_plan : PlanBase {
@@ -895,6 +1001,7 @@ struct kudnn_linear_res_plan : PlanBase {
     GemmCore core;
     GemmCore mul;   // RES_MUL: linearRes = C x res
     EpiExtras x;
+    mutable Workspace ws;
 };
 
 struct kudnn_linear_postops_plan : PlanBase {
@@ -902,6 +1009,7 @@ struct kudnn_linear_postops_plan : PlanBase {
     kudnn_tensor_desc a{}, b{}, y{}, bias{}, src{};
     GemmCore core;
     EpiExtras x;
+    mutable Workspace ws;
 };
 
 namespace {
@@ -1108,7 +1216,7 @@ int kudnn_gemm_run(kudnn_gemm_t plan, const void *a, const void *b, void *c, con
     if (rc == 0) rc = stg.Add(bias, plan->core.hasBias ? DescExtentBytes(plan->bias) : 0, true, false, &dbias);
     if (rc == 0) {
         EpiExtras x;
-        rc = RunCore(core, x, da, db, dc, dbias, nullptr, nullptr, alpha, beta, 0.0f, st);
+        rc = RunCore(core, x, da, db, dc, dbias, nullptr, nullptr, alpha, beta, 0.0f, plan->ws, st);
     }
     return stg.Finish(rc);
 }
@@ -1210,7 +1318,7 @@ int kudnn_linear_act_run(kudnn_linear_act_t plan, const void *a, const void *b, 
     if (rc == 0) rc = stg.Add(c, DescExtentBytes(plan->c), false, true, &dc);
     if (rc == 0) rc = stg.Add(bias, plan->core.hasBias ? DescExtentBytes(plan->bias) : 0, true, false, &dbias);
     if (rc == 0) {
-        rc = RunCore(plan->core, plan->x, da, db, dc, dbias, nullptr, nullptr, 1.0f, 0.0f, 0.0f, st);
+        rc = RunCore(plan->core, plan->x, da, db, dc, dbias, nullptr, nullptr, 1.0f, 0.0f, 0.0f, plan->ws, st);
     }
     return stg.Finish(rc);
 }
@@ -1348,13 +1456,13 @@ int kudnn_linear_res_run(kudnn_linear_res_t plan, const void *a, const void *b, 
     if (rc == 0) {
         if (mul) {
             EpiExtras none;
-            rc = RunCore(plan->core, none, da, db, dc, dbias, nullptr, nullptr, 1.0f, 0.0f, 0.0f, st);
+            rc = RunCore(plan->core, none, da, db, dc, dbias, nullptr, nullptr, 1.0f, 0.0f, 0.0f, plan->ws, st);
             if (rc == 0) {
                 float one = 1.0f, zero = 0.0f;
-                rc = RunCore(plan->mul, none, dc, dres, dlr, nullptr, nullptr, nullptr, one, zero, 0.0f, st);
+                rc = RunCore(plan->mul, none, dc, dres, dlr, nullptr, nullptr, nullptr, one, zero, 0.0f, plan->ws, st);
             }
         } else {
-            rc = RunCore(plan->core, plan->x, da, db, dc, dbias, dres, dlr, 1.0f, 0.0f, gamma, st);
+            rc = RunCore(plan->core, plan->x, da, db, dc, dbias, dres, dlr, 1.0f, 0.0f, gamma, plan->ws, st);
         }
     }
     return stg.Finish(rc);
@@ -1462,7 +1570,7 @@ int kudnn_linear_postops_run(kudnn_linear_postops_t plan, const void *a, const v
     if (rc == 0) rc = stg.Add(bias, plan->core.hasBias ? DescExtentBytes(plan->bias) : 0, true, false, &dbias);
     if (rc == 0) rc = stg.Add(src, plan->x.hasSrc ? DescExtentBytes(plan->src) : 0, true, false, &dsrc);
     if (rc == 0) {
-        rc = RunCore(plan->core, plan->x, da, db, dy, dbias, dsrc, nullptr, 1.0f, 0.0f, gamma, st);
+        rc = RunCore(plan->core, plan->x, da, db, dy, dbias, dsrc, nullptr, 1.0f, 0.0f, gamma, plan->ws, st);
     }
     return stg.Finish(rc);
 }

@@ -7,8 +7,9 @@
 //
 // Design (one workgroup of 4 waves per BM x BN output tile, waves arranged 2 x 2):
 //  - k-tiles of 128 bytes per row (64 bf16 / 32 fp32) go straight from global memory into LDS with
-//    gfx950's global_load_lds_dwordx4 (no staging registers), double buffered: the loads of tile k+1 are
-//    issued right after the barrier that opens tile k and land while tile k's MFMAs run.
+//    gfx950's global_load_lds_dwordx4 (no staging registers) through an ST-stage ring: the loads of tile k+ST-1
+//    are issued right after the barrier that opens tile k (ST = 2 for 256 x 256, up to 4 where the tiles are
+//    small enough, so that a small grid is not bound by one memory latency per k-tile).
 //  - A wave's LDS DMA instruction fills 8 rows x 128 bytes; lane l writes 16-byte slot l, and fetches the
 //    global chunk that the XOR swizzle (chunk ^ (row & 7)) assigns to that slot, so the ds_read_b128 of
 //    32 consecutive rows at one logical k-chunk hits every bank once.
@@ -21,8 +22,15 @@
 //    back row-major so each lane applies bias / activation / residual to 8 consecutive columns and
 //    writes them with one 16-byte store (a wave writes 16 rows x 64 contiguous bytes per instruction).
 //  - Blocks are remapped so consecutive tiles run on the same XCD and walked in groups of tile-rows.
+//  - The activation and the epilogue's tensor types are template arguments (see the forms in device_common.h):
+//    full tiles in the bf16 / f32 forms run short straight-line code; other tiles and the generic form go one
+//    element at a time.
+//  - Split-K for grids too small to fill the chip: grid.z splits the k-tiles, each split writes its raw f32 partial
+//    tile to a workspace (form EPI_FORM_PARTIAL), and splitk_reduce_kernel sums the splits in split order (the same
+//    bits on every run) and applies the epilogue.
 // Requirements (the dispatcher packs operands otherwise): K a multiple of the k-tile, rows 16-byte
 // aligned. Rows past M / N are clamped (read but never stored).
+#include <algorithm>
 #include <type_traits>
 #include <utility>
 
@@ -40,11 +48,35 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kChunks = 8;   // 16-byte chunks per 128-byte LDS row
 constexpr int kStagePitch = 36;  // epilogue staging row pitch in floats (32 columns + 4 pad)
-// s_waitcnt immediate for vmcnt(0) with expcnt/lgkmcnt left unconstrained (gfx9 encoding: vmcnt[3:0] and
-// [15:14], expcnt[6:4], lgkmcnt[11:8]).
-constexpr int kWaitVmcnt0 = 0x0F70;
 
 __device__ __forceinline__ int swz(int row, int chunk) { return (chunk ^ (row & 7)); }
+
+// s_waitcnt vmcnt(N) with N a compile-time constant (expcnt / lgkmcnt unconstrained).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// Waits until at most `ahead` tiles of PER DMA instructions each are outstanding (ahead < ST - 1).
+template <int PER, int ST>
+__device__ __forceinline__ void wait_tiles(int ahead)
+{
+    if constexpr (ST >= 4) {
+        if (ahead >= 2) {
+            wait_vmcnt<2 * PER>();
+            return;
+        }
+    }
+    if constexpr (ST >= 3) {
+        if (ahead >= 1) {
+            wait_vmcnt<PER>();
+            return;
+        }
+    }
+    wait_vmcnt<0>();
+}
 
 // Calls f(std::integral_constant<int, I>) for I = 0 .. N-1 (a loop whose index is a compile-time constant).
 template <int... I, typename F>
@@ -58,9 +90,12 @@ __device__ __forceinline__ void static_for(F &&f)
     static_for_impl(std::make_integer_sequence<int, N>{}, f);
 }
 
-template <bool F32, int BM, int BN, int WM, int WN>
+// Raw f32 partial tiles of a split-K launch: split z of output (m, n) at partial[z * M * N + m * N + n].
+constexpr int EPI_FORM_PARTIAL = 3;
+
+template <bool F32, int BM, int BN, int WM, int WN, int ST, int ACT, int FORM>
 __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands op, EpiParams ep, int tilesM,
-                                                                  int tilesN, int group)
+                                                                  int tilesN, int group, float *partial)
 {
     using T = typename std::conditional<F32, float, uint16_t>::type;
     constexpr int EPC = 16 / static_cast<int>(sizeof(T));  // elements per 16-byte chunk
@@ -73,12 +108,12 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
     constexpr int GA = BM / 8 / NW;  // 8-row LDS DMA groups per wave per A tile
     constexpr int GB = BN / 8 / NW;
     static_assert(GA >= 1 && GB >= 1, "tile too small for the wave count");
-    static_assert(NW * TM * kStagePitch * 4 <= (BM + BN) * kChunks * 16 * 2, "epilogue staging exceeds LDS");
+    static_assert(NW * TM * kStagePitch * 4 <= (BM + BN) * kChunks * 16 * ST, "epilogue staging exceeds LDS");
 
-    // one LDS array: two A stages, then two B stages; reused as epilogue staging after the k-loop
-    __shared__ uint4 lds[2 * (BM + BN) * kChunks];
+    // one LDS array: ST A stages, then ST B stages; reused as epilogue staging after the k-loop
+    __shared__ uint4 lds[ST * (BM + BN) * kChunks];
     uint4(*sA)[BM * kChunks] = reinterpret_cast<uint4(*)[BM * kChunks]>(lds);
-    uint4(*sB)[BN * kChunks] = reinterpret_cast<uint4(*)[BN * kChunks]>(lds + 2 * BM * kChunks);
+    uint4(*sB)[BN * kChunks] = reinterpret_cast<uint4(*)[BN * kChunks]>(lds + ST * BM * kChunks);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -143,17 +178,30 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
 
     const int lrow = lane & 31;
     const int lhalf = lane >> 5;
-    const int KT = static_cast<int>(K / kBK);
+    // k-tiles of this launch: all of them, or split z's share of a split-K launch
+    const int KTall = static_cast<int>(K / kBK);
+    const int kt0 = static_cast<int>(static_cast<int64_t>(KTall) * blockIdx.z / gridDim.z);
+    const int kt1 = static_cast<int>(static_cast<int64_t>(KTall) * (blockIdx.z + 1) / gridDim.z);
+    const int KT = kt1 - kt0;
 
-    issue_tile(0, 0);
+    // ST-stage pipeline: tiles kt+1 .. kt+ST-1 are in flight while tile kt is computed. Each tile is GA + GB
+    // DMA instructions per wave and they complete in order, so "tile kt landed" is vmcnt <= (tiles issued after
+    // it) * (GA + GB).
+#pragma unroll
+    for (int s = 0; s < ST - 1; ++s) {
+        if (s < KT) {
+            issue_tile(s, static_cast<int64_t>(kt0 + s) * kBK);
+        }
+    }
     for (int kt = 0; kt < KT; ++kt) {
-        const int cur = kt & 1;
-        // Wait for this thread's DMA of tile kt (vmcnt(0)); the barrier then makes every wave's tile kt
-        // visible and guarantees every wave finished reading buffer cur ^ 1 (tile kt - 1).
-        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        const int cur = kt % ST;
+        const int ahead = KT - 1 - kt < ST - 2 ? KT - 1 - kt : ST - 2;  // tiles issued after tile kt so far
+        wait_tiles<GA + GB, ST>(ahead);
+        // the barrier makes every wave's tile kt visible and guarantees every wave finished reading the buffer
+        // of tile kt - 1, which the issue below refills
         __syncthreads();
-        if (kt + 1 < KT) {
-            issue_tile(cur ^ 1, static_cast<int64_t>(kt + 1) * kBK);
+        if (kt + ST - 1 < KT) {
+            issue_tile((kt + ST - 1) % ST, static_cast<int64_t>(kt0 + kt + ST - 1) * kBK);
         }
         uint4 va[2][FM], vb[2][FN];
         auto read_frags = [&](int slot, int s) {
@@ -208,9 +256,12 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
     }
 
     // Epilogue through LDS, one 32-column strip of each wave tile at a time. The strip index is a
-    // compile-time constant (static_for) so the accumulators stay in registers.
+    // compile-time constant (static_for) so the accumulators stay in registers. Lanes then read the strip
+    // back row-major: 4 lanes per row, 8 columns per lane, 16 rows per pass.
     float *stage = reinterpret_cast<float *>(lds) + wave * (TM * kStagePitch);
     const EpiBatch ob = epi_batch_offsets(ep, batch);
+    const bool full = m0 + BM <= M && n0 + BN <= N;
+    const int col8 = (lane & 3) * 8;
     static_for<FN>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
         __syncthreads();  // previous strip fully read back (and, for j = 0, the k-loop's last LDS reads done)
@@ -224,54 +275,189 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
             }
         }
         __syncthreads();
-        // row-major read back: 4 lanes per row, 8 columns per lane, 16 rows per pass
-        const int col8 = (lane & 3) * 8;
-        for (int r = lane >> 2; r < TM; r += 16) {
-            const int64_t m = m0 + wm * TM + r;
-            const int64_t n = n0 + wn * TN + j * 32 + col8;
-            if (m < M && n < N) {
+        const int64_t n = n0 + wn * TN + j * 32 + col8;
+        if constexpr (FORM == EPI_FORM_PARTIAL) {
+            float *part = partial + static_cast<int64_t>(blockIdx.z) * M * N;
+#pragma unroll 1
+            for (int r = lane >> 2; r < TM; r += 16) {
+                const int64_t m = m0 + wm * TM + r;
+                if (m >= M) {
+                    continue;
+                }
                 const float *src = stage + r * kStagePitch + col8;
-                const float4 lo = *reinterpret_cast<const float4 *>(src);
-                const float4 hi = *reinterpret_cast<const float4 *>(src + 4);
-                const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-                epi_apply8(ep, ob, m, n, N, v);
+#pragma unroll 1
+                for (int q = 0; q < 8; ++q) {
+                    if (n + q < N) {
+                        part[m * N + n + q] = src[q];
+                    }
+                }
+            }
+        } else if constexpr (FORM == EPI_FORM_GENERIC) {
+#pragma unroll 1
+            for (int r = lane >> 2; r < TM; r += 16) {
+                const int64_t m = m0 + wm * TM + r;
+                if (m >= M) {
+                    continue;
+                }
+                const float *src = stage + r * kStagePitch + col8;
+#pragma unroll 1
+                for (int q = 0; q < 8; ++q) {
+                    if (n + q < N) {
+                        epi_apply(ep, ob, m, n + q, src[q]);
+                    }
+                }
+            }
+        } else {
+#pragma unroll 1
+            for (int r = lane >> 2; r < TM; r += 16) {
+                const int64_t m = m0 + wm * TM + r;
+                const float *src = stage + r * kStagePitch + col8;
+                if (full || (m < M && n + 7 < N)) {
+                    const Pre8 pre = epi_prefetch8<FORM>(ep, ob, m, n);
+                    const float4 lo = *reinterpret_cast<const float4 *>(src);
+                    const float4 hi = *reinterpret_cast<const float4 *>(src + 4);
+                    const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                    epi_fast8<ACT, FORM>(ep, ob, m, n, v, pre);
+                } else if (m < M) {
+#pragma unroll 1
+                    for (int q = 0; q < 8; ++q) {
+                        if (n + q < N) {
+                            epi_elem<ACT, FORM>(ep, ob, m, n + q, src[q]);
+                        }
+                    }
+                }
             }
         }
     });
 }
 
-template <bool F32, int BM, int BN, int WM, int WN>
-int launch_cfg(const GemmOperands &op, const EpiParams &ep, int64_t batches, int group, hipStream_t stream)
+// Split-K reduction: y[m, n] = epilogue(sum over splits z = 0, 1, ... of partial[z][m][n]), four consecutive
+// columns of one row per thread; the sum runs in split order, so the result does not depend on timing.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *partial, int splits, int64_t M, int64_t N,
+                                                            EpiParams ep)
+{
+    const int64_t n4 = (N + 3) / 4;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= M * n4) {
+        return;
+    }
+    const int64_t m = idx / n4;
+    const int64_t n = (idx - m * n4) * 4;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (N % 4 == 0) {  // 16-byte aligned rows (the workspace base is 256-byte aligned)
+        for (int z = 0; z < splits; ++z) {
+            const float4 t = *reinterpret_cast<const float4 *>(partial + (static_cast<int64_t>(z) * M + m) * N + n);
+            v[0] += t.x;
+            v[1] += t.y;
+            v[2] += t.z;
+            v[3] += t.w;
+        }
+    } else {
+        for (int z = 0; z < splits; ++z) {
+            const float *src = partial + (static_cast<int64_t>(z) * M + m) * N + n;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (n + q < N) {
+                    v[q] += src[q];
+                }
+            }
+        }
+    }
+    const EpiBatch ob = epi_batch_offsets(ep, 0);
+    epi_apply4(ep, ob, m, n, N, v);
+}
+
+// Split-K factor of a launch: the tiles cover less than half of the 256 CUs and each split keeps at least 4 k-tiles.
+int splitk_splits(const GemmOperands &op, int64_t batches, int BM, int BN, int kBK)
+{
+    const int64_t tiles = ((op.M + BM - 1) / BM) * ((op.N + BN - 1) / BN) * batches;
+    const int64_t KT = op.K / kBK;
+    if (batches != 1 || tiles >= 128 || KT < 8) {
+        return 1;
+    }
+    return static_cast<int>(std::min<int64_t>(KT / 4, (384 + tiles - 1) / tiles));
+}
+
+template <bool F32, int BM, int BN, int WM, int WN, int ST>
+int launch_cfg(const GemmOperands &op, const EpiParams &ep, int64_t batches, int group, void *ws, hipStream_t stream)
 {
     constexpr int kBK = F32 ? 32 : 64;
     if (op.K % kBK != 0) {
         return -1;  // the dispatcher pads K by packing
     }
-    int tilesM = static_cast<int>((op.M + BM - 1) / BM);
-    int tilesN = static_cast<int>((op.N + BN - 1) / BN);
-    dim3 grid(static_cast<unsigned>(tilesM * tilesN), static_cast<unsigned>(batches));
+    const int tilesM = static_cast<int>((op.M + BM - 1) / BM);
+    const int tilesN = static_cast<int>((op.N + BN - 1) / BN);
     dim3 block(WM * WN * 64);
-    hipLaunchKernelGGL((gemm_mfma_kernel<F32, BM, BN, WM, WN>), grid, block, 0, stream, op, ep, tilesM, tilesN, group);
+
+    const int splits = ws != nullptr ? splitk_splits(op, batches, BM, BN, kBK) : 1;
+    if (splits > 1) {
+        float *partial = static_cast<float *>(ws);
+        dim3 grid(static_cast<unsigned>(tilesM * tilesN), 1, static_cast<unsigned>(splits));
+        hipLaunchKernelGGL((gemm_mfma_kernel<F32, BM, BN, WM, WN, ST, 0, EPI_FORM_PARTIAL>), grid, block, 0, stream, op, ep,
+                           tilesM, tilesN, group, partial);
+        const int64_t threads = op.M * ((op.N + 3) / 4);
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, stream,
+                           partial, splits, op.M, op.N, ep);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
+
+    // the activation and the epilogue's tensor types select one of the compiled variants
+    decltype(&gemm_mfma_kernel<F32, BM, BN, WM, WN, ST, 0, EPI_FORM_GENERIC>) kernel = nullptr;
+    constexpr int kForm = F32 ? EPI_FORM_F32 : EPI_FORM_BF16;  // the fixed form compiled for this compute type
+    if (epi_form(ep) == kForm) {
+        switch (ep.act) {
+            case KUDNN_ACT_UNIMPLEMENTED: kernel = gemm_mfma_kernel<F32, BM, BN, WM, WN, ST, KUDNN_ACT_UNIMPLEMENTED, kForm>; break;
+            case KUDNN_ACT_RELU: kernel = gemm_mfma_kernel<F32, BM, BN, WM, WN, ST, KUDNN_ACT_RELU, kForm>; break;
+            case KUDNN_ACT_SWISH: kernel = gemm_mfma_kernel<F32, BM, BN, WM, WN, ST, KUDNN_ACT_SWISH, kForm>; break;
+            case KUDNN_ACT_GELU_TANH: kernel = gemm_mfma_kernel<F32, BM, BN, WM, WN, ST, KUDNN_ACT_GELU_TANH, kForm>; break;
+            case KUDNN_ACT_GELU_ERF: kernel = gemm_mfma_kernel<F32, BM, BN, WM, WN, ST, KUDNN_ACT_GELU_ERF, kForm>; break;
+            default: break;
+        }
+    }
+    if (kernel == nullptr) {
+        kernel = gemm_mfma_kernel<F32, BM, BN, WM, WN, ST, 0, EPI_FORM_GENERIC>;  // reads the activation at run time
+    }
+    dim3 grid(static_cast<unsigned>(tilesM * tilesN), static_cast<unsigned>(batches));
+    hipLaunchKernelGGL(kernel, grid, block, 0, stream, op, ep, tilesM, tilesN, group, static_cast<float *>(nullptr));
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 }  // namespace
 
-int kudnn_launch_gemm_bf16(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, hipStream_t stream)
+size_t kudnn_gemm_workspace_bytes(const GemmOperands &op, int64_t batches, int cfg)
+{
+    int bm = 0, bn = 0, bk = 0;
+    switch (cfg) {
+        case KUDNN_CFG_BF16_256x256: bm = 256; bn = 256; bk = 64; break;
+        case KUDNN_CFG_BF16_256x128: bm = 256; bn = 128; bk = 64; break;
+        case KUDNN_CFG_BF16_128x128: bm = 128; bn = 128; bk = 64; break;
+        case KUDNN_CFG_F32_128x128: bm = 128; bn = 128; bk = 32; break;
+        case KUDNN_CFG_F32_64x64: bm = 64; bn = 64; bk = 32; break;
+        default: return 0;
+    }
+    const int splits = splitk_splits(op, batches, bm, bn, bk);
+    return splits > 1 ? static_cast<size_t>(splits) * op.M * op.N * sizeof(float) : 0;
+}
+
+int kudnn_launch_gemm_bf16(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, void *ws,
+                           hipStream_t stream)
 {
     switch (cfg) {
-        case KUDNN_CFG_BF16_256x256: return launch_cfg<false, 256, 256, 2, 2>(op, ep, batches, 8, stream);
-        case KUDNN_CFG_BF16_256x128: return launch_cfg<false, 256, 128, 2, 2>(op, ep, batches, 8, stream);
-        case KUDNN_CFG_BF16_128x128: return launch_cfg<false, 128, 128, 2, 2>(op, ep, batches, 8, stream);
+        case KUDNN_CFG_BF16_256x256: return launch_cfg<false, 256, 256, 2, 2, 2>(op, ep, batches, 8, ws, stream);
+        case KUDNN_CFG_BF16_256x128: return launch_cfg<false, 256, 128, 2, 2, 3>(op, ep, batches, 8, ws, stream);
+        case KUDNN_CFG_BF16_128x128: return launch_cfg<false, 128, 128, 2, 2, 4>(op, ep, batches, 8, ws, stream);
         default: return -1;
     }
 }
 
-int kudnn_launch_gemm_f32(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, hipStream_t stream)
+int kudnn_launch_gemm_f32(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, void *ws,
+                          hipStream_t stream)
 {
     switch (cfg) {
-        case KUDNN_CFG_F32_128x128: return launch_cfg<true, 128, 128, 2, 2>(op, ep, batches, 8, stream);
-        case KUDNN_CFG_F32_64x64: return launch_cfg<true, 64, 64, 2, 2>(op, ep, batches, 8, stream);
+        // 128 x 128 serves grids of >= 256 tiles: two stages keep two workgroups per CU, which hides latency better
+        // than a deeper ring at one workgroup per CU
+        case KUDNN_CFG_F32_128x128: return launch_cfg<true, 128, 128, 2, 2, 2>(op, ep, batches, 8, ws, stream);
+        case KUDNN_CFG_F32_64x64: return launch_cfg<true, 64, 64, 2, 2, 4>(op, ep, batches, 8, ws, stream);
         default: return -1;
     }
 }

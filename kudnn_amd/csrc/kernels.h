@@ -19,12 +19,17 @@ enum {
 };
 
 // Returns 0 on success, -1 if the launch failed or cfg is unknown.
-int kudnn_launch_gemm_bf16(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, hipStream_t stream);
+// 4-wave MFMA kernels (gemm_mfma.hip). A grid too small for the chip is split along K when `ws` (device memory of at
+// least kudnn_gemm_workspace_bytes bytes, 256-byte aligned) is given; with ws == nullptr it runs unsplit.
+size_t kudnn_gemm_workspace_bytes(const GemmOperands &op, int64_t batches, int cfg);
+int kudnn_launch_gemm_bf16(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, void *ws,
+                           hipStream_t stream);
 // 8-wave ping-pong schedule, 256x256 tile (gemm_pingpong.hip). Needs K a multiple of 64, 16-byte aligned rows and
 // 32-bit operand offsets; kudnn_pingpong_eligible says whether `op` qualifies.
 bool kudnn_pingpong_eligible(const GemmOperands &op);
 int kudnn_launch_gemm_bf16_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream);
-int kudnn_launch_gemm_f32(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, hipStream_t stream);
+int kudnn_launch_gemm_f32(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, void *ws,
+                          hipStream_t stream);
 // M <= 16, bf16 operands, B contiguous along K (M == 1: row-per-wave GEMV, otherwise 16-row MFMA tiles).
 int kudnn_launch_skinny_bf16(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream);
 

@@ -269,6 +269,56 @@ def test_m1_row_gemv_batched_broadcast_weight():
     compare(from_device(dc, O.BF16), ref.buf, O.BF16, plan.describe())
 
 
+@pytest.mark.parametrize("dt", [O.F32, O.BF16])
+@pytest.mark.parametrize("mnk", [(128, 1024, 1024), (100, 200, 2048), (64, 70, 512)])
+@pytest.mark.parametrize("post", ["gelu_add", "swish_mul", "gemm_beta"])
+def test_split_k_small_grids(dt, mnk, post):
+    # grids of fewer than 128 tiles with at least 8 k-tiles run split along K: raw f32 partials in the plan's
+    # workspace, then one pass that sums them in split order and applies the whole epilogue
+    M, N, Kd = mnk
+    x = Case([M, Kd], dt, seed=220, dist="normal", lo=0.0, hi=1.0)
+    w = Case([Kd, N], dt, "BA", seed=221, dist="normal", lo=0.0, hi=1.0 / 32)
+    b = Case([1, N], dt, seed=222, lo=-0.2, hi=0.2)
+    y = Case([M, N], dt, seed=223, lo=-1.0, hi=1.0) if post == "gemm_beta" else Case([M, N], dt, zero=True)
+    dy = torch.from_numpy(y.t.buf.view(np.int16).copy() if dt != O.F32 else y.t.buf.copy()).cuda()
+    ref = O.Tensor(y.t.dims, y.t.strides, dt, y.t.buf.copy())
+    if post == "gemm_beta":
+        plan = K.Gemm(x.desc, w.desc, y.desc, b.desc)
+        plan.run(x.device(), w.device(), dy, b.device(), alpha=0.5, beta=0.25)
+        O.gemm(x.t, w.t, ref, b.t, 0.5, 0.25)
+    else:
+        act, binary = (O.ACT_GELU_TANH, O.BIN_ADD) if post == "gelu_add" else (O.ACT_SWISH, O.BIN_MUL)
+        s = Case([M, N], dt, seed=224, lo=0.5, hi=1.5)
+        plan = K.LinearPostOps(x.desc, w.desc, y.desc, b.desc, act=act, act_alpha=1.0, binary=binary, src=s.desc)
+        plan.run(x.device(), w.device(), dy, b.device(), s.device())
+        O.linear_postops(x.t, w.t, ref, b.t, act, 1.0, binary, s.t)
+    torch.cuda.synchronize()
+    compare(from_device(dy, dt), ref.buf, dt, f"split-K {post} {plan.describe()}")
+
+
+def test_plan_workspace_across_streams():
+    # one plan with a workspace (split-K) run alternately on two streams: the workspace is ordered between them
+    M, N, Kd = 128, 1024, 1024
+    dt = O.F32
+    xs = [Case([M, Kd], dt, seed=230 + i, dist="normal", lo=0.0, hi=1.0) for i in range(4)]
+    w = Case([Kd, N], dt, "BA", seed=240, dist="normal", lo=0.0, hi=1.0 / 32)
+    y = Case([M, N], dt, zero=True)
+    plan = K.LinearActivation(xs[0].desc, w.desc, y.desc, None, 0.0, 0.0, K.ACT_RELU)
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    dw = w.device()
+    dxs = [x.device() for x in xs]
+    outs = [zeros_device(y) for _ in xs]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for i, (dx, dout) in enumerate(zip(dxs, outs)):
+            plan.run(dx, dw, dout, None, stream=streams[i % 2])
+    torch.cuda.synchronize()
+    for x, dout in zip(xs, outs):
+        ref = y.clone_empty()
+        O.linear_act(x.t, w.t, ref, None, O.ACT_RELU, 0.0)
+        compare(from_device(dout, dt), ref.buf, dt, f"two streams {plan.describe()}")
+
+
 def test_c5_bf16_3d_silu_kmajor_rows():
     B, S, Kd, N = 8, 2048, 5120, 13824
     x = Case([B, S, Kd], O.BF16, "ABC", seed=0, dist="normal", lo=0.0, hi=1.0)
