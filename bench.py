@@ -53,6 +53,49 @@ def parse():
     return p.parse_args()
 
 
+# ---------------------------------------------------------------------------------------------------
+# synthetic inputs: SplitMix64 (Vigna) per tensor, seed = config seed 0 + stream offset (X 0, W 1, bias 2,
+# R / M2 3); uniform from the top 53 bits, normal by Box-Muller over two consecutive draws; a bf16 tensor is the
+# RNE of the f32 sample. The k-th draw of a stream is mix(seed + k * golden gamma), so a whole tensor is generated on
+# the device in one pass of int64 arithmetic (wrapping multiplication, masked shifts for the logical right shift).
+
+_GAMMA = 0x9E3779B97F4A7C15
+_MUL1 = 0xBF58476D1CE4E5B9
+_MUL2 = 0x94D049BB133111EB
+
+
+def _i64(c):
+    return c - (1 << 64) if c >= (1 << 63) else c
+
+
+def _u01(torch, first, n, seed, dev):
+    k = torch.arange(first, first + n, device=dev, dtype=torch.int64)
+    z = k * _i64(_GAMMA) + _i64(seed % (1 << 64))
+    z = (z ^ ((z >> 30) & ((1 << 34) - 1))) * _i64(_MUL1)
+    z = (z ^ ((z >> 27) & ((1 << 37) - 1))) * _i64(_MUL2)
+    z = z ^ ((z >> 31) & ((1 << 33) - 1))
+    return ((z >> 11) & ((1 << 53) - 1)).to(torch.float64) * (1.0 / 9007199254740992.0)
+
+
+def synth(torch, shape, seed, dist, a, b, dtype, dev="cuda", chunk=1 << 24):
+    """Tensor of `shape`: dist "uniform" on [a, b) or "normal" with mean a and standard deviation b. Generated in
+    pieces of `chunk` elements, which bounds the int64 / float64 temporaries."""
+    n = 1
+    for d in shape:
+        n *= d
+    out = torch.empty(n, device=dev, dtype=torch.float32)
+    for c0 in range(0, n, chunk):
+        m = min(chunk, n - c0)
+        if dist == "uniform":
+            v = a + (b - a) * _u01(torch, c0 + 1, m, seed, dev)
+        else:
+            u = _u01(torch, 2 * c0 + 1, 2 * m, seed, dev).view(m, 2)
+            u1 = torch.clamp(u[:, 0], min=1e-300)
+            v = a + b * torch.sqrt(-2.0 * torch.log(u1)) * torch.cos(6.283185307179586 * u[:, 1])
+        out[c0:c0 + m] = v.to(torch.float32)
+    return out.view(*shape).to(dtype)
+
+
 def time_launches(fn, steps, warmup, torch, stream, prewarm_ms=0.0):
     t_end = time.perf_counter() + prewarm_ms * 1e-3
     while time.perf_counter() < t_end:
@@ -77,13 +120,12 @@ def time_launches(fn, steps, warmup, torch, stream, prewarm_ms=0.0):
 def bench_c3(args, torch, K):
     M, Kd, N = 4096, 4096, 11008
     dev = "cuda"
-    g = torch.Generator(device=dev)
-    g.manual_seed(0)
-    x = torch.randn(M, Kd, device=dev, generator=g).to(torch.bfloat16)
-    w = (torch.randn(N, Kd, device=dev, generator=g) * 0.02).to(torch.bfloat16)  # nn.Linear weight [N][K]
-    bias = torch.zeros(1, N, device=dev, dtype=torch.bfloat16)
-    r = torch.randn(M, N, device=dev, generator=g).to(torch.bfloat16)
-    y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+    bf = torch.bfloat16
+    x = synth(torch, (M, Kd), 0, "normal", 0.0, 1.0, bf)
+    w = synth(torch, (N, Kd), 1, "normal", 0.0, 0.02, bf)  # nn.Linear weight [N][K]
+    bias = torch.zeros(1, N, device=dev, dtype=bf)
+    r = synth(torch, (M, N), 3, "normal", 0.0, 1.0, bf)
+    y = torch.empty(M, N, device=dev, dtype=bf)
 
     dx = K.desc([M, Kd], K.BF16, "AB")
     dw = K.desc([Kd, N], K.BF16, "BA")  # logical [K,N], physical [N][K]
@@ -114,11 +156,11 @@ def bench_decode(args, torch, K, N, M=1):
     dev = "cuda"
     wbytes = N * Kd * 2
     copies = max(2, -(-512 * 2**20 // wbytes))  # >= 512 MB of distinct weights
-    g = torch.Generator(device=dev)
-    g.manual_seed(1)
-    ws = [(torch.randn(N, Kd, device=dev, generator=g) * 0.02).to(torch.bfloat16) for _ in range(copies)]
-    x = torch.randn(M, Kd, device=dev, generator=g).to(torch.bfloat16)
-    m2 = (torch.rand(M, N, device=dev, generator=g) + 0.5).to(torch.bfloat16)
+    bf = torch.bfloat16
+    # copy c of the weight is stream 1 + 16 * c, so the copies differ and copy 0 is the config's W
+    ws = [synth(torch, (N, Kd), 1 + 16 * c, "normal", 0.0, 0.02, bf) for c in range(copies)]
+    x = synth(torch, (M, Kd), 0, "normal", 0.0, 1.0, bf)
+    m2 = synth(torch, (M, N), 3, "uniform", 0.5, 1.5, bf)
     y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
     plan = K.LinearPostOps(K.desc([M, Kd], K.BF16), K.desc([Kd, N], K.BF16, "BA"), K.desc([M, N], K.BF16),
                            binary=K.BIN_MUL, src=K.desc([M, N], K.BF16))
@@ -141,24 +183,26 @@ def bench_config(args, torch, K, name):
     C2's inputs are rotated over 4 copies (>= 512 MB) so that the Infinity Cache does not hold them; C1's 5 MB working
     set is cache-resident whatever is done, and C5's 760 MB footprint exceeds the cache by itself."""
     dev = "cuda"
-    g = torch.Generator(device=dev)
-    g.manual_seed(2)
     if name == "C1":
         M, Kd, N, dt, kind, alpha, copies = 128, 1024, 1024, torch.float32, K.ACT_RELU, 0.0, 1
+        xd, wd, bd = ("uniform", -1.0, 1.0), ("uniform", -1.0, 1.0), ("uniform", -0.1, 0.1)
     elif name == "C2":
         M, Kd, N, dt, kind, alpha, copies = 2048, 4096, 4096, torch.float32, K.ACT_SWISH, 1.0, 4
+        xd, wd, bd = ("normal", 0.0, 1.0), ("normal", 0.0, 1.0 / 64), ("normal", 0.0, 0.02)
     else:
         M, Kd, N, dt, kind, alpha, copies = 16384, 5120, 13824, torch.bfloat16, K.ACT_SWISH, 1.0, 1
+        xd, wd, bd = ("normal", 0.0, 1.0), ("normal", 0.0, 0.014), ("normal", 0.0, 0.02)
     kdt = K.F32 if dt == torch.float32 else K.BF16
-    xs = [torch.randn(M, Kd, device=dev, generator=g).to(dt) for _ in range(copies)]
+    # copy c of an input is its stream + 16 * c (copy 0 is the config's tensor)
+    xs = [synth(torch, (M, Kd), 0 + 16 * c, *xd, dt) for c in range(copies)]
     if name == "C5":  # W{1,5120,13824} ABC: K-major [K][N], broadcast over the batch of 8
-        ws = [(torch.randn(Kd, N, device=dev, generator=g) * 0.014).to(dt)]
+        ws = [synth(torch, (Kd, N), 1, *wd, dt)]
         da, db, dc = K.desc([8, 2048, Kd], kdt, "ABC"), K.desc([1, Kd, N], kdt, "ABC"), K.desc([8, 2048, N], kdt, "ABC")
         dbias = K.desc([1, 1, N], kdt, "ABC")
     else:  # nn.Linear weight [N][K] (logical [K,N], layout BA)
-        ws = [(torch.randn(N, Kd, device=dev, generator=g) * (1.0 / 64)).to(dt) for _ in range(copies)]
+        ws = [synth(torch, (N, Kd), 1 + 16 * c, *wd, dt) for c in range(copies)]
         da, db, dc, dbias = K.desc([M, Kd], kdt), K.desc([Kd, N], kdt, "BA"), K.desc([M, N], kdt), K.desc([1, N], kdt)
-    bias = (torch.randn(1, N, device=dev, generator=g) * 0.02).to(dt)
+    bias = synth(torch, (1, N), 2, *bd, dt)
     y = torch.empty(M, N, device=dev, dtype=dt)
     plan = K.LinearActivation(da, db, dc, dbias, alpha, 0.0, kind)
     stream = torch.cuda.current_stream()
@@ -265,7 +309,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (torch.randn on device: X~N(0,1), W~N(0,0.02), R~N(0,1), zero bias)",
+        "data": "synthetic: SplitMix64 seed 0 + stream offset (X 0, W 1, R 3), Box-Muller normals, RNE to bf16; "
+                "X~N(0,1), W~N(0,0.02), R~N(0,1), zero bias",
         "config": {"workload": "C3 bf16 Linear+GELU_tanh+residual add", "M": 4096, "K": 4096, "N": 11008,
                    "weight_layout": "BA ([N][K], nn.Linear)", "plan": c3["plan"]},
         "roofline": {"bound": "mfma", "achieved": round(c3["tflops"], 2), "peak": PEAK_BF16_TFLOPS,
