@@ -435,3 +435,50 @@ def test_c3_plan_uses_pingpong():
     dx, dw, dy = K.desc([4096, 4096], K.BF16), K.desc([4096, 11008], K.BF16, "BA"), K.desc([4096, 11008], K.BF16)
     plan = K.LinearPostOps(dx, dw, dy, K.desc([1, 11008], K.BF16), act=K.ACT_GELU_TANH, binary=K.BIN_ADD, src=dy)
     assert plan.describe().startswith("mfma_bf16_pingpong_256x256")
+
+
+@pytest.mark.parametrize("shape", ["pingpong", "split_k", "gemv"])
+def test_hip_graph_capture_replays(shape):
+    # a plan's run captured into a HIP graph (after one eager run, which sizes the plan's workspace) and replayed
+    # three times with eager work in between; every replay must equal the eager result
+    dt = O.BF16
+    M, N, Kd = {"pingpong": (512, 512, 256), "split_k": (100, 200, 2048), "gemv": (1, 300, 1024)}[shape]
+    x = Case([M, Kd], dt, seed=250, dist="normal", lo=0.0, hi=1.0)
+    w = Case([Kd, N], dt, "BA", seed=251, dist="normal", lo=0.0, hi=0.05)
+    s = Case([M, N], dt, seed=252, lo=-1.0, hi=1.0)
+    y = Case([M, N], dt, zero=True)
+    force = {"pingpong": "4", "split_k": None, "gemv": None}[shape]
+    import os
+    old = os.environ.get("KUDNN_HIP_FORCE_CFG")
+    if force:
+        os.environ["KUDNN_HIP_FORCE_CFG"] = force
+    try:
+        plan = K.LinearPostOps(x.desc, w.desc, y.desc, None, act=K.ACT_GELU_TANH, binary=K.BIN_ADD, src=s.desc)
+    finally:
+        if force:
+            if old is None:
+                del os.environ["KUDNN_HIP_FORCE_CFG"]
+            else:
+                os.environ["KUDNN_HIP_FORCE_CFG"] = old
+    dx, dw, ds = x.device(), w.device(), s.device()
+    eager = zeros_device(y)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        plan.run(dx, dw, eager, None, ds, stream=stream)
+    torch.cuda.synchronize()
+    ref = y.clone_empty()
+    O.linear_postops(x.t, w.t, ref, None, O.ACT_GELU_TANH, 0.0, O.BIN_ADD, s.t)
+    compare(from_device(eager, dt), ref.buf, dt, f"eager {plan.describe()}")
+
+    out = zeros_device(y)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        plan.run(dx, dw, out, None, ds, stream=torch.cuda.current_stream())
+    for rep in range(3):
+        out.zero_()
+        junk = torch.randn(1 << 20, device="cuda").sum()  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep} of {plan.describe()} differs from the eager run"
+        del junk
