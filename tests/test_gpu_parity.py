@@ -482,3 +482,51 @@ def test_hip_graph_capture_replays(shape):
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {rep} of {plan.describe()} differs from the eager run"
         del junk
+
+
+def _sampled_tensor(rows_np, dt):
+    """O.Tensor of a dense [r, c] numpy block (bf16 as uint16 bits)."""
+    r, c = rows_np.shape
+    return O.Tensor((r, c), (c, 1), dt, np.ascontiguousarray(rows_np).reshape(-1).copy())
+
+
+def _bits(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("case", ["gemm_2gib_x", "skinny_2gib_w", "gemv_2gib_w"])
+def test_operands_of_2_gib(case):
+    # an operand of 2^31 bytes: the ping-pong GEMM (32-bit buffer offsets) hands over to the 4-wave kernel, the
+    # 2 <= M <= 16 row kernel to the MFMA-layout skinny kernel, and the M = 1 GEMV takes it directly; sampled output
+    # rows / columns are checked against the oracle
+    dt = O.BF16
+    g = torch.Generator(device="cuda").manual_seed(260)
+    if case == "gemm_2gib_x":
+        M, Kd, N = 131072, 8192, 256                     # X is 2^31 bytes
+    else:
+        M, Kd, N = (4 if case == "skinny_2gib_w" else 1), 8192, 131072  # W is 2^31 bytes
+    x = torch.randn(M, Kd, device="cuda", generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, Kd, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    plan = K.LinearActivation(K.desc([M, Kd], K.BF16), K.desc([Kd, N], K.BF16, "BA"), K.desc([M, N], K.BF16), None,
+                              1.0, 0.0, K.ACT_SWISH)
+    plan.run(x, w, y)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(261)
+    if case == "gemm_2gib_x":
+        rows = np.unique(np.concatenate([[0, M // 2, M - 1], rng.choice(M, 13, replace=False)]))
+        xs = _sampled_tensor(_bits(x[torch.as_tensor(rows, device="cuda")]), dt)
+        wt = _bits(w)  # [N][K] = logical [K, N] in layout BA
+        ws = O.Tensor((Kd, N), (1, Kd), dt, wt.reshape(-1).copy())
+        ref = O.empty((len(rows), N), (N, 1), dt)
+        O.linear_act(xs, ws, ref, None, O.ACT_SWISH, 1.0)
+        got = _bits(y[torch.as_tensor(rows, device="cuda")]).reshape(-1)
+    else:
+        cols = np.unique(np.concatenate([[0, N // 2, N - 1], rng.choice(N, 61, replace=False)]))
+        xs = _sampled_tensor(_bits(x), dt)
+        wsub = _bits(w[torch.as_tensor(cols, device="cuda")])      # [n][K]
+        ws = O.Tensor((Kd, len(cols)), (1, Kd), dt, wsub.reshape(-1).copy())
+        ref = O.empty((M, len(cols)), (len(cols), 1), dt)
+        O.linear_act(xs, ws, ref, None, O.ACT_SWISH, 1.0)
+        got = _bits(y[:, torch.as_tensor(cols, device="cuda")]).reshape(-1)
+    compare(got, ref.buf, dt, f"{case} {plan.describe()}")
