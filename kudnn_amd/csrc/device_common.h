@@ -27,14 +27,27 @@ __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return u2f(static_cast<uint32_t>(h) << 16); }
 
-// Round-to-nearest-even f32 -> bf16 (NaN kept quiet). Both results are computed and one is selected, so the
-// conversion is straight-line code.
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f)
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Round-to-nearest-even f32 -> bf16 by gfx950's conversion instruction (v_cvt_pk_bf16_f32). Over all 2^32 inputs it
+// equals (u + 0x7fff + ((u >> 16) & 1)) >> 16 for non-NaN u, and (u >> 16) | 0x40 (quiet, top payload bits kept)
+// for NaN: denormals are rounded, not flushed.
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f)); }
+
+// Two RNE conversions in one instruction: lo in bits 0-15, hi in bits 16-31.
+__device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi)
 {
-    const uint32_t u = f2u(f);
-    const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-    const uint32_t quiet = (u >> 16) | 0x0040u;
-    return static_cast<uint16_t>((u & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
+    const f32x2_t v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
+// a, b <- their RNE bf16 values, as f32.
+__device__ __forceinline__ void round_bf16_pair(float &a, float &b)
+{
+    const uint32_t p = pack_bf16x2_rne(a, b);
+    a = u2f(p << 16);
+    b = u2f(p & 0xffff0000u);
 }
 
 // Truncating f32 -> bf16 (keep the top 16 bits).
@@ -91,20 +104,6 @@ __device__ __forceinline__ void store_elem(void *p, int dt, int64_t idx, float v
 // exp via the hardware base-2 exponential: e^x = 2^(x*log2 e).
 __device__ __forceinline__ float fast_exp(float x) { return __expf(x); }
 
-// tanh from its exponential form tanh(y) = 1 - 2/(e^{2y}+1), odd-symmetric, saturating for large |y|.
-__device__ __forceinline__ float tanh_f32(float y)
-{
-    float a = fabsf(y);
-    float t;
-    if (a < 0.0004f) {
-        t = a;  // tanh(a) = a - a^3/3 + ..., the cubic term is below f32 resolution here
-    } else {
-        float e = fast_exp(2.0f * fminf(a, 20.0f));
-        t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
-    }
-    return copysignf(t, y);
-}
-
 // RELU: x <= 0 -> alpha*x, else x (relu/relu.c:14-25; a negative input times alpha 0 keeps its sign).
 __device__ __forceinline__ float act_relu(float x, float alpha) { return (x <= 0.0f) ? x * alpha : x; }
 
@@ -124,13 +123,16 @@ __device__ __forceinline__ float act_swish(float x, float alpha)
     return x * s;
 }
 
-// GELU (tanh form): 0.5*x*(1 + tanh(sqrt(2/pi)*x*(1 + 0.044715*x^2))) (gelu_tanh/vml_sve_la_gelu_tanh.h:22-39).
+// GELU (tanh form): 0.5*x*(1 + tanh(y)), y = sqrt(2/pi)*x*(1 + 0.044715*x^2) (gelu_tanh/vml_sve_la_gelu_tanh.h:22-39).
+// Evaluated through 0.5*(1 + tanh(y)) = 1/(1 + e^{-2y}) as x / (1 + 2^(x*(c0 + c1*x^2))), c0 = -2*sqrt(2/pi)*log2(e),
+// c1 = 0.044715*c0: one exp2 and one reciprocal, and no cancellation near 0. The limits are those of the tanh form:
+// x -> +inf gives x, x -> -inf gives -0 for finite x and NaN for -inf (-inf * 0).
 __device__ __forceinline__ float act_gelu_tanh(float x)
 {
-    const float kSqrt2OverPi = 0.7978845608028654f;
-    const float kCoef = 0.044715f;
-    float y = kSqrt2OverPi * x * (1.0f + kCoef * x * x);
-    return 0.5f * x * (1.0f + tanh_f32(y));
+    const float kC0 = -2.302208198144325f;   // -2 * sqrt(2/pi) * log2(e)
+    const float kC1 = -0.1029432395800235f;   // 0.044715 * kC0
+    const float z = x * fmaf(kC1, x * x, kC0);
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z));
 }
 
 // GELU (erf form): 0.5*x*(1 + erf(x/sqrt(2))) (gelu_erf/vml_sve_la_gelu_erf.h:20-28).
@@ -304,8 +306,8 @@ __device__ __forceinline__ void epi_apply4(const EpiParams &e, const EpiBatch &o
         }
         int64_t yi = ob.y + m * e.y_sm + n;
         if (e.y_dt == KUDNN_DT_BF16) {
-            uint32_t lo = static_cast<uint32_t>(f32_to_bf16_rne(v[0])) | (static_cast<uint32_t>(f32_to_bf16_rne(v[1])) << 16);
-            uint32_t hi = static_cast<uint32_t>(f32_to_bf16_rne(v[2])) | (static_cast<uint32_t>(f32_to_bf16_rne(v[3])) << 16);
+            uint32_t lo = pack_bf16x2_rne(v[0], v[1]);
+            uint32_t hi = pack_bf16x2_rne(v[2], v[3]);
             *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(e.y) + yi) = make_uint2(lo, hi);
         } else if (e.y_dt == KUDNN_DT_F32) {
             *reinterpret_cast<float4 *>(static_cast<float *>(e.y) + yi) = make_float4(v[0], v[1], v[2], v[3]);
@@ -400,8 +402,7 @@ __device__ __forceinline__ void epi_apply8(const EpiParams &e, const EpiBatch &o
             uint32_t w[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                w[q] = static_cast<uint32_t>(f32_to_bf16_rne(v[2 * q])) |
-                       (static_cast<uint32_t>(f32_to_bf16_rne(v[2 * q + 1])) << 16);
+                w[q] = pack_bf16x2_rne(v[2 * q], v[2 * q + 1]);
             }
             *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(e.y) + yi) = make_uint4(w[0], w[1], w[2], w[3]);
         } else if (e.y_dt == KUDNN_DT_F32) {
@@ -544,7 +545,11 @@ __device__ __forceinline__ void epi_fast8(const EpiParams &e, const EpiBatch &ob
         unpack_raw8<FORM>(pre.bias, bv);
     }
 #pragma unroll
-    for (int q = 0; q < 8; ++q) v[q] = round_store(DT, acc[q] * e.alpha + bv[q]);
+    for (int q = 0; q < 8; ++q) v[q] = acc[q] * e.alpha + bv[q];
+    if constexpr (DT == KUDNN_DT_BF16) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) round_bf16_pair(v[2 * q], v[2 * q + 1]);
+    }
     if constexpr (ACT != KUDNN_ACT_UNIMPLEMENTED) {
 #pragma unroll
         for (int q = 0; q < 8; ++q) v[q] = act_round(DT, ACT, act_fixed<ACT>(v[q], e.act_alpha));
@@ -567,10 +572,7 @@ __device__ __forceinline__ void epi_fast8(const EpiParams &e, const EpiBatch &ob
     if constexpr (FORM == EPI_FORM_BF16) {
         uint32_t w[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            w[q] = static_cast<uint32_t>(f32_to_bf16_rne(v[2 * q])) |
-                   (static_cast<uint32_t>(f32_to_bf16_rne(v[2 * q + 1])) << 16);
-        }
+        for (int q = 0; q < 4; ++q) w[q] = pack_bf16x2_rne(v[2 * q], v[2 * q + 1]);
         *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(e.y) + yi) = make_uint4(w[0], w[1], w[2], w[3]);
     } else {
         float *yp = static_cast<float *>(e.y) + yi;
