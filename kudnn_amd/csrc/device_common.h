@@ -508,23 +508,37 @@ __device__ __forceinline__ void unpack_raw8(const Raw8 &r, float v[8])
     }
 }
 
-// Loads the binary operand and the bias of group (m, n .. n+7). A bias broadcast along n (bias_sn == 0) is one
-// value, kept as f32 bits in bias.lo.x.
+// Binary operand of group (m, n .. n+7).
+template <int FORM>
+__device__ __forceinline__ Raw8 epi_prefetch8_src(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n)
+{
+    Raw8 r{};
+    if (e.bin != KUDNN_BINARY_NONE) {
+        r = load_raw8<FORM>(e.src, ob.src + m * e.src_sm + n);
+    }
+    return r;
+}
+
+// Bias of group (m, n .. n+7). A bias broadcast along n (bias_sn == 0) is one value, kept as f32 bits in lo.x.
+template <int FORM>
+__device__ __forceinline__ Raw8 epi_prefetch8_bias(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n)
+{
+    Raw8 r{};
+    if (e.bias != nullptr) {
+        if (e.bias_sn == 0) {
+            r.lo.x = f2u(load_elem(e.bias, form_dt<FORM>(), ob.bias + m * e.bias_sm));
+        } else {
+            r = load_raw8<FORM>(e.bias, ob.bias + m * e.bias_sm + n);
+        }
+    }
+    return r;
+}
+
+// Loads the binary operand and the bias of group (m, n .. n+7).
 template <int FORM>
 __device__ __forceinline__ Pre8 epi_prefetch8(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n)
 {
-    Pre8 p{};
-    if (e.bin != KUDNN_BINARY_NONE) {
-        p.src = load_raw8<FORM>(e.src, ob.src + m * e.src_sm + n);
-    }
-    if (e.bias != nullptr) {
-        if (e.bias_sn == 0) {
-            p.bias.lo.x = f2u(load_elem(e.bias, form_dt<FORM>(), ob.bias + m * e.bias_sm));
-        } else {
-            p.bias = load_raw8<FORM>(e.bias, ob.bias + m * e.bias_sm + n);
-        }
-    }
-    return p;
+    return Pre8{epi_prefetch8_src<FORM>(e, ob, m, n), epi_prefetch8_bias<FORM>(e, ob, m, n)};
 }
 
 // Epilogue of the 8-column group (m, n .. n+7), all in bounds, operands from epi_prefetch8.

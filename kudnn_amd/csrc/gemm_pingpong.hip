@@ -28,7 +28,7 @@
 //
 // Epilogue: the accumulators pass through LDS one 32-column strip at a time and are read back row-major, 8
 // consecutive columns per lane, so bias / activation / residual run on 8 values and the result is one 16-byte store;
-// the bias and binary operand of a strip are loaded before its staging round trip. The activation is a template
+// the bias and binary operand are loaded two strips ahead of their use. The activation is a template
 // argument of the kernel and the all-bf16 case has its own code, so the epilogue of a full tile is short straight-line
 // code (an epilogue that dispatched every option at run time at each of its 16 call sites made the kernel 2.2 MB and
 // spent most of its time in instruction-cache misses). Tiles that cross the matrix edge take a rolled per-element loop.
@@ -75,7 +75,9 @@ __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC
 __device__ __forceinline__ void copy_block(const uint16_t *base, uint32_t totalBytes, uint32_t elemOff, uint32_t voff, uint4 *dst)
 {
     const uint32_t off = elemOff * 2u;
-    const uint32_t remain = off < totalBytes ? totalBytes - off : 0u;
+    // the clamped difference is a saturating subtract, which only the vector ALU has; without readfirstlane the
+    // resource would look divergent and every copy would be wrapped in a waterfall loop
+    const uint32_t remain = __builtin_amdgcn_readfirstlane(off < totalBytes ? totalBytes - off : 0u);
     __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)(base + elemOff), (short)0, (int)remain, 0x00020000);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)dst, 16, voff, 0, 0, 0);
 }
@@ -102,33 +104,47 @@ __device__ __forceinline__ void wave_sync()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Epilogue of a full tile (all rows and columns in bounds) in a fixed form: lane -> row rl + 16 * pass, columns
-// col8 .. +8 of each strip.
+// Epilogue of a full tile (all rows and columns in bounds) in a fixed form, with no bias or a bias that is one row
+// broadcast over m: lane -> row rl + 16 * pass, columns col8 .. +8 of each strip. The bias and binary operand of
+// two strips are in flight at a time (strip j + 2's loads are issued once strip j is stored), and those of strips 0
+// and 1 are issued before the barrier that ends the main loop, so one memory latency is exposed per tile instead of
+// one per strip. The bias is the same for the four rows a lane covers in a strip and is loaded once.
 template <int ACT, int FORM>
 __device__ __forceinline__ void epilogue_full(const EpiParams &ep, const EpiBatch &ob, const f32x16_t (&acc)[4][2],
                                               float *stage, int lane, int64_t mW, int64_t nW)
 {
     const int lrow = lane & 31, lh = lane >> 5;
     const int col8 = (lane & 3) * 8, rl = lane >> 2;
+    Raw8 src[2][4], bias[2];
+    auto fetch = [&](auto jc) __attribute__((always_inline)) {
+        constexpr int j = decltype(jc)::value;
+        const int64_t n = nW + j * 32 + col8;
+        bias[j & 1] = epi_prefetch8_bias<FORM>(ep, ob, mW + rl, n);
+        sfor<4>([&](auto pc) __attribute__((always_inline)) {
+            constexpr int ps = decltype(pc)::value;
+            src[j & 1][ps] = epi_prefetch8_src<FORM>(ep, ob, mW + rl + ps * 16, n);
+        });
+    };
+    fetch(std::integral_constant<int, 0>{});
+    fetch(std::integral_constant<int, 1>{});
+    __syncthreads();  // every wave is done with the tile buffers that the staging area reuses
     sfor<4>([&](auto jc) __attribute__((always_inline)) {
         constexpr int j = decltype(jc)::value;
         const int64_t n = nW + j * 32 + col8;
-        Pre8 pre[4];
-        sfor<4>([&](auto pc) __attribute__((always_inline)) {
-            constexpr int ps = decltype(pc)::value;
-            pre[ps] = epi_prefetch8<FORM>(ep, ob, mW + rl + ps * 16, n);
-        });
         stage_strip(acc[j], stage, lrow, lh);
         wave_sync();
         sfor<4>([&](auto pc) __attribute__((always_inline)) {
             constexpr int ps = decltype(pc)::value;
             const int r = rl + ps * 16;
-            const float *src = stage + r * kPitch + col8;
-            const float4 lo = *reinterpret_cast<const float4 *>(src);
-            const float4 hi = *reinterpret_cast<const float4 *>(src + 4);
+            const float *sp = stage + r * kPitch + col8;
+            const float4 lo = *reinterpret_cast<const float4 *>(sp);
+            const float4 hi = *reinterpret_cast<const float4 *>(sp + 4);
             const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-            epi_fast8<ACT, FORM>(ep, ob, mW + r, n, v, pre[ps]);
+            epi_fast8<ACT, FORM>(ep, ob, mW + r, n, v, Pre8{src[j & 1][ps], bias[j & 1]});
         });
+        if constexpr (j + 2 < 4) {
+            fetch(std::integral_constant<int, j + 2>{});
+        }
         wave_sync();
     });
 }
@@ -141,6 +157,7 @@ __device__ __forceinline__ void epilogue_edge(const EpiParams &ep, const EpiBatc
 {
     const int lrow = lane & 31, lh = lane >> 5;
     const int col8 = (lane & 3) * 8, rl = lane >> 2;
+    __syncthreads();  // every wave is done with the tile buffers that the staging area reuses
     sfor<4>([&](auto jc) __attribute__((always_inline)) {
         constexpr int j = decltype(jc)::value;
         const int64_t n = nW + j * 32 + col8;
@@ -175,6 +192,7 @@ __device__ __forceinline__ void epilogue_generic(const EpiParams &ep, const EpiB
 {
     const int lrow = lane & 31, lh = lane >> 5;
     const int col8 = (lane & 3) * 8, rl = lane >> 2;
+    __syncthreads();  // every wave is done with the tile buffers that the staging area reuses
     sfor<4>([&](auto jc) __attribute__((always_inline)) {
         constexpr int j = decltype(jc)::value;
         const int64_t n = nW + j * 32 + col8;
@@ -358,14 +376,14 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_pingpong_kernel(GemmOperands
 
     // ---- epilogue: wave (p, g) owns rows p*64 .. +64, columns g*128 .. +128; 4 strips of 32 columns
     wait_vmcnt<0>();
-    __syncthreads();  // every wave is done with the tile buffers that the staging area reuses
+    // each epilogue starts with a barrier: every wave is done with the tile buffers that the staging area reuses
     // 64 x 36 floats (9 KB) per wave: waves 0-2 stage in a0, 3-5 in a1, 6-7 in b0
     float *stage = reinterpret_cast<float *>(wave < 3 ? a0 : (wave < 6 ? a1 : b0)) + (wave % 3) * (64 * kPitch);
     const EpiBatch ob = epi_batch_offsets(ep, batch);
     const int64_t mW = m0 + p * 64, nW = n0 + g * 128;
     if constexpr (FORM == EPI_FORM_GENERIC) {
         epilogue_generic(ep, ob, acc, stage, lane, mW, nW, M, N);
-    } else if (m0 + kBM <= M && n0 + kBN <= N) {
+    } else if (m0 + kBM <= M && n0 + kBN <= N && (ep.bias == nullptr || ep.bias_sm == 0)) {
         epilogue_full<ACT, FORM>(ep, ob, acc, stage, lane, mW, nW);
     } else {
         epilogue_edge<ACT, FORM>(ep, ob, acc, stage, lane, mW, nW, M, N);

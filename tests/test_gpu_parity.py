@@ -393,6 +393,52 @@ def test_pingpong_epilogue_forms(force_pingpong, mnk, ydt, bias_rows):
     compare(from_device(dy, ydt), ref.buf, ydt, f"{plan.describe()} ydt={ydt} bias_rows={bias_rows}")
 
 
+def _rounding_boundary_values(seed: int = 7, nans: bool = False) -> np.ndarray:
+    """f32 bit patterns at every kind of f32 -> bf16 rounding boundary: upper halves (sign, exponent including 0 for
+    denormals, top mantissa bits; random plus special ones) joined with lower halves 0, 1, 0x7fff, 0x8000 (the tie),
+    0x8001 and 0xffff. That covers ties to even and to odd, the largest finite values (which round to +-Inf), +-Inf
+    and, with nans, quiet and signalling NaNs with payloads in either half."""
+    rng = np.random.default_rng(seed)
+    special = [0x0000, 0x8000, 0x0001, 0x8001, 0x007F, 0x0080, 0x807F, 0x7F7F, 0xFF7F, 0x7F80, 0xFF80, 0x3F80, 0x3F81,
+               0xBF80, 0xBF81, 0x7FC0, 0xFFC0, 0x7FBF, 0x7F81]
+    hi = np.concatenate([rng.integers(0, 1 << 16, 1500), special]).astype(np.uint32)
+    lo = np.array([0x0000, 0x0001, 0x7FFF, 0x8000, 0x8001, 0xFFFF], np.uint32)
+    u = ((hi[:, None] << 16) | lo[None, :]).reshape(-1)
+    return u if nans else u[(u & 0x7FFFFFFF) <= 0x7F800000]
+
+
+@pytest.mark.parametrize("M", [3, 64])
+@pytest.mark.parametrize("via", ["weight", "bias"])
+def test_bf16_output_rounding_boundaries(M, via):
+    # Y(bf16) = X(f32, ones) @ W(f32) + bias(f32): each output is one W value (zero bias) or one bias value (zero W),
+    # so the store is the RNE of arbitrary f32 bit patterns, checked bit for bit against the oracle. NaNs go through
+    # the bias only (the epilogue's f32 add keeps their payloads; the MFMA need not).
+    u = _rounding_boundary_values(nans=(via == "bias"))
+    N = u.size
+    vals = u.view(np.float32)
+    zeros = np.zeros(N, np.float32)
+    x = O.Tensor((M, 1), (1, 1), O.F32, np.ones(M, np.float32))
+    w = O.Tensor((1, N), (1, 1), O.F32, vals.copy() if via == "weight" else zeros)  # BA: physically [N][1]
+    b = O.Tensor((1, N), (0, 1), O.F32, zeros if via == "weight" else vals.copy())  # a size-1 dim has stride 0
+    ref = O.empty((M, N), (N, 1), O.BF16)
+    O.linear_postops(x, w, ref, b)
+    want = O.from_f32_rne(vals, O.BF16)
+    # the oracle stores the RNE of each value (-0 excepted: +0 + -0 is +0)
+    nz = u != 0x80000000
+    assert np.array_equal(ref.buf.reshape(M, N)[0][nz], want[nz])
+    assert np.count_nonzero(want != (u >> 16).astype(np.uint16)) > 1000  # many cases round away from truncation
+    plan = K.LinearPostOps(K.desc([M, 1], K.F32), K.desc([1, N], K.F32, "BA"), K.desc([M, N], K.BF16),
+                           K.desc([1, N], K.F32))
+    dy = torch.zeros(M * N, dtype=torch.int16, device="cuda")
+    dev = lambda t: torch.from_numpy(t.buf).cuda()
+    plan.run(dev(x), dev(w), dy, dev(b))
+    torch.cuda.synchronize()
+    got = dy.cpu().numpy().view(np.uint16)
+    bad = np.nonzero(got != ref.buf)[0]
+    assert bad.size == 0, (f"{plan.describe()}: {bad.size} outputs differ, first value {u[bad[0] % N]:#010x} "
+                           f"got {got[bad[0]]:#06x} want {ref.buf[bad[0]]:#06x}")
+
+
 @pytest.mark.parametrize("kind", [O.RES_IDENTIAL, O.RES_EXT])
 def test_pingpong_linear_res_stores_c(force_pingpong, kind):
     # LinearResFWD writes C and linearRes from one launch (the generic form of the epilogue)
