@@ -188,23 +188,68 @@ __device__ __forceinline__ EpiBatch epi_batch_offsets(const EpiParams &e, int64_
     return o;
 }
 
+// Epilogue forms (the types of every epilogue tensor, fixed at compile time in the fast paths): all bf16, all f32, or
+// read at run time.
+enum { EPI_FORM_BF16 = 0, EPI_FORM_F32 = 1, EPI_FORM_GENERIC = 2 };
+
+template <int FORM>
+constexpr int form_dt()
+{
+    return FORM == EPI_FORM_BF16 ? KUDNN_DT_BF16 : KUDNN_DT_F32;
+}
+
+// Raw bits of one element of dtype dt (f32: 32 bits; bf16 / f16: 16 bits, zero-extended).
+__device__ __forceinline__ uint32_t load_raw1(const void *p, int dt, int64_t idx)
+{
+    switch (dt) {
+        case KUDNN_DT_F32: return static_cast<const uint32_t *>(p)[idx];
+        case KUDNN_DT_BF16:
+        case KUDNN_DT_F16: return static_cast<const uint16_t *>(p)[idx];
+        default: return 0u;
+    }
+}
+
+__device__ __forceinline__ float raw1_to_f32(uint32_t r, int dt)
+{
+    switch (dt) {
+        case KUDNN_DT_F32: return u2f(r);
+        case KUDNN_DT_BF16: return u2f(r << 16);
+        case KUDNN_DT_F16: return f16_to_f32(static_cast<uint16_t>(r));
+        default: return 0.0f;
+    }
+}
+
+// Marks x as read and rewritten here, so that nothing computed from it is moved above this point.
+__device__ __forceinline__ uint32_t use_here(uint32_t x)
+{
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
 // Epilogue operands of one output element (C when beta != 0, bias, binary operand), loadable ahead of the
-// accumulator so that their latency overlaps the main loop.
+// accumulator so that their latency overlaps the main loop. They are kept as raw bits and converted where they are
+// used (behind use_here): a conversion next to the load would make the wave wait for it before issuing the loads
+// that follow.
 struct EpiPre1 {
-    float c, bias, src;
+    uint32_t c, bias, src;
 };
 
+// FORM fixes the operand types (a fixed form has beta == 0 and bias / binary operand of the output's type); the
+// generic form reads them from e.
+template <int FORM = EPI_FORM_GENERIC>
 __device__ __forceinline__ EpiPre1 epi_prefetch1(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n)
 {
-    EpiPre1 p{0.0f, 0.0f, 0.0f};
-    if (e.beta != 0.0f) {
-        p.c = load_elem(e.c, e.c_dt, ob.c + m * e.c_sm + n * e.c_sn);
+    EpiPre1 p{0u, 0u, 0u};
+    if (FORM == EPI_FORM_GENERIC && e.beta != 0.0f) {
+        p.c = load_raw1(e.c, e.c_dt, ob.c + m * e.c_sm + n * e.c_sn);
     }
     if (e.bias != nullptr) {
-        p.bias = load_elem(e.bias, e.bias_dt, ob.bias + m * e.bias_sm + n * e.bias_sn);
+        p.bias = load_raw1(e.bias, FORM == EPI_FORM_GENERIC ? e.bias_dt : form_dt<FORM>(),
+                           ob.bias + m * e.bias_sm + n * e.bias_sn);
     }
     if (e.bin != KUDNN_BINARY_NONE) {
-        p.src = load_elem(e.src, e.src_dt, ob.src + m * e.src_sm + n * e.src_sn);
+        p.src = load_raw1(e.src, FORM == EPI_FORM_GENERIC ? e.src_dt : form_dt<FORM>(),
+                          ob.src + m * e.src_sm + n * e.src_sn);
     }
     return p;
 }
@@ -215,10 +260,10 @@ __device__ __forceinline__ void epi_apply_pre(const EpiParams &e, const EpiBatch
 {
     float v = acc * e.alpha;
     if (e.beta != 0.0f) {
-        v += e.beta * p.c;
+        v += e.beta * raw1_to_f32(use_here(p.c), e.c_dt);
     }
     if (e.bias != nullptr) {
-        v += p.bias;
+        v += raw1_to_f32(use_here(p.bias), e.bias_dt);
     }
     v = round_store(e.c_dt, v);
     if (e.store_c) {
@@ -228,12 +273,13 @@ __device__ __forceinline__ void epi_apply_pre(const EpiParams &e, const EpiBatch
         v = act_round(e.c_dt, e.act, apply_act(e.act, v, e.act_alpha));
     }
     if (e.bin != KUDNN_BINARY_NONE) {
+        const float sv = raw1_to_f32(use_here(p.src), e.src_dt);
         if (e.bin == KUDNN_BINARY_ADD) {
-            v = v + p.src;
+            v = v + sv;
         } else if (e.bin == KUDNN_BINARY_EXT) {
-            v = fmaf(p.src, e.gamma, v);
+            v = fmaf(sv, e.gamma, v);
         } else {
-            v = v * p.src;
+            v = v * sv;
         }
     }
     store_elem(e.y, e.y_dt, ob.y + m * e.y_sm + n * e.y_sn, v);
@@ -247,8 +293,59 @@ __device__ __forceinline__ void epi_apply(const EpiParams &e, const EpiBatch &ob
 
 // Epilogue for four consecutive columns n..n+3 of row m (the MFMA output layout gives each lane runs
 // of four columns). Uses 8/16-byte accesses when the tensors are contiguous along n and aligned.
-__device__ __forceinline__ void epi_apply4(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, int64_t N,
-                                           const float acc[4])
+// Raw bits of the bias and binary operand of a run of 4 columns (m, n .. n+3), loaded ahead of the accumulators
+// when the run takes the fast4 path with f32 or bf16 operands (other cases load at use). Each width has its own
+// registers, so no copy (and no wait for the load) joins the two load paths.
+struct EpiPre4 {
+    uint2 src16, bias16;
+    uint4 src32, bias32;
+};
+
+__device__ __forceinline__ EpiPre4 epi_prefetch4(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, int64_t N)
+{
+    EpiPre4 p{make_uint2(0u, 0u), make_uint2(0u, 0u), make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
+    if (n + 3 < N && e.fast4) {
+        if (e.bin != KUDNN_BINARY_NONE) {
+            const int64_t si = ob.src + m * e.src_sm + n;
+            if (e.src_dt == KUDNN_DT_BF16) {
+                p.src16 = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(e.src) + si);
+            } else if (e.src_dt == KUDNN_DT_F32) {
+                p.src32 = *reinterpret_cast<const uint4 *>(static_cast<const float *>(e.src) + si);
+            }
+        }
+        if (e.bias != nullptr && e.bias_sn != 0) {
+            const int64_t bi = ob.bias + m * e.bias_sm + n * e.bias_sn;
+            if (e.bias_dt == KUDNN_DT_BF16) {
+                p.bias16 = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(e.bias) + bi);
+            } else if (e.bias_dt == KUDNN_DT_F32) {
+                p.bias32 = *reinterpret_cast<const uint4 *>(static_cast<const float *>(e.bias) + bi);
+            }
+        }
+    }
+    return p;
+}
+
+// 4 values of dtype dt (f32 or bf16) from the raw bits of epi_prefetch4.
+__device__ __forceinline__ void unpack_pre4(const uint2 &r16, const uint4 &r32, int dt, float v[4])
+{
+    if (dt == KUDNN_DT_BF16) {
+        const uint32_t x = use_here(r16.x), y = use_here(r16.y);
+        v[0] = u2f(x << 16);
+        v[1] = u2f(x & 0xffff0000u);
+        v[2] = u2f(y << 16);
+        v[3] = u2f(y & 0xffff0000u);
+    } else {
+        v[0] = u2f(use_here(r32.x));
+        v[1] = u2f(use_here(r32.y));
+        v[2] = u2f(use_here(r32.z));
+        v[3] = u2f(use_here(r32.w));
+    }
+}
+
+// Epilogue of the run of 4 columns (m, n .. n+3) (the columns at or past N are skipped), with operands from
+// epi_prefetch4.
+__device__ __forceinline__ void epi_apply4_pre(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, int64_t N,
+                                               const float acc[4], const EpiPre4 &pre)
 {
     if (n + 3 < N && e.fast4) {
         // fast4: y (and src / bias when present) are contiguous along n and 4-element aligned,
@@ -260,9 +357,8 @@ __device__ __forceinline__ void epi_apply4(const EpiParams &e, const EpiBatch &o
             if (e.bias_sn == 0) {
                 float b0 = load_elem(e.bias, e.bias_dt, bi);
                 bv[0] = bv[1] = bv[2] = bv[3] = b0;
-            } else if (e.bias_dt == KUDNN_DT_F32) {
-                float4 t = *reinterpret_cast<const float4 *>(static_cast<const float *>(e.bias) + bi);
-                bv[0] = t.x; bv[1] = t.y; bv[2] = t.z; bv[3] = t.w;
+            } else if (e.bias_dt == KUDNN_DT_F32 || e.bias_dt == KUDNN_DT_BF16) {
+                unpack_pre4(pre.bias16, pre.bias32, e.bias_dt, bv);
             } else {
                 for (int q = 0; q < 4; ++q) bv[q] = load_elem(e.bias, e.bias_dt, bi + q);
             }
@@ -284,13 +380,8 @@ __device__ __forceinline__ void epi_apply4(const EpiParams &e, const EpiBatch &o
         if (e.bin != KUDNN_BINARY_NONE) {
             int64_t si = ob.src + m * e.src_sm + n;
             float s[4];
-            if (e.src_dt == KUDNN_DT_BF16) {
-                uint2 raw = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(e.src) + si);
-                s[0] = u2f(raw.x << 16); s[1] = u2f(raw.x & 0xffff0000u);
-                s[2] = u2f(raw.y << 16); s[3] = u2f(raw.y & 0xffff0000u);
-            } else if (e.src_dt == KUDNN_DT_F32) {
-                float4 t = *reinterpret_cast<const float4 *>(static_cast<const float *>(e.src) + si);
-                s[0] = t.x; s[1] = t.y; s[2] = t.z; s[3] = t.w;
+            if (e.src_dt == KUDNN_DT_BF16 || e.src_dt == KUDNN_DT_F32) {
+                unpack_pre4(pre.src16, pre.src32, e.src_dt, s);
             } else {
                 for (int q = 0; q < 4; ++q) s[q] = load_elem(e.src, e.src_dt, si + q);
             }
@@ -321,6 +412,12 @@ __device__ __forceinline__ void epi_apply4(const EpiParams &e, const EpiBatch &o
             epi_apply(e, ob, m, n + q, acc[q]);
         }
     }
+}
+
+__device__ __forceinline__ void epi_apply4(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, int64_t N,
+                                           const float acc[4])
+{
+    epi_apply4_pre(e, ob, m, n, N, acc, epi_prefetch4(e, ob, m, n, N));
 }
 
 // Epilogue for eight consecutive columns n..n+7 of row m (n a multiple of 8): one 16-byte bf16 (or two
@@ -429,8 +526,6 @@ __device__ __forceinline__ void epi_apply8(const EpiParams &e, const EpiBatch &o
 // operand contiguous along n, 16-byte aligned 8-column groups). Anything else is EPI_FORM_GENERIC and goes through
 // epi_apply. Arithmetic and rounding are those of epi_apply.
 
-enum { EPI_FORM_BF16 = 0, EPI_FORM_F32 = 1, EPI_FORM_GENERIC = 2 };
-
 // Host-side choice of the form for an epilogue. need8: the kernel stores 8-column groups with 16-byte accesses
 // (fast8 must hold); a kernel that stores single elements passes false.
 inline int epi_form(const EpiParams &e, bool need8 = true)
@@ -444,12 +539,6 @@ inline int epi_form(const EpiParams &e, bool need8 = true)
         return EPI_FORM_GENERIC;
     }
     return dt == KUDNN_DT_BF16 ? EPI_FORM_BF16 : EPI_FORM_F32;
-}
-
-template <int FORM>
-constexpr int form_dt()
-{
-    return FORM == EPI_FORM_BF16 ? KUDNN_DT_BF16 : KUDNN_DT_F32;
 }
 
 template <int ACT>
@@ -603,19 +692,20 @@ __device__ __forceinline__ void epi_elem_pre(const EpiParams &e, const EpiBatch 
     constexpr int DT = form_dt<FORM>();
     float v = acc * e.alpha;
     if (e.bias != nullptr) {
-        v += p.bias;
+        v += raw1_to_f32(use_here(p.bias), DT);
     }
     v = round_store(DT, v);
     if constexpr (ACT != KUDNN_ACT_UNIMPLEMENTED) {
         v = act_round(DT, ACT, act_fixed<ACT>(v, e.act_alpha));
     }
     if (e.bin != KUDNN_BINARY_NONE) {
+        const float sv = raw1_to_f32(use_here(p.src), DT);
         if (e.bin == KUDNN_BINARY_ADD) {
-            v = v + p.src;
+            v = v + sv;
         } else if (e.bin == KUDNN_BINARY_EXT) {
-            v = fmaf(p.src, e.gamma, v);
+            v = fmaf(sv, e.gamma, v);
         } else {
-            v = v * p.src;
+            v = v * sv;
         }
     }
     store_elem(e.y, DT, ob.y + m * e.y_sm + n * e.y_sn, v);

@@ -168,7 +168,7 @@ __global__ __launch_bounds__(256) void gemv_bf16_kernel(GemmOperands op, EpiPara
     // rows are 16-byte aligned with a zero-padded or exact multiple-of-8 length (the planner packs otherwise), so whole
     // 16-byte chunks up to ceil(K / 8) are in bounds; the launcher guarantees ceil(K / 8) < 2^31
     const int chunks = static_cast<int>((op.K + 7) / 8);
-    const EpiPre1 pre = epi_prefetch1(ep, ob, 0, n);
+    const EpiPre1 pre = epi_prefetch1<FORM>(ep, ob, 0, n);
     float sum = 0.0f;
     int c0 = 0;
     for (; c0 + kGemvCh * 64 <= chunks; c0 += kGemvCh * 64) {
@@ -281,6 +281,13 @@ __global__ __launch_bounds__(KW * 64) void skinny_rows_kernel(GemmOperands op, E
     }
     u32x4_t *tw = tile[wave];
 
+    // wave 0 runs the epilogue: its bias and binary operand are loaded right after its first block's loads, so their
+    // latency overlaps that block's instead of following the K loop
+    const EpiBatch ob = epi_batch_offsets(ep, batch);
+    const int64_t nq = n0 + 4 * q;  // lane holds D[n = nq + i][m = r16], i = 0..3, after the K loop
+    EpiPre4 pre{make_uint2(0u, 0u), make_uint2(0u, 0u), make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
+    const bool epiLane = wave == 0 && r16 < M && nq < N;
+
     f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int b = wave; b < blocks; b += KW) {
         const int c0 = b * 32;
@@ -295,6 +302,9 @@ __global__ __launch_bounds__(KW * 64) void skinny_rows_kernel(GemmOperands op, E
             const int kc = c0 + 4 * k + q;
             const bool in = r16 < M && kc < chunks;
             xv[k] = __builtin_amdgcn_raw_buffer_load_b128(xrs, in ? xrow + static_cast<uint32_t>(kc) * 16u : kOut, 0, 0);
+        }
+        if (b == 0 && epiLane) {
+            pre = epi_prefetch4(ep, ob, r16, nq, N);
         }
         // the previous block's tile reads have returned (their MFMAs consumed them); order the rewrite after them
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -327,14 +337,11 @@ __global__ __launch_bounds__(KW * 64) void skinny_rows_kernel(GemmOperands op, E
         sum[2] += p[2];
         sum[3] += p[3];
     }
-    // lane holds D[n = n0 + 4q + i][m = r16], i = 0..3
-    const int64_t n = n0 + 4 * q;
-    if (r16 >= M || n >= N) {
+    if (r16 >= M || nq >= N) {
         return;
     }
-    const EpiBatch ob = epi_batch_offsets(ep, batch);
     const float v[4] = {sum[0], sum[1], sum[2], sum[3]};
-    epi_apply4(ep, ob, r16, n, N, v);
+    epi_apply4_pre(ep, ob, r16, nq, N, v, pre);
 }
 
 template <int KW, int UNR>
