@@ -190,6 +190,62 @@ __global__ __launch_bounds__(256) void gemv_bf16_kernel(GemmOperands op, EpiPara
     }
 }
 
+// The single-batch, fixed-form launch takes only what it reads (about 100 bytes instead of the 380 of GemmOperands +
+// EpiParams): the kernel-argument block is copied and read on every launch, which costs about 0.25 us per launch at
+// the larger size, measured on MI355X, against a decode step of 7-19 us.
+struct GemvArgs {
+    const uint16_t *x;
+    const uint16_t *w;
+    const void *bias;
+    const void *src;
+    void *y;
+    int64_t ldb;
+    int64_t bias_sn, src_sn, y_sn;
+    int n, chunks;
+    float alpha, gamma, act_alpha;
+    int bin;
+};
+
+template <int ACT, int FORM>
+__global__ __launch_bounds__(256) void gemv_bf16_compact_kernel(GemvArgs a)
+{
+    const int lane = threadIdx.x & 63;
+    const int n = static_cast<int>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (n >= a.n) {
+        return;
+    }
+    // the epilogue helpers read an EpiParams: the fields a fixed-form M = 1 epilogue uses, the rest zero
+    EpiParams ep{};
+    ep.alpha = a.alpha;
+    ep.gamma = a.gamma;
+    ep.act_alpha = a.act_alpha;
+    ep.bin = a.bin;
+    ep.bias = a.bias;
+    ep.src = a.src;
+    ep.y = a.y;
+    ep.bias_sn = a.bias_sn;
+    ep.src_sn = a.src_sn;
+    ep.y_sn = a.y_sn;
+    const EpiBatch ob{0, 0, 0, 0};
+    const EpiPre1 pre = epi_prefetch1<FORM>(ep, ob, 0, n);
+    const uint16_t *W = a.w + static_cast<int64_t>(n) * a.ldb;
+    float sum = 0.0f;
+    int c0 = 0;
+    for (; c0 + kGemvCh * 64 <= a.chunks; c0 += kGemvCh * 64) {
+        sum += gemv_block<true>(a.x, W, c0, a.chunks, lane);
+    }
+    if (c0 < a.chunks) {
+        sum += gemv_block<false>(a.x, W, c0, a.chunks, lane);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        sum += __shfl_xor(sum, o);
+    }
+    if (lane == 0) {
+        epi_elem_pre<ACT, FORM>(ep, ob, 0, n, sum, pre);
+    }
+}
+
 // 32-bit row and chunk indices
 bool gemv_eligible(const GemmOperands &op)
 {
@@ -211,6 +267,47 @@ int launch_gemv(const GemmOperands &op, const EpiParams &ep, int64_t batches, hi
             default: break;
         }
     };
+    dim3 grid(static_cast<unsigned>((op.N + 3) / 4), static_cast<unsigned>(batches));
+    if (batches == 1 && form != EPI_FORM_GENERIC) {
+        decltype(&gemv_bf16_compact_kernel<0, EPI_FORM_BF16>) ck = nullptr;
+        auto pickc = [&](auto formc) {
+            constexpr int F = decltype(formc)::value;
+            switch (ep.act) {
+                case KUDNN_ACT_UNIMPLEMENTED: ck = gemv_bf16_compact_kernel<KUDNN_ACT_UNIMPLEMENTED, F>; break;
+                case KUDNN_ACT_RELU: ck = gemv_bf16_compact_kernel<KUDNN_ACT_RELU, F>; break;
+                case KUDNN_ACT_SWISH: ck = gemv_bf16_compact_kernel<KUDNN_ACT_SWISH, F>; break;
+                case KUDNN_ACT_GELU_TANH: ck = gemv_bf16_compact_kernel<KUDNN_ACT_GELU_TANH, F>; break;
+                case KUDNN_ACT_GELU_ERF: ck = gemv_bf16_compact_kernel<KUDNN_ACT_GELU_ERF, F>; break;
+                default: break;
+            }
+        };
+        if (form == EPI_FORM_BF16) {
+            pickc(std::integral_constant<int, EPI_FORM_BF16>{});
+        } else {
+            pickc(std::integral_constant<int, EPI_FORM_F32>{});
+        }
+        if (ck == nullptr) {
+            return -1;
+        }
+        GemvArgs a{};
+        a.x = static_cast<const uint16_t *>(op.a);
+        a.w = static_cast<const uint16_t *>(op.b);
+        a.bias = ep.bias;
+        a.src = ep.src;
+        a.y = ep.y;
+        a.ldb = op.ldb;
+        a.bias_sn = ep.bias_sn;
+        a.src_sn = ep.src_sn;
+        a.y_sn = ep.y_sn;
+        a.n = static_cast<int>(op.N);
+        a.chunks = static_cast<int>((op.K + 7) / 8);
+        a.alpha = ep.alpha;
+        a.gamma = ep.gamma;
+        a.act_alpha = ep.act_alpha;
+        a.bin = ep.bin;
+        hipLaunchKernelGGL(ck, grid, dim3(256), 0, stream, a);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
     if (form == EPI_FORM_BF16) {
         pick(std::integral_constant<int, EPI_FORM_BF16>{});
     } else if (form == EPI_FORM_F32) {
@@ -221,7 +318,6 @@ int launch_gemv(const GemmOperands &op, const EpiParams &ep, int64_t batches, hi
     if (kernel == nullptr) {
         return -1;
     }
-    dim3 grid(static_cast<unsigned>((op.N + 3) / 4), static_cast<unsigned>(batches));
     hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, op, ep);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
