@@ -318,6 +318,7 @@ float RoundBf16(float f)
 // ---------------------------------------------------------------------------------------------------
 // the GEMM core plan: one (possibly batched) GEMM launch plus its operand packs
 
+// ENGINE_MFMA_BF16 and ENGINE_SKINNY_BF16 run the 16- and 8-bit operand types (bf16, f16; s8 on the MFMA engine only).
 enum Engine { ENGINE_MFMA_BF16 = 1, ENGINE_MFMA_F32 = 2, ENGINE_SKINNY_BF16 = 3 };
 
 struct OperandSpec {
@@ -369,7 +370,7 @@ void BatchStrides(const kudnn_tensor_desc &t, int64_t bs[3], int64_t dims[3])
     }
 }
 
-int ElemsPerChunk(int computeDt) { return computeDt == KUDNN_DT_F32 ? 4 : 8; }
+int ElemsPerChunk(int computeDt) { return 16 / DtSize(computeDt); }
 
 // Builds the core plan of C = A x B (+ bias) from validated descriptors. Returns a status.
 // `extra` lists further m-indexed epilogue tensors (linearRes, the binary operand) that must allow a batch
@@ -385,13 +386,32 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
     core.N = b.dims[nd - 1];
 
     // dtype combination -> compute type (the registry of kudnn_gemm.cpp:590-601 and the widening / all-f32
-    // fallback of ChooseImpl, :628-708)
+    // fallback of ChooseImpl, :628-708):
+    //  - bf16 x bf16: bf16 MFMA (cblas_sbgemm / cblas_bgemm);
+    //  - f16 x f16, f16 x s8, f16 x u8: f16 MFMA (cblas_hgemm / cblas_shgemm; an 8-bit weight is converted to f16
+    //    exactly, as the reference's MatrixConverter does before hgemm, :341-372);
+    //  - s8 x s8 -> s32 (bias s32 or none): int8 MFMA into exact int32 (cblas_gemm_s8s8s32, :243-264);
+    //  - integer operands with a floating output: the all-f32 fallback (the operands are converted exactly);
+    //  - the u8 and mixed-sign integer GEMMs into s32, and a floating GEMM into an integer output, have no restatable
+    //    semantics here (closed KML routines, or ConvertFp32ToS32 of a rounded f32 sum) and are refused;
+    //  - everything else computes in f32.
     const int biasDt = IsNone(bias) ? c.dtype : bias->dtype;
-    if (!IsFp(a.dtype) || !IsFp(b.dtype) || !IsFp(c.dtype) || !IsFp(biasDt)) {
-        return Fail(KUDNN_STATUS_UNSUPPORTED,
-                    std::string(op) + ": integer element types are not implemented on the MI355X path");
+    const bool intOut = !IsFp(c.dtype) || !IsFp(biasDt);
+    if (intOut) {
+        if (!(a.dtype == KUDNN_DT_S8 && b.dtype == KUDNN_DT_S8 && c.dtype == KUDNN_DT_S32 && biasDt == KUDNN_DT_S32)) {
+            return Fail(KUDNN_STATUS_UNSUPPORTED,
+                        std::string(op) + ": the only integer output implemented on the MI355X path is s8 x s8 -> s32 "
+                                          "(with an s32 bias or none)");
+        }
+        core.computeDt = KUDNN_DT_S8;
+    } else if (a.dtype == KUDNN_DT_BF16 && b.dtype == KUDNN_DT_BF16) {
+        core.computeDt = KUDNN_DT_BF16;
+    } else if (a.dtype == KUDNN_DT_F16 &&
+               (b.dtype == KUDNN_DT_F16 || b.dtype == KUDNN_DT_S8 || b.dtype == KUDNN_DT_U8)) {
+        core.computeDt = KUDNN_DT_F16;
+    } else {
+        core.computeDt = KUDNN_DT_F32;
     }
-    core.computeDt = (a.dtype == KUDNN_DT_BF16 && b.dtype == KUDNN_DT_BF16) ? KUDNN_DT_BF16 : KUDNN_DT_F32;
 
     // batch dims
     int64_t aDims[3], bDims[3], cDims[3], tmp[3];
@@ -464,10 +484,11 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
     // Operands the MFMA kernels cannot read in place: wrong dtype, not contiguous along K, or rows /
     // batches not aligned to 16-byte chunks.
     const int epc = ElemsPerChunk(core.computeDt);
-    const int64_t bk = core.computeDt == KUDNN_DT_F32 ? 32 : 64;
+    const int64_t bk = 128 / DtSize(core.computeDt);  // k-tile: 128 bytes of each row
+    const bool lowp16 = core.computeDt == KUDNN_DT_BF16 || core.computeDt == KUDNN_DT_F16;
     // The MFMA kernels need K to be a whole number of k-tiles (a padded pack provides it); the skinny
     // kernel masks its K tail itself.
-    const bool kTiles = core.M <= 16 && core.computeDt == KUDNN_DT_BF16 ? true : (core.K % bk == 0);
+    const bool kTiles = core.M <= 16 && lowp16 ? true : (core.K % bk == 0);
     auto needsPack = [&](const OperandSpec &o) {
         bool direct = o.dt == core.computeDt && (o.s_k == 1) && (core.K % epc == 0) && (o.s_r % epc == 0) && kTiles;
         for (int s = 0; s < 3; ++s) {
@@ -481,8 +502,8 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
 
     // engine and tile configuration
     const int64_t batches = core.Batches();
-    if (core.computeDt == KUDNN_DT_BF16) {
-        if (core.M <= 16) {
+    if (core.computeDt != KUDNN_DT_F32) {
+        if (core.M <= 16 && lowp16) {
             core.engine = ENGINE_SKINNY_BF16;
             core.cfg = core.M == 1 ? KUDNN_CFG_GEMV_BF16 : KUDNN_CFG_SKINNY_BF16;
         } else {
@@ -503,10 +524,10 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
     }
     if (const char *force = std::getenv("KUDNN_HIP_FORCE_CFG")) {
         int f = std::atoi(force);
-        bool okBf16 = core.computeDt == KUDNN_DT_BF16 &&
+        bool okBf16 = core.computeDt != KUDNN_DT_F32 &&
                       (f == KUDNN_CFG_BF16_256x256 || f == KUDNN_CFG_BF16_256x128 || f == KUDNN_CFG_BF16_128x128 ||
                        (f == KUDNN_CFG_BF16_PINGPONG_256x256 && core.M > 16) ||
-                       (f == KUDNN_CFG_SKINNY_BF16 && core.M <= 16));
+                       (f == KUDNN_CFG_SKINNY_BF16 && core.M <= 16 && lowp16));
         bool okF32 = core.computeDt == KUDNN_DT_F32 && (f == KUDNN_CFG_F32_128x128 || f == KUDNN_CFG_F32_64x64);
         if (okBf16 || okF32) {
             core.cfg = f;
@@ -534,8 +555,15 @@ const char *CfgName(int cfg)
 
 std::string DescribeCore(const GemmCore &c)
 {
+    // the 16- and 8-bit configurations carry the bf16 names; name the operand type actually computed
+    std::string cfg = CfgName(c.cfg);
+    const char *ct = c.computeDt == KUDNN_DT_F16 ? "f16" : (c.computeDt == KUDNN_DT_S8 ? "s8" : nullptr);
+    const size_t at = cfg.find("bf16");
+    if (ct != nullptr && at != std::string::npos) {
+        cfg.replace(at, 4, ct);
+    }
     char buf[256];
-    std::snprintf(buf, sizeof(buf), "%s M=%lld N=%lld K=%lld batches=%lld%s%s%s", CfgName(c.cfg),
+    std::snprintf(buf, sizeof(buf), "%s M=%lld N=%lld K=%lld batches=%lld%s%s%s", cfg.c_str(),
                   static_cast<long long>(c.M), static_cast<long long>(c.N), static_cast<long long>(c.K),
                   static_cast<long long>(c.Batches()), c.A.staticPack ? " packA" : "", c.B.staticPack ? " packB" : "",
                   c.serial ? " serial" : "");
@@ -727,7 +755,7 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
     shape.K = core.kp;
     const bool mfma4 = core.engine == ENGINE_MFMA_F32 ||
                        (core.engine == ENGINE_MFMA_BF16 && core.cfg != KUDNN_CFG_BF16_PINGPONG_256x256);
-    const size_t wsS = mfma4 ? align256(kudnn_gemm_workspace_bytes(shape, batches, core.cfg)) : 0;
+    const size_t wsS = mfma4 ? align256(kudnn_gemm_workspace_bytes(shape, batches, core.cfg, core.computeDt)) : 0;
     void *ws = nullptr;
     bool acquired = false;
     if (wsA + wsB + wsS > 0) {
@@ -823,15 +851,15 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
 
     int lrc = 0;
     if (core.engine == ENGINE_SKINNY_BF16) {
-        lrc = kudnn_launch_skinny_bf16(op, ep, batches, stream);
+        lrc = kudnn_launch_skinny(op, ep, batches, core.computeDt, stream);
     } else if (core.engine == ENGINE_MFMA_BF16) {
-        if (core.cfg == KUDNN_CFG_BF16_PINGPONG_256x256 && kudnn_pingpong_eligible(op)) {
-            lrc = kudnn_launch_gemm_bf16_pingpong(op, ep, batches, stream);
+        if (core.cfg == KUDNN_CFG_BF16_PINGPONG_256x256 && kudnn_pingpong_eligible(op, core.computeDt)) {
+            lrc = kudnn_launch_gemm_pingpong(op, ep, batches, core.computeDt, stream);
         } else {
             // operands the ping-pong kernel cannot address (e.g. offsets beyond 2 GiB) use the 4-wave kernel
             // (no split-K workspace was reserved for the ping-pong configuration: runs unsplit)
             const int cfg = core.cfg == KUDNN_CFG_BF16_PINGPONG_256x256 ? KUDNN_CFG_BF16_256x256 : core.cfg;
-            lrc = kudnn_launch_gemm_bf16(op, ep, batches, cfg, splitWs, stream);
+            lrc = kudnn_launch_gemm_mfma(op, ep, batches, cfg, core.computeDt, splitWs, stream);
         }
     } else {
         lrc = kudnn_launch_gemm_f32(op, ep, batches, core.cfg, splitWs, stream);
@@ -1202,6 +1230,10 @@ int kudnn_gemm_run(kudnn_gemm_t plan, const void *a, const void *b, void *c, con
     }
     hipStream_t st = static_cast<hipStream_t>(stream);
     const GemmCore &core = plan->core;
+    if (core.computeDt == KUDNN_DT_S8 && (alpha != 1.0f || beta != 0.0f)) {
+        // cblas_gemm_s8s8s32's scaling of an int32 result by float alpha / beta is KML-internal and unpinned
+        return Fail(KUDNN_STATUS_UNSUPPORTED, "GEMM: s8 x s8 -> s32 runs with alpha = 1 and beta = 0 only");
+    }
     // cblas_bgemm takes bf16 alpha/beta when a bf16 C has no bias (kudnn_gemm.cpp:222-226).
     if (!core.hasBias && core.C.dt == KUDNN_DT_BF16 && core.computeDt == KUDNN_DT_BF16) {
         alpha = RoundBf16(alpha);
@@ -1283,6 +1315,9 @@ int kudnn_linear_act_create(const kudnn_tensor_desc *a, const kudnn_tensor_desc 
     p->c = *c;
     CopyDesc(bias, p->bias);
     s = BuildCore(*a, *b, *c, &p->bias, p->core, "LinearActivationLayerFWD");
+    if (s == KUDNN_STATUS_SUCCESS && p->core.computeDt == KUDNN_DT_S8) {
+        s = Fail(KUDNN_STATUS_UNSUPPORTED, "LinearActivationLayerFWD: integer GEMMs run through Gemm only");
+    }
     if (s != KUDNN_STATUS_SUCCESS) {
         delete p;
         return s;
@@ -1386,8 +1421,14 @@ int kudnn_linear_res_create(const kudnn_tensor_desc *a, const kudnn_tensor_desc 
         p->x.Src = SpecOf(*linear_res);   // res is read in linearRes's memory order
         p->x.Src.dt = res->dtype;
         s = BuildCore(*a, *b, *c, &p->bias, p->core, "LinearResFWD", &p->x.Y, &p->x.Src);
+        if (s == KUDNN_STATUS_SUCCESS && p->core.computeDt == KUDNN_DT_S8) {
+            s = Fail(KUDNN_STATUS_UNSUPPORTED, "LinearResFWD: integer GEMMs run through Gemm only");
+        }
     } else {
         s = BuildCore(*a, *b, *c, &p->bias, p->core, "LinearResFWD");
+        if (s == KUDNN_STATUS_SUCCESS && p->core.computeDt == KUDNN_DT_S8) {
+            s = Fail(KUDNN_STATUS_UNSUPPORTED, "LinearResFWD: integer GEMMs run through Gemm only");
+        }
     }
     if (s == KUDNN_STATUS_SUCCESS && kind == KUDNN_RES_MUL) {
         kudnn_tensor_desc none{};
@@ -1535,6 +1576,9 @@ int kudnn_linear_postops_create(const kudnn_tensor_desc *a, const kudnn_tensor_d
         p->x.Src = SpecOf(*src);
     }
     s = BuildCore(*a, *b, *y, &p->bias, p->core, "LinearPostOpsFWD", p->x.hasSrc ? &p->x.Src : nullptr);
+    if (s == KUDNN_STATUS_SUCCESS && p->core.computeDt == KUDNN_DT_S8 && (act_kind != KUDNN_ACT_UNIMPLEMENTED || p->x.hasSrc)) {
+        s = Fail(KUDNN_STATUS_UNSUPPORTED, "LinearPostOpsFWD: an s8 x s8 -> s32 Linear takes no activation or binary operand");
+    }
     if (s != KUDNN_STATUS_SUCCESS) {
         delete p;
         return s;

@@ -77,23 +77,31 @@ __device__ __forceinline__ float round_store(int dt, float f)
     return f;
 }
 
+// Element of dtype dt as f32 (8-bit integers are exact; int32 rounds beyond 2^24 and is read this way only where the
+// values are small, as in operand packing).
 __device__ __forceinline__ float load_elem(const void *p, int dt, int64_t idx)
 {
     switch (dt) {
         case KUDNN_DT_F32: return static_cast<const float *>(p)[idx];
         case KUDNN_DT_BF16: return bf16_to_f32(static_cast<const uint16_t *>(p)[idx]);
         case KUDNN_DT_F16: return f16_to_f32(static_cast<const uint16_t *>(p)[idx]);
+        case KUDNN_DT_S8: return static_cast<float>(static_cast<const int8_t *>(p)[idx]);
+        case KUDNN_DT_U8: return static_cast<float>(static_cast<const uint8_t *>(p)[idx]);
+        case KUDNN_DT_S32: return static_cast<float>(static_cast<const int32_t *>(p)[idx]);
         default: return 0.0f;
     }
 }
 
-// Stores a value that is already rounded to dt (exact conversion), or rounds with RNE.
+// Stores a value that is already rounded to dt (exact conversion), or rounds with RNE. Integer stores take values
+// that are already integers in range (operand packing of 8-bit data).
 __device__ __forceinline__ void store_elem(void *p, int dt, int64_t idx, float v)
 {
     switch (dt) {
         case KUDNN_DT_F32: static_cast<float *>(p)[idx] = v; break;
         case KUDNN_DT_BF16: static_cast<uint16_t *>(p)[idx] = f32_to_bf16_rne(v); break;
         case KUDNN_DT_F16: static_cast<uint16_t *>(p)[idx] = f32_to_f16_rne(v); break;
+        case KUDNN_DT_S8: static_cast<int8_t *>(p)[idx] = static_cast<int8_t>(v); break;
+        case KUDNN_DT_U8: static_cast<uint8_t *>(p)[idx] = static_cast<uint8_t>(v); break;
         default: break;
     }
 }
@@ -188,14 +196,15 @@ __device__ __forceinline__ EpiBatch epi_batch_offsets(const EpiParams &e, int64_
     return o;
 }
 
-// Epilogue forms (the types of every epilogue tensor, fixed at compile time in the fast paths): all bf16, all f32, or
-// read at run time.
-enum { EPI_FORM_BF16 = 0, EPI_FORM_F32 = 1, EPI_FORM_GENERIC = 2 };
+// Epilogue forms (the types of every epilogue tensor, fixed at compile time in the fast paths): all bf16, all f32,
+// all f16, or read at run time; EPI_FORM_I32 is the integer epilogue of s8 x s8 -> s32 (further below). Value 3 is
+// taken by the split-K partial stores of gemm_mfma.hip.
+enum { EPI_FORM_BF16 = 0, EPI_FORM_F32 = 1, EPI_FORM_GENERIC = 2, EPI_FORM_I32 = 4, EPI_FORM_F16 = 5 };
 
 template <int FORM>
 constexpr int form_dt()
 {
-    return FORM == EPI_FORM_BF16 ? KUDNN_DT_BF16 : KUDNN_DT_F32;
+    return FORM == EPI_FORM_BF16 ? KUDNN_DT_BF16 : (FORM == EPI_FORM_F16 ? KUDNN_DT_F16 : KUDNN_DT_F32);
 }
 
 // Raw bits of one element of dtype dt (f32: 32 bits; bf16 / f16: 16 bits, zero-extended).
@@ -530,15 +539,19 @@ __device__ __forceinline__ void epi_apply8(const EpiParams &e, const EpiBatch &o
 // (fast8 must hold); a kernel that stores single elements passes false.
 inline int epi_form(const EpiParams &e, bool need8 = true)
 {
+    const int dt = e.y_dt;
+    if (dt == KUDNN_DT_S32) {
+        // the only epilogue of an integer output (the host admits no other options); it checks fast8 itself
+        return EPI_FORM_I32;
+    }
     if ((need8 && !e.fast8) || e.store_c || e.beta != 0.0f) {
         return EPI_FORM_GENERIC;
     }
-    const int dt = e.y_dt;
-    if ((dt != KUDNN_DT_BF16 && dt != KUDNN_DT_F32) || e.c_dt != dt || (e.bin != KUDNN_BINARY_NONE && e.src_dt != dt) ||
-        (e.bias != nullptr && e.bias_dt != dt)) {
+    if ((dt != KUDNN_DT_BF16 && dt != KUDNN_DT_F32 && dt != KUDNN_DT_F16) || e.c_dt != dt ||
+        (e.bin != KUDNN_BINARY_NONE && e.src_dt != dt) || (e.bias != nullptr && e.bias_dt != dt)) {
         return EPI_FORM_GENERIC;
     }
-    return dt == KUDNN_DT_BF16 ? EPI_FORM_BF16 : EPI_FORM_F32;
+    return dt == KUDNN_DT_BF16 ? EPI_FORM_BF16 : (dt == KUDNN_DT_F16 ? EPI_FORM_F16 : EPI_FORM_F32);
 }
 
 template <int ACT>
@@ -571,7 +584,7 @@ template <int FORM>
 __device__ __forceinline__ Raw8 load_raw8(const void *p, int64_t idx)
 {
     Raw8 r{make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
-    if constexpr (FORM == EPI_FORM_BF16) {
+    if constexpr (FORM == EPI_FORM_BF16 || FORM == EPI_FORM_F16) {
         r.lo = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p) + idx);
     } else {
         const uint4 *q = reinterpret_cast<const uint4 *>(static_cast<const float *>(p) + idx);
@@ -590,6 +603,12 @@ __device__ __forceinline__ void unpack_raw8(const Raw8 &r, float v[8])
         for (int q = 0; q < 4; ++q) {
             v[2 * q] = u2f(w[q] << 16);
             v[2 * q + 1] = u2f(w[q] & 0xffff0000u);
+        }
+    } else if constexpr (FORM == EPI_FORM_F16) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            v[2 * q] = f16_to_f32(static_cast<uint16_t>(w[q]));
+            v[2 * q + 1] = f16_to_f32(static_cast<uint16_t>(w[q] >> 16));
         }
     } else {
 #pragma unroll
@@ -652,6 +671,9 @@ __device__ __forceinline__ void epi_fast8(const EpiParams &e, const EpiBatch &ob
     if constexpr (DT == KUDNN_DT_BF16) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) round_bf16_pair(v[2 * q], v[2 * q + 1]);
+    } else if constexpr (DT == KUDNN_DT_F16) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = round_store(DT, v[q]);
     }
     if constexpr (ACT != KUDNN_ACT_UNIMPLEMENTED) {
 #pragma unroll
@@ -676,6 +698,13 @@ __device__ __forceinline__ void epi_fast8(const EpiParams &e, const EpiBatch &ob
         uint32_t w[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) w[q] = pack_bf16x2_rne(v[2 * q], v[2 * q + 1]);
+        *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(e.y) + yi) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else if constexpr (FORM == EPI_FORM_F16) {
+        uint32_t w[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            w[q] = static_cast<uint32_t>(f32_to_f16_rne(v[2 * q])) | (static_cast<uint32_t>(f32_to_f16_rne(v[2 * q + 1])) << 16);
+        }
         *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(e.y) + yi) = make_uint4(w[0], w[1], w[2], w[3]);
     } else {
         float *yp = static_cast<float *>(e.y) + yi;
@@ -735,6 +764,32 @@ __device__ __forceinline__ void epi_elem(const EpiParams &e, const EpiBatch &ob,
         }
     }
     store_elem(e.y, DT, ob.y + m * e.y_sm + n, v);
+}
+
+// Integer epilogue: s8 x s8 -> s32 (cblas_gemm_s8s8s32, src/dnn/src/kudnn_gemm.cpp:243-264, with the bias passed as
+// the C offset for a row / column vector and added afterwards for a full [M, N] bias: the same sum either way).
+// y = acc + bias in int32 with two's-complement wrap; alpha 1, beta 0, no activation or binary operand (the host
+// rejects anything else). The accumulators arrive as the bit patterns of the MFMA's int32 results.
+__device__ __forceinline__ uint32_t i32_bias(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n)
+{
+    return e.bias == nullptr ? 0u : static_cast<const uint32_t *>(e.bias)[ob.bias + m * e.bias_sm + n * e.bias_sn];
+}
+
+// 8 consecutive columns (m, n .. n+7), all in bounds, y contiguous along n with 16-byte aligned groups (fast8; callers
+// check it and use epi_i32_1 otherwise).
+__device__ __forceinline__ void epi_i32_8(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, const float acc[8])
+{
+    uint32_t v[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v[q] = f2u(acc[q]) + i32_bias(e, ob, m, n + q);
+    uint4 *y = reinterpret_cast<uint4 *>(static_cast<uint32_t *>(e.y) + ob.y + m * e.y_sm + n);
+    y[0] = make_uint4(v[0], v[1], v[2], v[3]);
+    y[1] = make_uint4(v[4], v[5], v[6], v[7]);
+}
+
+__device__ __forceinline__ void epi_i32_1(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, float acc)
+{
+    static_cast<uint32_t *>(e.y)[ob.y + m * e.y_sm + n * e.y_sn] = f2u(acc) + i32_bias(e, ob, m, n);
 }
 
 // XCD-aware block order. The hardware deals workgroups round-robin over the 8 XCDs (block b runs on

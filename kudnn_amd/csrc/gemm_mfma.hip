@@ -1,9 +1,9 @@
-// bf16 and fp32 GEMM on gfx950 MFMA with the fused epilogue.
+// bf16, f16, s8 and fp32 GEMM on gfx950 MFMA with the fused epilogue.
 //
 // Computes, per batch, Y = epilogue(A[M][K] x B[N][K]^T) with both operands contiguous along K
 // (A = activations/X rows, B = nn.Linear-style weight rows). This is the kernel behind cblas_sbgemm /
-// cblas_bgemm (bf16) and cblas_sgemm (fp32) in the reference (src/dnn/src/kudnn_gemm.cpp:157-241) plus
-// its post-op passes.
+// cblas_bgemm (bf16), cblas_hgemm / cblas_shgemm (f16), cblas_gemm_s8s8s32 (s8 -> s32) and cblas_sgemm (fp32) in the
+// reference (src/dnn/src/kudnn_gemm.cpp:157-264) plus its post-op passes.
 //
 // Design (one workgroup of 4 waves per BM x BN output tile, waves arranged 2 x 2):
 //  - k-tiles of 128 bytes per row (64 bf16 / 32 fp32) go straight from global memory into LDS with
@@ -14,8 +14,12 @@
 //    global chunk that the XOR swizzle (chunk ^ (row & 7)) assigns to that slot, so the ds_read_b128 of
 //    32 consecutive rows at one logical k-chunk hits every bank once.
 //  - MFMA fragments of k16-substep s+1 are read from LDS while substep s's MFMAs issue.
-//  - bf16: v_mfma_f32_32x32x16_bf16; fp32: v_mfma_f32_32x32x2f32 fed from one 16-byte LDS read per lane
-//    (four k values; MFMA q consumes element q of both lane halves, which covers every k exactly once).
+//  - bf16: v_mfma_f32_32x32x16_bf16; f16: v_mfma_f32_32x32x16_f16; s8: v_mfma_i32_32x32x32_i8 (int32 accumulators,
+//    kept in the same registers as bit patterns); fp32: v_mfma_f32_32x32x2f32 fed from one 16-byte LDS read per lane
+//    (four k values; MFMA q consumes element q of both lane halves, which covers every k exactly once). The 16- and
+//    8-bit instructions all take 16 bytes of one row per lane, lane half h holding bytes 16h .. 16h+15 of each
+//    32-byte k step for both operands, so one data path serves all three: the sum over k does not depend on how the
+//    hardware orders the k values inside a lane, as long as both operands use the same order.
 //  - The operands are swapped (weight tile as the first MFMA operand): each lane then owns, per 32x32
 //    sub-tile, one output row m and four runs of four consecutive columns n.
 //  - Epilogue: the accumulators pass through LDS, one 32-column strip per wave at a time, and are read
@@ -42,6 +46,9 @@ using namespace kudnn_dev;
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
@@ -93,11 +100,13 @@ __device__ __forceinline__ void static_for(F &&f)
 // Raw f32 partial tiles of a split-K launch: split z of output (m, n) at partial[z * M * N + m * N + n].
 constexpr int EPI_FORM_PARTIAL = 3;
 
-template <bool F32, int BM, int BN, int WM, int WN, int ST, int ACT, int FORM>
+// CT: compute (operand) type, KUDNN_DT_F32 / BF16 / F16 / S8.
+template <int CT, int BM, int BN, int WM, int WN, int ST, int ACT, int FORM>
 __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands op, EpiParams ep, int tilesM,
                                                                   int tilesN, int group, float *partial)
 {
-    using T = typename std::conditional<F32, float, uint16_t>::type;
+    constexpr bool F32 = CT == KUDNN_DT_F32;
+    using T = typename std::conditional<F32, float, typename std::conditional<CT == KUDNN_DT_S8, int8_t, uint16_t>::type>::type;
     constexpr int EPC = 16 / static_cast<int>(sizeof(T));  // elements per 16-byte chunk
     constexpr int kBK = kChunks * EPC;                      // k-tile in elements
     constexpr int NW = WM * WN;                             // waves
@@ -245,9 +254,18 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
                 for (int j = 0; j < FN; ++j) {
 #pragma unroll
                     for (int i = 0; i < FM; ++i) {
-                        acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vb[sl][j]),
-                                                                            __builtin_bit_cast(bf16x8_t, va[sl][i]),
-                                                                            acc[j][i], 0, 0, 0);
+                        if constexpr (CT == KUDNN_DT_BF16) {
+                            acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                                __builtin_bit_cast(bf16x8_t, vb[sl][j]), __builtin_bit_cast(bf16x8_t, va[sl][i]), acc[j][i], 0, 0, 0);
+                        } else if constexpr (CT == KUDNN_DT_F16) {
+                            acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                                __builtin_bit_cast(f16x8_t, vb[sl][j]), __builtin_bit_cast(f16x8_t, va[sl][i]), acc[j][i], 0, 0, 0);
+                        } else {
+                            acc[j][i] = __builtin_bit_cast(
+                                f32x16_t, __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4_t, vb[sl][j]),
+                                                                               __builtin_bit_cast(i32x4_t, va[sl][i]),
+                                                                               __builtin_bit_cast(i32x16_t, acc[j][i]), 0, 0, 0));
+                        }
                     }
                 }
             }
@@ -289,6 +307,25 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
                 for (int q = 0; q < 8; ++q) {
                     if (n + q < N) {
                         part[m * N + n + q] = src[q];
+                    }
+                }
+            }
+        } else if constexpr (FORM == EPI_FORM_I32) {
+#pragma unroll 1
+            for (int r = lane >> 2; r < TM; r += 16) {
+                const int64_t m = m0 + wm * TM + r;
+                const float *src = stage + r * kStagePitch + col8;
+                if (ep.fast8 && (full || (m < M && n + 7 < N))) {
+                    const float4 lo = *reinterpret_cast<const float4 *>(src);
+                    const float4 hi = *reinterpret_cast<const float4 *>(src + 4);
+                    const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                    epi_i32_8(ep, ob, m, n, v);
+                } else if (m < M) {
+#pragma unroll 1
+                    for (int q = 0; q < 8; ++q) {
+                        if (n + q < N) {
+                            epi_i32_1(ep, ob, m, n + q, src[q]);
+                        }
                     }
                 }
             }
@@ -378,54 +415,67 @@ int splitk_splits(const GemmOperands &op, int64_t batches, int BM, int BN, int k
     return static_cast<int>(std::min<int64_t>(KT / 4, (384 + tiles - 1) / tiles));
 }
 
-template <bool F32, int BM, int BN, int WM, int WN, int ST>
+template <int CT, int BM, int BN, int WM, int WN, int ST>
 int launch_cfg(const GemmOperands &op, const EpiParams &ep, int64_t batches, int group, void *ws, hipStream_t stream)
 {
-    constexpr int kBK = F32 ? 32 : 64;
+    constexpr int kBK = CT == KUDNN_DT_F32 ? 32 : (CT == KUDNN_DT_S8 ? 128 : 64);
     if (op.K % kBK != 0) {
         return -1;  // the dispatcher pads K by packing
     }
     const int tilesM = static_cast<int>((op.M + BM - 1) / BM);
     const int tilesN = static_cast<int>((op.N + BN - 1) / BN);
     dim3 block(WM * WN * 64);
+    dim3 grid(static_cast<unsigned>(tilesM * tilesN), static_cast<unsigned>(batches));
+    if constexpr (CT == KUDNN_DT_S8) {
+        // integer accumulators: no split-K (its partials are f32), one epilogue
+        if (epi_form(ep) != EPI_FORM_I32) {
+            return -1;
+        }
+        hipLaunchKernelGGL((gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, 0, EPI_FORM_I32>), grid, block, 0, stream, op, ep,
+                           tilesM, tilesN, group, static_cast<float *>(nullptr));
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    } else {
+        const int splits = ws != nullptr ? splitk_splits(op, batches, BM, BN, kBK) : 1;
+        if (splits > 1) {
+            float *partial = static_cast<float *>(ws);
+            dim3 sgrid(static_cast<unsigned>(tilesM * tilesN), 1, static_cast<unsigned>(splits));
+            hipLaunchKernelGGL((gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, 0, EPI_FORM_PARTIAL>), sgrid, block, 0, stream, op,
+                               ep, tilesM, tilesN, group, partial);
+            const int64_t threads = op.M * ((op.N + 3) / 4);
+            hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
+                               stream, partial, splits, op.M, op.N, ep);
+            return hipGetLastError() == hipSuccess ? 0 : -1;
+        }
 
-    const int splits = ws != nullptr ? splitk_splits(op, batches, BM, BN, kBK) : 1;
-    if (splits > 1) {
-        float *partial = static_cast<float *>(ws);
-        dim3 grid(static_cast<unsigned>(tilesM * tilesN), 1, static_cast<unsigned>(splits));
-        hipLaunchKernelGGL((gemm_mfma_kernel<F32, BM, BN, WM, WN, ST, 0, EPI_FORM_PARTIAL>), grid, block, 0, stream, op, ep,
-                           tilesM, tilesN, group, partial);
-        const int64_t threads = op.M * ((op.N + 3) / 4);
-        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, stream,
-                           partial, splits, op.M, op.N, ep);
+        // the activation and the epilogue's tensor types select one of the compiled variants
+        decltype(&gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, 0, EPI_FORM_GENERIC>) kernel = nullptr;
+        // the fixed form compiled for this compute type
+        constexpr int kForm = CT == KUDNN_DT_F32 ? EPI_FORM_F32 : (CT == KUDNN_DT_F16 ? EPI_FORM_F16 : EPI_FORM_BF16);
+        if (epi_form(ep) == kForm) {
+            switch (ep.act) {
+                case KUDNN_ACT_UNIMPLEMENTED: kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_UNIMPLEMENTED, kForm>; break;
+                case KUDNN_ACT_RELU: kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_RELU, kForm>; break;
+                case KUDNN_ACT_SWISH: kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_SWISH, kForm>; break;
+                case KUDNN_ACT_GELU_TANH: kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_GELU_TANH, kForm>; break;
+                case KUDNN_ACT_GELU_ERF: kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_GELU_ERF, kForm>; break;
+                default: break;
+            }
+        }
+        if (kernel == nullptr) {
+            kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, 0, EPI_FORM_GENERIC>;  // reads the activation at run time
+        }
+        hipLaunchKernelGGL(kernel, grid, block, 0, stream, op, ep, tilesM, tilesN, group, static_cast<float *>(nullptr));
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
-
-    // the activation and the epilogue's tensor types select one of the compiled variants
-    decltype(&gemm_mfma_kernel<F32, BM, BN, WM, WN, ST, 0, EPI_FORM_GENERIC>) kernel = nullptr;
-    constexpr int kForm = F32 ? EPI_FORM_F32 : EPI_FORM_BF16;  // the fixed form compiled for this compute type
-    if (epi_form(ep) == kForm) {
-        switch (ep.act) {
-            case KUDNN_ACT_UNIMPLEMENTED: kernel = gemm_mfma_kernel<F32, BM, BN, WM, WN, ST, KUDNN_ACT_UNIMPLEMENTED, kForm>; break;
-            case KUDNN_ACT_RELU: kernel = gemm_mfma_kernel<F32, BM, BN, WM, WN, ST, KUDNN_ACT_RELU, kForm>; break;
-            case KUDNN_ACT_SWISH: kernel = gemm_mfma_kernel<F32, BM, BN, WM, WN, ST, KUDNN_ACT_SWISH, kForm>; break;
-            case KUDNN_ACT_GELU_TANH: kernel = gemm_mfma_kernel<F32, BM, BN, WM, WN, ST, KUDNN_ACT_GELU_TANH, kForm>; break;
-            case KUDNN_ACT_GELU_ERF: kernel = gemm_mfma_kernel<F32, BM, BN, WM, WN, ST, KUDNN_ACT_GELU_ERF, kForm>; break;
-            default: break;
-        }
-    }
-    if (kernel == nullptr) {
-        kernel = gemm_mfma_kernel<F32, BM, BN, WM, WN, ST, 0, EPI_FORM_GENERIC>;  // reads the activation at run time
-    }
-    dim3 grid(static_cast<unsigned>(tilesM * tilesN), static_cast<unsigned>(batches));
-    hipLaunchKernelGGL(kernel, grid, block, 0, stream, op, ep, tilesM, tilesN, group, static_cast<float *>(nullptr));
-    return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 }  // namespace
 
-size_t kudnn_gemm_workspace_bytes(const GemmOperands &op, int64_t batches, int cfg)
+size_t kudnn_gemm_workspace_bytes(const GemmOperands &op, int64_t batches, int cfg, int ct)
 {
+    if (ct == KUDNN_DT_S8) {
+        return 0;  // integer launches are never split
+    }
     int bm = 0, bn = 0, bk = 0;
     switch (cfg) {
         case KUDNN_CFG_BF16_256x256: bm = 256; bn = 256; bk = 64; break;
@@ -439,13 +489,28 @@ size_t kudnn_gemm_workspace_bytes(const GemmOperands &op, int64_t batches, int c
     return splits > 1 ? static_cast<size_t>(splits) * op.M * op.N * sizeof(float) : 0;
 }
 
-int kudnn_launch_gemm_bf16(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, void *ws,
-                           hipStream_t stream)
+namespace {
+
+template <int CT>
+int launch_lowp(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, void *ws, hipStream_t stream)
 {
     switch (cfg) {
-        case KUDNN_CFG_BF16_256x256: return launch_cfg<false, 256, 256, 2, 2, 2>(op, ep, batches, 8, ws, stream);
-        case KUDNN_CFG_BF16_256x128: return launch_cfg<false, 256, 128, 2, 2, 3>(op, ep, batches, 8, ws, stream);
-        case KUDNN_CFG_BF16_128x128: return launch_cfg<false, 128, 128, 2, 2, 4>(op, ep, batches, 8, ws, stream);
+        case KUDNN_CFG_BF16_256x256: return launch_cfg<CT, 256, 256, 2, 2, 2>(op, ep, batches, 8, ws, stream);
+        case KUDNN_CFG_BF16_256x128: return launch_cfg<CT, 256, 128, 2, 2, 3>(op, ep, batches, 8, ws, stream);
+        case KUDNN_CFG_BF16_128x128: return launch_cfg<CT, 128, 128, 2, 2, 4>(op, ep, batches, 8, ws, stream);
+        default: return -1;
+    }
+}
+
+}  // namespace
+
+int kudnn_launch_gemm_mfma(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, int ct, void *ws,
+                           hipStream_t stream)
+{
+    switch (ct) {
+        case KUDNN_DT_BF16: return launch_lowp<KUDNN_DT_BF16>(op, ep, batches, cfg, ws, stream);
+        case KUDNN_DT_F16: return launch_lowp<KUDNN_DT_F16>(op, ep, batches, cfg, ws, stream);
+        case KUDNN_DT_S8: return launch_lowp<KUDNN_DT_S8>(op, ep, batches, cfg, nullptr, stream);
         default: return -1;
     }
 }
@@ -456,8 +521,8 @@ int kudnn_launch_gemm_f32(const GemmOperands &op, const EpiParams &ep, int64_t b
     switch (cfg) {
         // 128 x 128 serves grids of >= 256 tiles: two stages keep two workgroups per CU, which hides latency better
         // than a deeper ring at one workgroup per CU
-        case KUDNN_CFG_F32_128x128: return launch_cfg<true, 128, 128, 2, 2, 2>(op, ep, batches, 8, ws, stream);
-        case KUDNN_CFG_F32_64x64: return launch_cfg<true, 64, 64, 2, 2, 4>(op, ep, batches, 8, ws, stream);
+        case KUDNN_CFG_F32_128x128: return launch_cfg<KUDNN_DT_F32, 128, 128, 2, 2, 2>(op, ep, batches, 8, ws, stream);
+        case KUDNN_CFG_F32_64x64: return launch_cfg<KUDNN_DT_F32, 64, 64, 2, 2, 4>(op, ep, batches, 8, ws, stream);
         default: return -1;
     }
 }

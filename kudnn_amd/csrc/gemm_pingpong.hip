@@ -1,7 +1,12 @@
-// bf16 GEMM on gfx950 MFMA, 8-wave ping-pong schedule, 256 x 256 output tile, k-tile 64, fused epilogue.
+// bf16 / f16 / s8 GEMM on gfx950 MFMA, 8-wave ping-pong schedule, 256 x 256 output tile, k-tile of 128 bytes
+// (64 bf16 or f16, 128 s8), fused epilogue.
 //
-// This is the kernel behind cblas_sbgemm / cblas_bgemm in the reference (src/dnn/src/kudnn_gemm.cpp:208-241)
-// for large M: Y = epilogue(A[M][K] x B[N][K]^T), both operands contiguous along K.
+// This is the kernel behind cblas_sbgemm / cblas_bgemm, cblas_hgemm / cblas_shgemm and cblas_gemm_s8s8s32 in the
+// reference (src/dnn/src/kudnn_gemm.cpp:182-264) for large M: Y = epilogue(A[M][K] x B[N][K]^T), both operands
+// contiguous along K. The three element types share the data path byte for byte: each MFMA
+// (v_mfma_f32_32x32x16_bf16 / _f16, v_mfma_i32_32x32x32_i8) takes 16 bytes of a row per lane, lane half h holding
+// bytes 16h .. 16h+15 of each 32-byte k step for both operands; s8 accumulates in int32 (the same registers, as bit
+// patterns) and ends in the exact integer epilogue.
 //
 // Why this schedule. On gfx950 a wave that issues a global->LDS copy (buffer_load ... lds) stalls until the
 // texture-address unit accepts it, about 22 cycles per 1 KB instruction per CU (measured; the cost is per 128-byte
@@ -42,10 +47,13 @@ using namespace kudnn_dev;
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kBM = 256, kBN = 256, kKC = 8, kBK = 64;
+constexpr int kBM = 256, kBN = 256, kKC = 8, kRowBytes = 128;  // k-tile: 128 bytes of each row
 constexpr int kTile = 256 * kKC;        // uint4 per A or B tile buffer (32 KB)
 constexpr int kPitch = 36;              // epilogue staging pitch in floats (32 columns + 4)
 
@@ -69,16 +77,15 @@ __device__ __forceinline__ void wait_vmcnt()
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 // One 1 KB copy global -> LDS of an 8-row block through a raw buffer resource. The resource starts at the block's
-// first element (wave-uniform `elemOff` from `base`) and covers the bytes of the operand that remain after it, so the
-// hardware range check, which applies to the per-lane offset `voff` only, turns rows past the end of the operand
-// into zeros instead of reads outside the allocation.
-__device__ __forceinline__ void copy_block(const uint16_t *base, uint32_t totalBytes, uint32_t elemOff, uint32_t voff, uint4 *dst)
+// first byte (wave-uniform byte offset `off` from `base`) and covers the bytes of the operand that remain after it,
+// so the hardware range check, which applies to the per-lane offset `voff` only, turns rows past the end of the
+// operand into zeros instead of reads outside the allocation.
+__device__ __forceinline__ void copy_block(const uint8_t *base, uint32_t totalBytes, uint32_t off, uint32_t voff, uint4 *dst)
 {
-    const uint32_t off = elemOff * 2u;
     // the clamped difference is a saturating subtract, which only the vector ALU has; without readfirstlane the
     // resource would look divergent and every copy would be wrapped in a waterfall loop
     const uint32_t remain = __builtin_amdgcn_readfirstlane(off < totalBytes ? totalBytes - off : 0u);
-    __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)(base + elemOff), (short)0, (int)remain, 0x00020000);
+    __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)(base + off), (short)0, (int)remain, 0x00020000);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)dst, 16, voff, 0, 0, 0);
 }
 
@@ -106,27 +113,28 @@ __device__ __forceinline__ void wave_sync()
 
 // Epilogue of a full tile (all rows and columns in bounds) in a fixed form, with no bias or a bias that is one row
 // broadcast over m: lane -> row rl + 16 * pass, columns col8 .. +8 of each strip. The bias and binary operand of
-// two strips are in flight at a time (strip j + 2's loads are issued once strip j is stored), and those of strips 0
-// and 1 are issued before the barrier that ends the main loop, so one memory latency is exposed per tile instead of
-// one per strip. The bias is the same for the four rows a lane covers in a strip and is loaded once.
+// AHEAD strips are in flight at a time (strip j + AHEAD's loads are issued once strip j is stored), and the first
+// AHEAD strips' are issued before the barrier that ends the main loop, so one memory latency is exposed per tile
+// instead of one per strip. Two strips ahead for the 16-bit forms; the f32 form's operands are twice the registers,
+// so it runs one ahead. The bias is the same for the four rows a lane covers in a strip and is loaded once.
 template <int ACT, int FORM>
 __device__ __forceinline__ void epilogue_full(const EpiParams &ep, const EpiBatch &ob, const f32x16_t (&acc)[4][2],
                                               float *stage, int lane, int64_t mW, int64_t nW)
 {
+    constexpr int AHEAD = FORM == EPI_FORM_F32 ? 1 : 2;
     const int lrow = lane & 31, lh = lane >> 5;
     const int col8 = (lane & 3) * 8, rl = lane >> 2;
-    Raw8 src[2][4], bias[2];
+    Raw8 src[AHEAD][4], bias[AHEAD];
     auto fetch = [&](auto jc) __attribute__((always_inline)) {
         constexpr int j = decltype(jc)::value;
         const int64_t n = nW + j * 32 + col8;
-        bias[j & 1] = epi_prefetch8_bias<FORM>(ep, ob, mW + rl, n);
+        bias[j % AHEAD] = epi_prefetch8_bias<FORM>(ep, ob, mW + rl, n);
         sfor<4>([&](auto pc) __attribute__((always_inline)) {
             constexpr int ps = decltype(pc)::value;
-            src[j & 1][ps] = epi_prefetch8_src<FORM>(ep, ob, mW + rl + ps * 16, n);
+            src[j % AHEAD][ps] = epi_prefetch8_src<FORM>(ep, ob, mW + rl + ps * 16, n);
         });
     };
-    fetch(std::integral_constant<int, 0>{});
-    fetch(std::integral_constant<int, 1>{});
+    sfor<AHEAD>([&](auto jc) __attribute__((always_inline)) { fetch(jc); });
     __syncthreads();  // every wave is done with the tile buffers that the staging area reuses
     sfor<4>([&](auto jc) __attribute__((always_inline)) {
         constexpr int j = decltype(jc)::value;
@@ -140,10 +148,10 @@ __device__ __forceinline__ void epilogue_full(const EpiParams &ep, const EpiBatc
             const float4 lo = *reinterpret_cast<const float4 *>(sp);
             const float4 hi = *reinterpret_cast<const float4 *>(sp + 4);
             const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-            epi_fast8<ACT, FORM>(ep, ob, mW + r, n, v, Pre8{src[j & 1][ps], bias[j & 1]});
+            epi_fast8<ACT, FORM>(ep, ob, mW + r, n, v, Pre8{src[j % AHEAD][ps], bias[j % AHEAD]});
         });
-        if constexpr (j + 2 < 4) {
-            fetch(std::integral_constant<int, j + 2>{});
+        if constexpr (j + AHEAD < 4) {
+            fetch(std::integral_constant<int, j + AHEAD>{});
         }
         wave_sync();
     });
@@ -215,10 +223,47 @@ __device__ __forceinline__ void epilogue_generic(const EpiParams &ep, const EpiB
     });
 }
 
-template <int ACT, int FORM>
-__global__ __launch_bounds__(512, 1) void gemm_bf16_pingpong_kernel(GemmOperands op, EpiParams ep, int tilesM,
-                                                                     int tilesN, int group)
+// Epilogue of the integer form (s8 x s8 -> s32): the accumulators hold int32 bit patterns; y = acc + bias exactly.
+__device__ __forceinline__ void epilogue_int(const EpiParams &ep, const EpiBatch &ob, const f32x16_t (&acc)[4][2],
+                                             float *stage, int lane, int64_t mW, int64_t nW, int64_t M, int64_t N)
 {
+    const int lrow = lane & 31, lh = lane >> 5;
+    const int col8 = (lane & 3) * 8, rl = lane >> 2;
+    __syncthreads();  // every wave is done with the tile buffers that the staging area reuses
+    sfor<4>([&](auto jc) __attribute__((always_inline)) {
+        constexpr int j = decltype(jc)::value;
+        const int64_t n = nW + j * 32 + col8;
+        stage_strip(acc[j], stage, lrow, lh);
+        wave_sync();
+#pragma unroll 1
+        for (int ps = 0; ps < 4; ++ps) {
+            const int r = rl + ps * 16;
+            const int64_t m = mW + r;
+            const float *src = stage + r * kPitch + col8;
+            if (ep.fast8 && m < M && n + 7 < N) {
+                const float4 lo = *reinterpret_cast<const float4 *>(src);
+                const float4 hi = *reinterpret_cast<const float4 *>(src + 4);
+                const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                epi_i32_8(ep, ob, m, n, v);
+            } else if (m < M) {
+#pragma unroll 1
+                for (int q = 0; q < 8; ++q) {
+                    if (n + q < N) {
+                        epi_i32_1(ep, ob, m, n + q, src[q]);
+                    }
+                }
+            }
+        }
+        wave_sync();
+    });
+}
+
+// CT: operand type, KUDNN_DT_BF16 / F16 / S8.
+template <int CT, int ACT, int FORM>
+__global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, EpiParams ep, int tilesM, int tilesN,
+                                                               int group)
+{
+    constexpr uint32_t ES = CT == KUDNN_DT_S8 ? 1u : 2u;  // element size in bytes
     __shared__ uint4 a0[kTile], a1[kTile], b0[kTile], b1[kTile], b2[kTile];
     auto abuf = [&](auto ic) __attribute__((always_inline)) -> uint4 * {
         if constexpr (decltype(ic)::value % 2 == 0) return a0; else return a1;
@@ -240,28 +285,28 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_pingpong_kernel(GemmOperands
     const int64_t i2 = batch % ep.bdim[2];
     const int64_t i1 = (batch / ep.bdim[2]) % ep.bdim[1];
     const int64_t i0 = batch / (ep.bdim[2] * ep.bdim[1]);
-    const uint16_t *A = static_cast<const uint16_t *>(op.a) + i0 * op.a_bs[0] + i1 * op.a_bs[1] + i2 * op.a_bs[2];
-    const uint16_t *B = static_cast<const uint16_t *>(op.b) + i0 * op.b_bs[0] + i1 * op.b_bs[1] + i2 * op.b_bs[2];
-    const uint32_t lda = static_cast<uint32_t>(op.lda), ldb = static_cast<uint32_t>(op.ldb);
-    const uint32_t bytesA = static_cast<uint32_t>(op.M) * lda * 2u, bytesB = static_cast<uint32_t>(op.N) * ldb * 2u;
+    const uint8_t *A = static_cast<const uint8_t *>(op.a) + (i0 * op.a_bs[0] + i1 * op.a_bs[1] + i2 * op.a_bs[2]) * ES;
+    const uint8_t *B = static_cast<const uint8_t *>(op.b) + (i0 * op.b_bs[0] + i1 * op.b_bs[1] + i2 * op.b_bs[2]) * ES;
+    const uint32_t lda = static_cast<uint32_t>(op.lda) * ES, ldb = static_cast<uint32_t>(op.ldb) * ES;  // row pitch, bytes
+    const uint32_t bytesA = static_cast<uint32_t>(op.M) * lda, bytesB = static_cast<uint32_t>(op.N) * ldb;
 
     // copy addressing: a 1 KB copy covers an 8-row block q (rows 8q .. 8q+7 of the tile); lane -> row lr, LDS slot ls,
     // source chunk ls ^ ((row >> 1) & 7) = ls ^ (4 * (q & 1) + (lr >> 1))
     const int lr = lane >> 3, ls = lane & 7;
-    const uint32_t loA0 = lr * lda * 2u + static_cast<uint32_t>((ls ^ (lr >> 1)) * 16);
-    const uint32_t loA1 = lr * lda * 2u + static_cast<uint32_t>((ls ^ (4 + (lr >> 1))) * 16);
-    const uint32_t loB0 = lr * ldb * 2u + static_cast<uint32_t>((ls ^ (lr >> 1)) * 16);
-    const uint32_t loB1 = lr * ldb * 2u + static_cast<uint32_t>((ls ^ (4 + (lr >> 1))) * 16);
+    const uint32_t loA0 = lr * lda + static_cast<uint32_t>((ls ^ (lr >> 1)) * 16);
+    const uint32_t loA1 = lr * lda + static_cast<uint32_t>((ls ^ (4 + (lr >> 1))) * 16);
+    const uint32_t loB0 = lr * ldb + static_cast<uint32_t>((ls ^ (lr >> 1)) * 16);
+    const uint32_t loB1 = lr * ldb + static_cast<uint32_t>((ls ^ (4 + (lr >> 1))) * 16);
     auto copyA = [&](int q, int t, uint4 *dst) __attribute__((always_inline)) {
-        copy_block(A, bytesA, static_cast<uint32_t>(m0 + q * 8) * lda + static_cast<uint32_t>(t * kBK), (q & 1) ? loA1 : loA0,
-                   dst + q * 8 * kKC);
+        copy_block(A, bytesA, static_cast<uint32_t>(m0 + q * 8) * lda + static_cast<uint32_t>(t * kRowBytes),
+                   (q & 1) ? loA1 : loA0, dst + q * 8 * kKC);
     };
     auto copyB = [&](int q, int t, uint4 *dst) __attribute__((always_inline)) {
-        copy_block(B, bytesB, static_cast<uint32_t>(n0 + q * 8) * ldb + static_cast<uint32_t>(t * kBK), (q & 1) ? loB1 : loB0,
-                   dst + q * 8 * kKC);
+        copy_block(B, bytesB, static_cast<uint32_t>(n0 + q * 8) * ldb + static_cast<uint32_t>(t * kRowBytes),
+                   (q & 1) ? loB1 : loB0, dst + q * 8 * kKC);
     };
     // the operand this wave streams inside the loop, selected once by value (group 0: A, group 1: B)
-    const uint16_t *sX = g == 0 ? A : B;
+    const uint8_t *sX = g == 0 ? A : B;
     const uint32_t sBytes = g == 0 ? bytesA : bytesB;
     const uint32_t sLd = g == 0 ? lda : ldb;
     const uint32_t sLo0 = g == 0 ? loA0 : loB0, sLo1 = g == 0 ? loA1 : loB1;
@@ -282,7 +327,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_pingpong_kernel(GemmOperands
         }
     }
     uint4 fa[4][2], fb[2][4];
-    const int KT = K / kBK;
+    const int KT = static_cast<int>(static_cast<uint32_t>(K) * ES / kRowBytes);
 
     // prologue: A(0), B(0), B(1); wave w copies 8-row blocks 4w .. 4w+3 of each
 #pragma unroll
@@ -325,7 +370,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_pingpong_kernel(GemmOperands
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const int q = p * 8 + j;
-                    copy_block(sX, sBytes, static_cast<uint32_t>(sR0 + q * 8) * sLd + static_cast<uint32_t>(tt * kBK),
+                    copy_block(sX, sBytes, static_cast<uint32_t>(sR0 + q * 8) * sLd + static_cast<uint32_t>(tt * kRowBytes),
                                (q & 1) ? sLo1 : sLo0, dst + q * 8 * kKC);
                 }
             }
@@ -346,8 +391,18 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_pingpong_kernel(GemmOperands
             for (int j = 0; j < 4; ++j) {
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
-                    acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fb[s & 1][j]),
-                                                                        __builtin_bit_cast(bf16x8_t, fa[s][i]), acc[j][i], 0, 0, 0);
+                    if constexpr (CT == KUDNN_DT_BF16) {
+                        acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fb[s & 1][j]),
+                                                                            __builtin_bit_cast(bf16x8_t, fa[s][i]), acc[j][i], 0, 0, 0);
+                    } else if constexpr (CT == KUDNN_DT_F16) {
+                        acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, fb[s & 1][j]),
+                                                                           __builtin_bit_cast(f16x8_t, fa[s][i]), acc[j][i], 0, 0, 0);
+                    } else {
+                        acc[j][i] = __builtin_bit_cast(
+                            f32x16_t, __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4_t, fb[s & 1][j]),
+                                                                           __builtin_bit_cast(i32x4_t, fa[s][i]),
+                                                                           __builtin_bit_cast(i32x16_t, acc[j][i]), 0, 0, 0));
+                    }
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -381,7 +436,9 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_pingpong_kernel(GemmOperands
     float *stage = reinterpret_cast<float *>(wave < 3 ? a0 : (wave < 6 ? a1 : b0)) + (wave % 3) * (64 * kPitch);
     const EpiBatch ob = epi_batch_offsets(ep, batch);
     const int64_t mW = m0 + p * 64, nW = n0 + g * 128;
-    if constexpr (FORM == EPI_FORM_GENERIC) {
+    if constexpr (FORM == EPI_FORM_I32) {
+        epilogue_int(ep, ob, acc, stage, lane, mW, nW, M, N);
+    } else if constexpr (FORM == EPI_FORM_GENERIC) {
         epilogue_generic(ep, ob, acc, stage, lane, mW, nW, M, N);
     } else if (m0 + kBM <= M && n0 + kBN <= N && (ep.bias == nullptr || ep.bias_sm == 0)) {
         epilogue_full<ACT, FORM>(ep, ob, acc, stage, lane, mW, nW);
@@ -392,45 +449,79 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_pingpong_kernel(GemmOperands
 
 }  // namespace
 
-bool kudnn_pingpong_eligible(const GemmOperands &op)
+bool kudnn_pingpong_eligible(const GemmOperands &op, int ct)
 {
     // whole k-tiles, 16-byte aligned rows, 32-bit buffer offsets
-    return op.K % kBK == 0 && op.lda % 8 == 0 && op.ldb % 8 == 0 && op.M * op.lda * 2 < (int64_t(1) << 31) &&
-           op.N * op.ldb * 2 < (int64_t(1) << 31) && op.K > 0;
+    const int64_t es = ct == KUDNN_DT_S8 ? 1 : 2;
+    return (ct == KUDNN_DT_BF16 || ct == KUDNN_DT_F16 || ct == KUDNN_DT_S8) && (op.K * es) % kRowBytes == 0 &&
+           (op.lda * es) % 16 == 0 && (op.ldb * es) % 16 == 0 && op.M * op.lda * es < (int64_t(1) << 31) &&
+           op.N * op.ldb * es < (int64_t(1) << 31) && op.K > 0;
 }
 
-int kudnn_launch_gemm_bf16_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream)
+namespace {
+
+template <int CT>
+int launch_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream)
 {
-    if (!kudnn_pingpong_eligible(op)) {
-        return -1;
-    }
     const int tilesM = static_cast<int>((op.M + kBM - 1) / kBM);
     const int tilesN = static_cast<int>((op.N + kBN - 1) / kBN);
     dim3 grid(static_cast<unsigned>(tilesM * tilesN), static_cast<unsigned>(batches));
     // the activation and the tensor types of the epilogue select one of the compiled variants
-    decltype(&gemm_bf16_pingpong_kernel<0, EPI_FORM_GENERIC>) kernel = nullptr;
+    decltype(&gemm_pingpong_kernel<CT, 0, EPI_FORM_GENERIC>) kernel = nullptr;
     const int form = epi_form(ep);
-    auto pick = [&](auto formc) {
-        constexpr int F = decltype(formc)::value;
-        switch (ep.act) {
-            case KUDNN_ACT_UNIMPLEMENTED: kernel = gemm_bf16_pingpong_kernel<KUDNN_ACT_UNIMPLEMENTED, F>; break;
-            case KUDNN_ACT_RELU: kernel = gemm_bf16_pingpong_kernel<KUDNN_ACT_RELU, F>; break;
-            case KUDNN_ACT_SWISH: kernel = gemm_bf16_pingpong_kernel<KUDNN_ACT_SWISH, F>; break;
-            case KUDNN_ACT_GELU_TANH: kernel = gemm_bf16_pingpong_kernel<KUDNN_ACT_GELU_TANH, F>; break;
-            case KUDNN_ACT_GELU_ERF: kernel = gemm_bf16_pingpong_kernel<KUDNN_ACT_GELU_ERF, F>; break;
-            default: break;
+    if constexpr (CT == KUDNN_DT_S8) {
+        if (form != EPI_FORM_I32) {
+            return -1;
         }
-    };
-    if (form == EPI_FORM_BF16) {
-        pick(std::integral_constant<int, EPI_FORM_BF16>{});
-    } else if (form == EPI_FORM_F32) {
-        pick(std::integral_constant<int, EPI_FORM_F32>{});
+        kernel = gemm_pingpong_kernel<CT, 0, EPI_FORM_I32>;
     } else {
-        kernel = gemm_bf16_pingpong_kernel<0, EPI_FORM_GENERIC>;  // reads the activation at run time
+        auto pick = [&](auto formc) {
+            constexpr int F = decltype(formc)::value;
+            switch (ep.act) {
+                case KUDNN_ACT_UNIMPLEMENTED: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_UNIMPLEMENTED, F>; break;
+                case KUDNN_ACT_RELU: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_RELU, F>; break;
+                case KUDNN_ACT_SWISH: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_SWISH, F>; break;
+                case KUDNN_ACT_GELU_TANH: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_GELU_TANH, F>; break;
+                case KUDNN_ACT_GELU_ERF: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_GELU_ERF, F>; break;
+                default: break;
+            }
+        };
+        // bf16 operands compile the bf16 and f32 output forms, f16 operands the f16 form; the rest is generic
+        if constexpr (CT == KUDNN_DT_BF16) {
+            if (form == EPI_FORM_BF16) {
+                pick(std::integral_constant<int, EPI_FORM_BF16>{});
+            } else if (form == EPI_FORM_F32) {
+                pick(std::integral_constant<int, EPI_FORM_F32>{});
+            }
+        } else {
+            if (form == EPI_FORM_F16) {
+                pick(std::integral_constant<int, EPI_FORM_F16>{});
+            }
+        }
+        if (kernel == nullptr && form != EPI_FORM_I32 && (ep.act == KUDNN_ACT_UNIMPLEMENTED || ep.act == KUDNN_ACT_RELU ||
+                                                          ep.act == KUDNN_ACT_SWISH || ep.act == KUDNN_ACT_GELU_TANH ||
+                                                          ep.act == KUDNN_ACT_GELU_ERF)) {
+            kernel = gemm_pingpong_kernel<CT, 0, EPI_FORM_GENERIC>;  // reads the activation at run time
+        }
     }
     if (kernel == nullptr) {
         return -1;  // not a fused activation
     }
     hipLaunchKernelGGL(kernel, grid, dim3(512), 0, stream, op, ep, tilesM, tilesN, 8);
     return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace
+
+int kudnn_launch_gemm_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, int ct, hipStream_t stream)
+{
+    if (!kudnn_pingpong_eligible(op, ct)) {
+        return -1;
+    }
+    switch (ct) {
+        case KUDNN_DT_BF16: return launch_pingpong<KUDNN_DT_BF16>(op, ep, batches, stream);
+        case KUDNN_DT_F16: return launch_pingpong<KUDNN_DT_F16>(op, ep, batches, stream);
+        case KUDNN_DT_S8: return launch_pingpong<KUDNN_DT_S8>(op, ep, batches, stream);
+        default: return -1;
+    }
 }

@@ -18,23 +18,27 @@ enum {
     KUDNN_CFG_GEMV_BF16 = 21,  // M == 1: one wave per weight row (skinny engine)
 };
 
-// Returns 0 on success, -1 if the launch failed or cfg is unknown.
+// Returns 0 on success, -1 if the launch failed or cfg is unknown. `ct` is the operand (compute) type of the 16- and
+// 8-bit kernels: KUDNN_DT_BF16, KUDNN_DT_F16 (f32 accumulation) or KUDNN_DT_S8 (int32 accumulation, integer
+// epilogue only). Their tile configurations keep the bf16 names; an s8 k-tile is 128 elements instead of 64.
 // 4-wave MFMA kernels (gemm_mfma.hip). A grid too small for the chip is split along K when `ws` (device memory of at
-// least kudnn_gemm_workspace_bytes bytes, 256-byte aligned) is given; with ws == nullptr it runs unsplit.
-size_t kudnn_gemm_workspace_bytes(const GemmOperands &op, int64_t batches, int cfg);
-int kudnn_launch_gemm_bf16(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, void *ws,
+// least kudnn_gemm_workspace_bytes bytes, 256-byte aligned) is given; with ws == nullptr it runs unsplit. s8 launches
+// are never split.
+size_t kudnn_gemm_workspace_bytes(const GemmOperands &op, int64_t batches, int cfg, int ct);
+int kudnn_launch_gemm_mfma(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, int ct, void *ws,
                            hipStream_t stream);
-// 8-wave ping-pong schedule, 256x256 tile (gemm_pingpong.hip). Needs K a multiple of 64, 16-byte aligned rows and
-// 32-bit operand offsets; kudnn_pingpong_eligible says whether `op` qualifies.
-bool kudnn_pingpong_eligible(const GemmOperands &op);
-int kudnn_launch_gemm_bf16_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream);
+// 8-wave ping-pong schedule, 256x256 tile (gemm_pingpong.hip). Needs K a whole number of 128-byte k-tiles, 16-byte
+// aligned rows and 32-bit operand offsets; kudnn_pingpong_eligible says whether `op` qualifies.
+bool kudnn_pingpong_eligible(const GemmOperands &op, int ct);
+int kudnn_launch_gemm_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, int ct, hipStream_t stream);
 int kudnn_launch_gemm_f32(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, void *ws,
                           hipStream_t stream);
-// M <= 16, bf16 operands, B contiguous along K (M == 1: row-per-wave GEMV, otherwise 16-row MFMA tiles).
-int kudnn_launch_skinny_bf16(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream);
+// M <= 16, bf16 or f16 operands (`ct`), B contiguous along K (M == 1: row-per-wave GEMV, otherwise 16-row MFMA tiles).
+int kudnn_launch_skinny(const GemmOperands &op, const EpiParams &ep, int64_t batches, int ct, hipStream_t stream);
 
 // Pack: dst[b][r][k] (row pitch kp, zero for k >= cols) = convert(src element (b, r, k)) where the source
-// element sits at src + b-offset + r*s_r + k*s_k. dst dtype is KUDNN_DT_BF16 or KUDNN_DT_F32.
+// element sits at src + b-offset + r*s_r + k*s_k. dst dtype is the compute type: F32, BF16, F16 or S8 (conversions are
+// exact: widening, 8-bit integers to f16 or f32, or a copy).
 struct PackArgs {
     const void *src;
     int src_dt;

@@ -1,4 +1,6 @@
-// Skinny-M (M <= 16) bf16 Linear for decode-shaped calls: Y = epilogue(X[M][K] x W[N][K]^T).
+// Skinny-M (M <= 16) bf16 / f16 Linear for decode-shaped calls: Y = epilogue(X[M][K] x W[N][K]^T). Every kernel here is
+// templated on the operand type CT (KUDNN_DT_BF16 or KUDNN_DT_F16): the MFMA (v_mfma_f32_16x16x32_bf16 / _f16) or the
+// conversion of the VALU dot product changes, nothing else.
 //
 // The reference reaches cblas_sgemv for m == 1 (src/dnn/src/kudnn_gemm.cpp:164-173) and cblas_sbgemm /
 // cblas_bgemm otherwise (:208-241). On MI355X this shape is bound by streaming W from HBM once, so the
@@ -19,10 +21,22 @@ using namespace kudnn_dev;
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-template <int KW, int UNR, bool KTAIL>
+// 16x16 MFMA step of the skinny kernels on 16-byte operand fragments of type CT.
+template <int CT>
+__device__ __forceinline__ f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t acc)
+{
+    if constexpr (CT == KUDNN_DT_F16) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), acc, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), acc, 0, 0, 0);
+    }
+}
+
+template <int CT, int KW, int UNR, bool KTAIL>
 __global__ __launch_bounds__(KW * 64) void skinny_bf16_kernel(GemmOperands op, EpiParams ep)
 {
     __shared__ f32x4_t part[KW][64];
@@ -71,8 +85,7 @@ __global__ __launch_bounds__(KW * 64) void skinny_bf16_kernel(GemmOperands op, E
         }
 #pragma unroll
         for (int u = 0; u < UNR; ++u) {
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, wv[u]),
-                                                          __builtin_bit_cast(bf16x8_t, xv[u]), acc, 0, 0, 0);
+            acc = mfma16<CT>(wv[u], xv[u], acc);
         }
     }
 
@@ -113,7 +126,7 @@ __global__ __launch_bounds__(KW * 64) void skinny_bf16_kernel(GemmOperands op, E
 // kernels) so the kernel's tail is short; batch indices are only decomposed when there is more than one batch.
 constexpr int kGemvCh = 8;  // chunks per lane per K block
 
-template <bool FULL>
+template <int CT, bool FULL>
 __device__ __forceinline__ float gemv_block(const uint16_t *X, const uint16_t *W, int c0, int chunks, int lane)
 {
     typedef uint32_t v4 __attribute__((ext_vector_type(4)));
@@ -137,14 +150,19 @@ __device__ __forceinline__ float gemv_block(const uint16_t *X, const uint16_t *W
         const uint32_t x[4] = {xv[c][0], xv[c][1], xv[c][2], xv[c][3]};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            sum = fmaf(u2f(w[j] << 16), u2f(x[j] << 16), sum);
-            sum = fmaf(u2f(w[j] & 0xffff0000u), u2f(x[j] & 0xffff0000u), sum);
+            if constexpr (CT == KUDNN_DT_F16) {
+                sum = fmaf(f16_to_f32(static_cast<uint16_t>(w[j])), f16_to_f32(static_cast<uint16_t>(x[j])), sum);
+                sum = fmaf(f16_to_f32(static_cast<uint16_t>(w[j] >> 16)), f16_to_f32(static_cast<uint16_t>(x[j] >> 16)), sum);
+            } else {
+                sum = fmaf(u2f(w[j] << 16), u2f(x[j] << 16), sum);
+                sum = fmaf(u2f(w[j] & 0xffff0000u), u2f(x[j] & 0xffff0000u), sum);
+            }
         }
     }
     return sum;
 }
 
-template <int ACT, int FORM>
+template <int CT, int ACT, int FORM>
 __global__ __launch_bounds__(256) void gemv_bf16_kernel(GemmOperands op, EpiParams ep)
 {
     const int lane = threadIdx.x & 63;
@@ -172,10 +190,10 @@ __global__ __launch_bounds__(256) void gemv_bf16_kernel(GemmOperands op, EpiPara
     float sum = 0.0f;
     int c0 = 0;
     for (; c0 + kGemvCh * 64 <= chunks; c0 += kGemvCh * 64) {
-        sum += gemv_block<true>(X, W, c0, chunks, lane);
+        sum += gemv_block<CT, true>(X, W, c0, chunks, lane);
     }
     if (c0 < chunks) {
-        sum += gemv_block<false>(X, W, c0, chunks, lane);
+        sum += gemv_block<CT, false>(X, W, c0, chunks, lane);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -206,7 +224,7 @@ struct GemvArgs {
     int bin;
 };
 
-template <int ACT, int FORM>
+template <int CT, int ACT, int FORM>
 __global__ __launch_bounds__(256) void gemv_bf16_compact_kernel(GemvArgs a)
 {
     const int lane = threadIdx.x & 63;
@@ -232,10 +250,10 @@ __global__ __launch_bounds__(256) void gemv_bf16_compact_kernel(GemvArgs a)
     float sum = 0.0f;
     int c0 = 0;
     for (; c0 + kGemvCh * 64 <= a.chunks; c0 += kGemvCh * 64) {
-        sum += gemv_block<true>(a.x, W, c0, a.chunks, lane);
+        sum += gemv_block<CT, true>(a.x, W, c0, a.chunks, lane);
     }
     if (c0 < a.chunks) {
-        sum += gemv_block<false>(a.x, W, c0, a.chunks, lane);
+        sum += gemv_block<CT, false>(a.x, W, c0, a.chunks, lane);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -252,37 +270,39 @@ bool gemv_eligible(const GemmOperands &op)
     return op.M == 1 && op.N < (int64_t(1) << 31) / 4 && (op.K + 7) / 8 < (int64_t(1) << 31);
 }
 
+template <int CT>
 int launch_gemv(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream)
 {
-    decltype(&gemv_bf16_kernel<0, EPI_FORM_GENERIC>) kernel = nullptr;
+    decltype(&gemv_bf16_kernel<CT, 0, EPI_FORM_GENERIC>) kernel = nullptr;
     const int form = epi_form(ep, false);
     auto pick = [&](auto formc) {
         constexpr int F = decltype(formc)::value;
         switch (ep.act) {
-            case KUDNN_ACT_UNIMPLEMENTED: kernel = gemv_bf16_kernel<KUDNN_ACT_UNIMPLEMENTED, F>; break;
-            case KUDNN_ACT_RELU: kernel = gemv_bf16_kernel<KUDNN_ACT_RELU, F>; break;
-            case KUDNN_ACT_SWISH: kernel = gemv_bf16_kernel<KUDNN_ACT_SWISH, F>; break;
-            case KUDNN_ACT_GELU_TANH: kernel = gemv_bf16_kernel<KUDNN_ACT_GELU_TANH, F>; break;
-            case KUDNN_ACT_GELU_ERF: kernel = gemv_bf16_kernel<KUDNN_ACT_GELU_ERF, F>; break;
+            case KUDNN_ACT_UNIMPLEMENTED: kernel = gemv_bf16_kernel<CT, KUDNN_ACT_UNIMPLEMENTED, F>; break;
+            case KUDNN_ACT_RELU: kernel = gemv_bf16_kernel<CT, KUDNN_ACT_RELU, F>; break;
+            case KUDNN_ACT_SWISH: kernel = gemv_bf16_kernel<CT, KUDNN_ACT_SWISH, F>; break;
+            case KUDNN_ACT_GELU_TANH: kernel = gemv_bf16_kernel<CT, KUDNN_ACT_GELU_TANH, F>; break;
+            case KUDNN_ACT_GELU_ERF: kernel = gemv_bf16_kernel<CT, KUDNN_ACT_GELU_ERF, F>; break;
             default: break;
         }
     };
     dim3 grid(static_cast<unsigned>((op.N + 3) / 4), static_cast<unsigned>(batches));
-    if (batches == 1 && form != EPI_FORM_GENERIC) {
-        decltype(&gemv_bf16_compact_kernel<0, EPI_FORM_BF16>) ck = nullptr;
+    constexpr int kForm16 = CT == KUDNN_DT_F16 ? EPI_FORM_F16 : EPI_FORM_BF16;  // the 16-bit form of this operand type
+    if (batches == 1 && (form == kForm16 || form == EPI_FORM_F32)) {
+        decltype(&gemv_bf16_compact_kernel<CT, 0, EPI_FORM_BF16>) ck = nullptr;
         auto pickc = [&](auto formc) {
             constexpr int F = decltype(formc)::value;
             switch (ep.act) {
-                case KUDNN_ACT_UNIMPLEMENTED: ck = gemv_bf16_compact_kernel<KUDNN_ACT_UNIMPLEMENTED, F>; break;
-                case KUDNN_ACT_RELU: ck = gemv_bf16_compact_kernel<KUDNN_ACT_RELU, F>; break;
-                case KUDNN_ACT_SWISH: ck = gemv_bf16_compact_kernel<KUDNN_ACT_SWISH, F>; break;
-                case KUDNN_ACT_GELU_TANH: ck = gemv_bf16_compact_kernel<KUDNN_ACT_GELU_TANH, F>; break;
-                case KUDNN_ACT_GELU_ERF: ck = gemv_bf16_compact_kernel<KUDNN_ACT_GELU_ERF, F>; break;
+                case KUDNN_ACT_UNIMPLEMENTED: ck = gemv_bf16_compact_kernel<CT, KUDNN_ACT_UNIMPLEMENTED, F>; break;
+                case KUDNN_ACT_RELU: ck = gemv_bf16_compact_kernel<CT, KUDNN_ACT_RELU, F>; break;
+                case KUDNN_ACT_SWISH: ck = gemv_bf16_compact_kernel<CT, KUDNN_ACT_SWISH, F>; break;
+                case KUDNN_ACT_GELU_TANH: ck = gemv_bf16_compact_kernel<CT, KUDNN_ACT_GELU_TANH, F>; break;
+                case KUDNN_ACT_GELU_ERF: ck = gemv_bf16_compact_kernel<CT, KUDNN_ACT_GELU_ERF, F>; break;
                 default: break;
             }
         };
-        if (form == EPI_FORM_BF16) {
-            pickc(std::integral_constant<int, EPI_FORM_BF16>{});
+        if (form == kForm16) {
+            pickc(std::integral_constant<int, kForm16>{});
         } else {
             pickc(std::integral_constant<int, EPI_FORM_F32>{});
         }
@@ -308,12 +328,12 @@ int launch_gemv(const GemmOperands &op, const EpiParams &ep, int64_t batches, hi
         hipLaunchKernelGGL(ck, grid, dim3(256), 0, stream, a);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
-    if (form == EPI_FORM_BF16) {
-        pick(std::integral_constant<int, EPI_FORM_BF16>{});
+    if (form == kForm16) {
+        pick(std::integral_constant<int, kForm16>{});
     } else if (form == EPI_FORM_F32) {
         pick(std::integral_constant<int, EPI_FORM_F32>{});
     } else {
-        kernel = gemv_bf16_kernel<0, EPI_FORM_GENERIC>;  // reads the activation at run time
+        kernel = gemv_bf16_kernel<CT, 0, EPI_FORM_GENERIC>;  // reads the activation at run time
     }
     if (kernel == nullptr) {
         return -1;
@@ -332,7 +352,7 @@ int launch_gemv(const GemmOperands &op, const EpiParams &ep, int64_t batches, hi
 // Loads go through buffer resources and are issued by every lane: a lane with nothing to load (a chunk past K, an X
 // row m >= M) gets an offset past the resource's range, which reads zero, so no branch separates the loads of a block.
 // The KW partial 16 x 16 tiles are summed through LDS and wave 0 runs the epilogue on runs of 4 consecutive columns.
-template <int KW>
+template <int CT, int KW>
 __global__ __launch_bounds__(KW * 64) void skinny_rows_kernel(GemmOperands op, EpiParams ep)
 {
     constexpr int kPitch = 33;  // chunks per LDS row
@@ -414,8 +434,7 @@ __global__ __launch_bounds__(KW * 64) void skinny_rows_kernel(GemmOperands op, E
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const u32x4_t wf = tw[r16 * kPitch + 4 * k + q];
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, wf), __builtin_bit_cast(bf16x8_t, xv[k]),
-                                                          acc, 0, 0, 0);
+            acc = mfma16<CT>(wf, xv[k], acc);
         }
     }
 
@@ -440,44 +459,54 @@ __global__ __launch_bounds__(KW * 64) void skinny_rows_kernel(GemmOperands op, E
     epi_apply4_pre(ep, ob, r16, nq, N, v, pre);
 }
 
-template <int KW, int UNR>
+template <int CT, int KW, int UNR>
 int launch(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream)
 {
     dim3 grid(static_cast<unsigned>((op.N + 15) / 16), static_cast<unsigned>(batches));
     dim3 block(KW * 64);
     if (op.K % 32 == 0) {
-        hipLaunchKernelGGL((skinny_bf16_kernel<KW, UNR, false>), grid, block, 0, stream, op, ep);
+        hipLaunchKernelGGL((skinny_bf16_kernel<CT, KW, UNR, false>), grid, block, 0, stream, op, ep);
     } else {
-        hipLaunchKernelGGL((skinny_bf16_kernel<KW, UNR, true>), grid, block, 0, stream, op, ep);
+        hipLaunchKernelGGL((skinny_bf16_kernel<CT, KW, UNR, true>), grid, block, 0, stream, op, ep);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-}  // namespace
-
-int kudnn_launch_skinny_bf16(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream)
+template <int CT>
+int launch_skinny(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream)
 {
     if (op.M > 16) {
         return -1;
     }
     if (gemv_eligible(op)) {
-        return launch_gemv(op, ep, batches, stream);
+        return launch_gemv<CT>(op, ep, batches, stream);
     }
     if (op.N * op.ldb * 2 < (int64_t(1) << 31) && op.M * op.lda * 2 < (int64_t(1) << 31)) {
         // fewer than 2 row groups per CU: split K over 16 waves (one workgroup per CU); otherwise 8 (two per CU)
         const int64_t groups = (op.N + 15) / 16 * batches;
         dim3 grid(static_cast<unsigned>((op.N + 15) / 16), static_cast<unsigned>(batches));
         if (groups < 512) {
-            hipLaunchKernelGGL(skinny_rows_kernel<16>, grid, dim3(16 * 64), 0, stream, op, ep);
+            hipLaunchKernelGGL((skinny_rows_kernel<CT, 16>), grid, dim3(16 * 64), 0, stream, op, ep);
         } else {
-            hipLaunchKernelGGL(skinny_rows_kernel<8>, grid, dim3(8 * 64), 0, stream, op, ep);
+            hipLaunchKernelGGL((skinny_rows_kernel<CT, 8>), grid, dim3(8 * 64), 0, stream, op, ep);
         }
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
     // Few weight row-groups: split K over 8 waves per workgroup to keep more loads in flight.
     const int64_t groups = (op.N + 15) / 16 * batches;
     if (groups < 1024) {
-        return launch<8, 8>(op, ep, batches, stream);
+        return launch<CT, 8, 8>(op, ep, batches, stream);
     }
-    return launch<4, 8>(op, ep, batches, stream);
+    return launch<CT, 4, 8>(op, ep, batches, stream);
+}
+
+}  // namespace
+
+int kudnn_launch_skinny(const GemmOperands &op, const EpiParams &ep, int64_t batches, int ct, hipStream_t stream)
+{
+    switch (ct) {
+        case KUDNN_DT_BF16: return launch_skinny<KUDNN_DT_BF16>(op, ep, batches, stream);
+        case KUDNN_DT_F16: return launch_skinny<KUDNN_DT_F16>(op, ep, batches, stream);
+        default: return -1;
+    }
 }

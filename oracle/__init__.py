@@ -19,7 +19,7 @@ import numpy as np
 _DIR = Path(__file__).resolve().parent
 LIB_PATH = _DIR / "liboracle.so"
 
-F32, F16, BF16 = 1, 2, 3
+F32, F16, BF16, S32, S8, U8 = 1, 2, 3, 4, 5, 6
 ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_SWISH, ACT_GELU_ERF = 0, 5, 20, 25, 27
 RES_EXT, RES_MUL, RES_IDENTIAL = 0, 1, 2
 BIN_NONE, BIN_ADD, BIN_EXT, BIN_MUL = 0, 1, 2, 3
@@ -94,7 +94,7 @@ def lib() -> ctypes.CDLL:
 
 
 def storage_dtype(dt: int):
-    return np.float32 if dt == F32 else np.uint16
+    return {F32: np.float32, S32: np.int32, S8: np.int8, U8: np.uint8}.get(dt, np.uint16)
 
 
 @dataclass
@@ -156,6 +156,8 @@ def to_f32(buf: np.ndarray, dt: int) -> np.ndarray:
         return (buf.astype(np.uint32) << 16).view(np.float32)
     if dt == F16:
         return buf.view(np.float16).astype(np.float32)
+    if dt in (S32, S8, U8):
+        return buf.astype(np.float32)
     raise ValueError(dt)
 
 

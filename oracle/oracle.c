@@ -41,6 +41,9 @@
 #define O_F32 1
 #define O_F16 2
 #define O_BF16 3
+#define O_S32 4
+#define O_S8 5
+#define O_U8 6
 
 #define O_ACT_NONE 0
 #define O_ACT_RELU 5
@@ -160,7 +163,21 @@ static float ld(const void *p, int dt, int64_t i)
         case O_F32: return ((const float *)p)[i];
         case O_BF16: return oracle_bf16_to_f32(((const uint16_t *)p)[i]);
         case O_F16: return oracle_f16_to_f32(((const uint16_t *)p)[i]);
+        case O_S8: return (float)((const int8_t *)p)[i];
+        case O_U8: return (float)((const uint8_t *)p)[i];
+        case O_S32: return (float)((const int32_t *)p)[i];
         default: return 0.0f;
+    }
+}
+
+/* Integer elements exactly (8-bit and 32-bit types). */
+static int64_t ld_int(const void *p, int dt, int64_t i)
+{
+    switch (dt) {
+        case O_S8: return ((const int8_t *)p)[i];
+        case O_U8: return ((const uint8_t *)p)[i];
+        case O_S32: return ((const int32_t *)p)[i];
+        default: return 0;
     }
 }
 
@@ -283,9 +300,17 @@ static float bf16_round_scalar(float f) { return oracle_bf16_to_f32(oracle_f32_t
  *  - every sum is formed in f32 (double here, rounded once);
  *  - bf16 C with bias: f32 temp = f32(C), temp = alpha*AB + beta*temp, temp += bias, RNE (:208-221);
  *  - bf16 C without bias: cblas_bgemm with bf16 alpha/beta, RNE (:222-226);
- *  - f32 / f16 C: value rounded once into C's type after bias (all-f32 fallback :672-705). */
+ *  - f32 / f16 C: value rounded once into C's type after bias (all-f32 fallback :672-705);
+ *  - s8 x s8 -> s32 (cblas_gemm_s8s8s32, :243-264): exact integer sum plus the s32 bias (a row / column vector is
+ *    KML's C offset, a full [M, N] bias is added afterwards: the same sum), two's-complement wrap into int32; only
+ *    alpha 1 and beta 0 are restated (the scaling of an int32 result by float alpha / beta is KML-internal). */
+static int oracle_gemm_s8(const ogemm *g);
+
 int oracle_gemm(const ogemm *g)
 {
+    if (g->c.dtype == O_S32) {
+        return oracle_gemm_s8(g);
+    }
     const int nd = g->a.ndims;
     if (nd < 2 || g->b.ndims != nd || g->c.ndims != nd) {
         return -1;
@@ -358,6 +383,58 @@ int oracle_gemm(const ogemm *g)
                     free(acc);
                 }
                 free(bf);
+            }
+        }
+    }
+    return 0;
+}
+
+static int oracle_gemm_s8(const ogemm *g)
+{
+    const int nd = g->a.ndims;
+    if (g->a.dtype != O_S8 || g->b.dtype != O_S8 || g->alpha != 1.0f || g->beta != 0.0f) {
+        return -3;
+    }
+    const int64_t M = g->a.dims[nd - 2], K = g->a.dims[nd - 1], N = g->b.dims[nd - 1];
+    const int hasBias = g->bias.ndims != 0 && total(&g->bias) != 0;
+    if (hasBias && g->bias.dtype != O_S32) {
+        return -3;
+    }
+    int64_t ad[3], as[3], bd[3], bs_[3], cd[3], cs[3], xd[3], xs[3] = {0, 0, 0};
+    batch_slots(&g->a, ad, as);
+    batch_slots(&g->b, bd, bs_);
+    batch_slots(&g->c, cd, cs);
+    if (hasBias) {
+        batch_slots(&g->bias, xd, xs);
+    }
+    int64_t L[3];
+    for (int s = 0; s < 3; ++s) {
+        L[s] = ad[s] > bd[s] ? ad[s] : bd[s];
+    }
+    const int64_t a_sm = g->a.strides[nd - 2], a_sk = g->a.strides[nd - 1];
+    const int64_t b_sk = g->b.strides[nd - 2], b_sn = g->b.strides[nd - 1];
+    const int64_t c_sm = g->c.strides[nd - 2], c_sn = g->c.strides[nd - 1];
+    const int64_t x_sm = hasBias ? g->bias.strides[nd - 2] : 0, x_sn = hasBias ? g->bias.strides[nd - 1] : 0;
+    for (int64_t i0 = 0; i0 < L[0]; ++i0) {
+        for (int64_t i1 = 0; i1 < L[1]; ++i1) {
+            for (int64_t i2 = 0; i2 < L[2]; ++i2) {
+                const int64_t ao = i0 * as[0] + i1 * as[1] + i2 * as[2];
+                const int64_t bo = i0 * bs_[0] + i1 * bs_[1] + i2 * bs_[2];
+                const int64_t co = i0 * cs[0] + i1 * cs[1] + i2 * cs[2];
+                const int64_t xo = i0 * xs[0] + i1 * xs[1] + i2 * xs[2];
+#pragma omp parallel for schedule(dynamic, 1)
+                for (int64_t m = 0; m < M; ++m) {
+                    for (int64_t n = 0; n < N; ++n) {
+                        int64_t acc = 0;
+                        for (int64_t k = 0; k < K; ++k) {
+                            acc += ld_int(g->pa, O_S8, ao + m * a_sm + k * a_sk) * ld_int(g->pb, O_S8, bo + k * b_sk + n * b_sn);
+                        }
+                        if (hasBias) {
+                            acc += ld_int(g->pbias, O_S32, xo + m * x_sm + n * x_sn);
+                        }
+                        ((int32_t *)g->pc)[co + m * c_sm + n * c_sn] = (int32_t)(uint32_t)(uint64_t)acc;
+                    }
+                }
             }
         }
     }

@@ -16,6 +16,8 @@ FP32_MAXNORM_TOL = 1e-5
 BF16_RTOL = 1e-2
 BF16_ATOL = 1e-2
 BF16_MAXNORM_TOL = 1e-2
+# f16 (not a north-star dtype): one f16 ulp is 2^-11 ~ 4.9e-4 relative; the outputs are RNE of an f32 value
+F16_TOL = 2e-3
 
 
 class Case:
@@ -25,7 +27,13 @@ class Case:
         self.desc = K.desc(dims, dt, layout, strides)
         self.dt = dt
         shape, st = self.desc.shape(), self.desc.stride()
-        self.t = O.empty(shape, st, dt) if zero else O.fill(shape, st, dt, seed, dist, lo, hi)
+        if dt in (O.S32, O.S8, O.U8) and not zero:
+            # integer tensors: uniform integers in [lo, hi] from a seeded numpy generator
+            t = O.empty(shape, st, dt)
+            t.buf[:] = np.random.default_rng(seed).integers(int(lo), int(hi) + 1, size=t.buf.size)
+            self.t = t
+        else:
+            self.t = O.empty(shape, st, dt) if zero else O.fill(shape, st, dt, seed, dist, lo, hi)
 
     def clone_empty(self) -> O.Tensor:
         return O.empty(self.t.dims, self.t.strides, self.dt)
@@ -43,16 +51,25 @@ def zeros_device(case: Case):
     import torch
 
     n = case.t.buf.size
-    return torch.zeros(n, dtype=torch.float32 if case.dt == O.F32 else torch.int16, device="cuda")
+    tdt = {O.F32: torch.float32, O.S32: torch.int32, O.S8: torch.int8, O.U8: torch.uint8}.get(case.dt, torch.int16)
+    return torch.zeros(n, dtype=tdt, device="cuda")
 
 
 def from_device(x, dt) -> np.ndarray:
     a = x.cpu().numpy()
-    return a.view(np.uint16) if dt != O.F32 else a.astype(np.float32, copy=False)
+    if dt == O.F32:
+        return a.astype(np.float32, copy=False)
+    return a.view(O.storage_dtype(dt))
 
 
 def compare(got_buf: np.ndarray, ref_buf: np.ndarray, dt: int, what: str = ""):
-    """Asserts the north-star tolerance; returns (max-normalised error, bit-exact fraction)."""
+    """Asserts the north-star tolerance (bit-exact for integer outputs); returns (max-normalised error, bit-exact
+    fraction)."""
+    if dt in (O.S32, O.S8, O.U8):
+        bad = np.nonzero(got_buf != ref_buf)[0]
+        assert bad.size == 0, (f"{what}: {bad.size} of {got_buf.size} integer outputs differ, first at {bad[0]}: "
+                               f"got {got_buf[bad[0]]} want {ref_buf[bad[0]]}")
+        return 0.0, 1.0
     g = O.to_f32(got_buf, dt).astype(np.float64)
     r = O.to_f32(ref_buf, dt).astype(np.float64)
     assert g.shape == r.shape
@@ -64,6 +81,10 @@ def compare(got_buf: np.ndarray, ref_buf: np.ndarray, dt: int, what: str = ""):
     exact = float(np.mean(got_buf == ref_buf)) if got_buf.size else 1.0
     if dt == O.F32:
         assert maxnorm <= FP32_MAXNORM_TOL, f"{what}: fp32 max-normalised error {maxnorm:.3e} > {FP32_MAXNORM_TOL}"
+    elif dt == O.F16:
+        assert maxnorm <= F16_TOL, f"{what}: f16 max-normalised error {maxnorm:.3e} > {F16_TOL}"
+        bad = d > (F16_TOL + F16_TOL * np.abs(r[fin]))
+        assert float(np.mean(bad)) <= 1e-4 if bad.size else True, f"{what}: {np.count_nonzero(bad)} elements outside 2e-3"
     else:
         assert maxnorm <= BF16_MAXNORM_TOL, f"{what}: max-normalised error {maxnorm:.3e} > {BF16_MAXNORM_TOL}"
         bad = d > (BF16_ATOL + BF16_RTOL * np.abs(r[fin]))

@@ -1,0 +1,183 @@
+"""GPU parity of the other dtype combinations of the primitive (the reference's GEMM registry,
+src/dnn/src/kudnn_gemm.cpp:590-601): f16 x f16 (cblas_hgemm / cblas_shgemm), f16 x s8 (W8A16: the weight converted
+to f16, :341-372) and s8 x s8 -> s32 (W8A8, cblas_gemm_s8s8s32, :243-264), each on its own MFMA kernels with the same
+epilogue. Integer results are compared bit for bit; f16 results within 2e-3 max-normalised.
+"""
+import numpy as np
+import pytest
+
+import kudnn_amd as K
+import oracle as O
+from support import Case, compare, from_device, zeros_device
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    K.lib()
+
+
+@pytest.fixture
+def force_pingpong(monkeypatch):
+    monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "4")
+
+
+# ---------------------------------------------------------------------------------------------------
+# s8 x s8 -> s32
+
+
+def run_s8(M, N, Kd, wlayout="BA", bias_dims=None, seed=0, expect=None, batch=None):
+    lead = list(batch) if batch else []
+    x = Case(lead + [M, Kd], O.S8, seed=seed, lo=-128, hi=127)
+    w = Case(lead + [Kd, N], O.S8, wlayout if not batch else None, seed=seed + 1, lo=-128, hi=127)
+    c = Case(lead + [M, N], O.S32, zero=True)
+    b = Case(bias_dims, O.S32, seed=seed + 2, lo=-(1 << 24), hi=1 << 24) if bias_dims else None
+    plan = K.Gemm(x.desc, w.desc, c.desc, b.desc if b else None)
+    if expect:
+        assert expect in plan.describe(), plan.describe()
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc, b.device() if b else None)
+    torch.cuda.synchronize()
+    ref = c.clone_empty()
+    O.gemm(x.t, w.t, ref, b.t if b else None)
+    compare(from_device(dc, O.S32), ref.buf, O.S32, plan.describe())
+    return plan
+
+
+@pytest.mark.parametrize("mnk", [(64, 64, 128), (300, 260, 256), (17, 33, 24), (5, 48, 64), (1, 70, 300), (256, 384, 1024)])
+@pytest.mark.parametrize("wlayout", ["BA", "AB"])
+def test_s8s8s32_shapes_layouts(mnk, wlayout):
+    M, N, Kd = mnk
+    run_s8(M, N, Kd, wlayout, bias_dims=[1, N], seed=200, expect="mfma_s8")
+
+
+@pytest.mark.parametrize("bias", [None, "1N", "M1", "MN"])
+def test_s8s8s32_bias_kinds(bias):
+    M, N, Kd = 96, 80, 256
+    dims = {"1N": [1, N], "M1": [M, 1], "MN": [M, N]}.get(bias)
+    run_s8(M, N, Kd, bias_dims=dims, seed=210)
+
+
+@pytest.mark.parametrize("mnk", [(256, 256, 128), (300, 520, 384), (40, 600, 256)])
+def test_s8s8s32_pingpong(force_pingpong, mnk):
+    M, N, Kd = mnk
+    run_s8(M, N, Kd, bias_dims=[1, N], seed=220, expect="mfma_s8_pingpong")
+
+
+def test_s8s8s32_batched_broadcast_weight():
+    x = Case([3, 40, 256], O.S8, seed=230, lo=-128, hi=127)
+    w = Case([1, 256, 72], O.S8, seed=231, lo=-128, hi=127)
+    c = Case([3, 40, 72], O.S32, zero=True)
+    plan = K.Gemm(x.desc, w.desc, c.desc)
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc)
+    torch.cuda.synchronize()
+    ref = c.clone_empty()
+    O.gemm(x.t, w.t, ref)
+    compare(from_device(dc, O.S32), ref.buf, O.S32, plan.describe())
+
+
+def test_s8s8s32_extremes_exact():
+    # every product at its extreme (-128 x -128 = 16384) over K = 4096: sums of 6.7e7, beyond f32's 2^24 integer range,
+    # must come out exact
+    M, N, Kd = 64, 64, 4096
+    x = Case([M, Kd], O.S8, zero=True)
+    w = Case([Kd, N], O.S8, "BA", zero=True)
+    x.t.buf[:] = -128
+    w.t.buf[:] = -128
+    w.t.buf[::7] = 127
+    c = Case([M, N], O.S32, zero=True)
+    plan = K.Gemm(x.desc, w.desc, c.desc)
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc)
+    torch.cuda.synchronize()
+    got = from_device(dc, O.S32).reshape(M, N)
+    want = (x.t.buf.astype(np.int64).reshape(M, Kd) @ w.t.buf.astype(np.int64).reshape(N, Kd).T).astype(np.int32)
+    assert np.array_equal(got, want)
+    assert np.abs(want).max() > (1 << 24)
+
+
+# ---------------------------------------------------------------------------------------------------
+# f16 x f16 and f16 x s8
+
+
+@pytest.mark.parametrize("mnk", [(64, 64, 64), (300, 260, 200), (17, 33, 24), (5, 48, 64), (1, 96, 520), (4, 130, 256)])
+@pytest.mark.parametrize("act", [O.ACT_RELU, O.ACT_SWISH, O.ACT_GELU_TANH, O.ACT_GELU_ERF])
+def test_f16_linear_act(mnk, act):
+    M, N, Kd = mnk
+    x = Case([M, Kd], O.F16, seed=240)
+    w = Case([Kd, N], O.F16, "BA", seed=241)
+    b = Case([1, N], O.F16, seed=242, lo=-0.1, hi=0.1)
+    c = Case([M, N], O.F16, zero=True)
+    alpha = 0.0 if act == O.ACT_RELU else 1.0
+    plan = K.LinearActivation(x.desc, w.desc, c.desc, b.desc, alpha, 0.0, act)
+    assert "f16" in plan.describe(), plan.describe()
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc, b.device())
+    torch.cuda.synchronize()
+    ref = c.clone_empty()
+    O.linear_act(x.t, w.t, ref, b.t, act, alpha)
+    compare(from_device(dc, O.F16), ref.buf, O.F16, plan.describe())
+
+
+@pytest.mark.parametrize("mnk", [(256, 256, 64), (300, 520, 192), (40, 600, 128)])
+@pytest.mark.parametrize("post", ["gelu_add", "none_f32out"])
+def test_f16_pingpong(force_pingpong, mnk, post):
+    M, N, Kd = mnk
+    ydt = O.F32 if post == "none_f32out" else O.F16
+    x = Case([M, Kd], O.F16, seed=250, dist="normal", lo=0.0, hi=1.0)
+    w = Case([Kd, N], O.F16, "BA", seed=251, dist="normal", lo=0.0, hi=0.05)
+    y = Case([M, N], ydt, zero=True)
+    s = Case([M, N], ydt, seed=252) if post == "gelu_add" else None
+    act = K.ACT_GELU_TANH if post == "gelu_add" else K.ACT_UNIMPLEMENTED
+    plan = K.LinearPostOps(x.desc, w.desc, y.desc, None, act=act, binary=K.BIN_ADD if s else K.BIN_NONE,
+                           src=s.desc if s else None)
+    assert "f16_pingpong" in plan.describe(), plan.describe()
+    dy = zeros_device(y)
+    plan.run(x.device(), w.device(), dy, None, s.device() if s else None)
+    torch.cuda.synchronize()
+    ref = y.clone_empty()
+    O.linear_postops(x.t, w.t, ref, None, O.ACT_GELU_TANH if s else O.ACT_NONE, 0.0, O.BIN_ADD if s else O.BIN_NONE,
+                     s.t if s else None)
+    compare(from_device(dy, ydt), ref.buf, ydt, plan.describe())
+
+
+@pytest.mark.parametrize("wdt", [O.S8, O.U8])
+@pytest.mark.parametrize("mnk", [(64, 96, 128), (1, 200, 256), (300, 130, 72)])
+def test_f16_x_8bit_weight(wdt, mnk):
+    # W8A16 (GEMMWrapper<__fp16, int8_t / uint8_t, __fp16, float>): the 8-bit weight is converted to f16, bias f32
+    M, N, Kd = mnk
+    x = Case([M, Kd], O.F16, seed=260)
+    lo, hi = (-128, 127) if wdt == O.S8 else (0, 255)
+    w = Case([Kd, N], wdt, "BA", seed=261, lo=lo, hi=hi)
+    b = Case([1, N], O.F32, seed=262, lo=-0.5, hi=0.5)
+    c = Case([M, N], O.F16, zero=True)
+    plan = K.Gemm(x.desc, w.desc, c.desc, b.desc)
+    assert "f16" in plan.describe() and "packB" in plan.describe(), plan.describe()
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc, b.device())
+    torch.cuda.synchronize()
+    ref = c.clone_empty()
+    O.gemm(x.t, w.t, ref, b.t)
+    compare(from_device(dc, O.F16), ref.buf, O.F16, plan.describe())
+
+
+def test_s8_operands_float_output():
+    # integer operands into a floating output take the reference's all-f32 fallback (ChooseImpl :672-705)
+    M, N, Kd = 50, 70, 96
+    x = Case([M, Kd], O.S8, seed=270, lo=-128, hi=127)
+    w = Case([Kd, N], O.S8, "BA", seed=271, lo=-128, hi=127)
+    c = Case([M, N], O.F32, zero=True)
+    plan = K.Gemm(x.desc, w.desc, c.desc)
+    assert "mfma_f32" in plan.describe(), plan.describe()
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc)
+    torch.cuda.synchronize()
+    ref = c.clone_empty()
+    O.gemm(x.t, w.t, ref)
+    compare(from_device(dc, O.F32), ref.buf, O.F32, plan.describe())
