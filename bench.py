@@ -6,12 +6,13 @@ is one call of the fused Linear post-op chain through the C ABI on inputs alread
 
 Also reported (not `value`): the decode-shaped skinny Linear at M in {1, 4, 16}, K=4096, N in {4096, 14336}
 (configs[3], Linear then element-wise multiply) in GB/s, timed over rotating weight copies (>= 512 MB) so that the 256 MB Infinity Cache
-cannot serve the weight stream; C1, C2 and C5 in TFLOP/s; and the CPU baseline (the reference tests' portable naive loop, timed
+cannot serve the weight stream; C1, C2 and C5 in TFLOP/s; C3's shape in f16 (same post-ops) and as an s8 x s8 -> s32
+GEMM (TOP/s against the 5.0 POP/s int8 peak); and the CPU baseline (the reference tests' portable naive loop, timed
 on a bounded row sample of the same workload on this host's cores).
 
 Before the W counted warmup steps, the step is also run untimed for --prewarm-ms of wall time (default 300 ms):
 the GPU raises its clocks over the first ~100 ms of sustained load, and a timed region that starts on a cold GPU
-reports the ramp rather than the kernel (a 25 ms region read 475 us per step cold against 412 us warm).
+reports the ramp rather than the kernel (10-15 % slower per step over the first tens of milliseconds).
 
 For profiling, --only c3 runs just the C3 step (JSON line without decode or CPU baseline), --only decode just the
 decode lines, and --only copy runs an
@@ -36,6 +37,8 @@ METRIC = "Linear+postop TFLOP/s (% MFMA peak) at 4096x4096x11008; M=1 GB/s (% HB
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 PEAK_F32_TFLOPS = 157.3    # MI355X dense fp32 MFMA
+PEAK_F16_TFLOPS = 2500.0   # MI355X dense f16 MFMA
+PEAK_I8_TOPS = 5000.0      # MI355X dense int8 MFMA
 
 
 def parse():
@@ -218,6 +221,42 @@ def bench_config(args, torch, K, name):
             "frac_peak": tflops / peak, "input_copies": copies}
 
 
+def bench_c3_dtype(args, torch, K, name):
+    """Informational: C3's shape in the other operand types of the primitive. "C3-f16": the same Linear + GELU_tanh +
+    residual add with f16 tensors; "C3-s8": the s8 x s8 -> s32 GEMM (W8A8; the integer path has no post-ops), inputs
+    uniform integers in [-128, 127] rounded from the same generator."""
+    M, Kd, N = 4096, 4096, 11008
+    stream = torch.cuda.current_stream()
+    if name == "C3-f16":
+        f16 = torch.float16
+        x = synth(torch, (M, Kd), 0, "normal", 0.0, 1.0, f16)
+        w = synth(torch, (N, Kd), 1, "normal", 0.0, 0.02, f16)
+        r = synth(torch, (M, N), 3, "normal", 0.0, 1.0, f16)
+        y = torch.empty(M, N, device="cuda", dtype=f16)
+        dy = K.desc([M, N], K.F16)
+        plan = K.LinearPostOps(K.desc([M, Kd], K.F16), K.desc([Kd, N], K.F16, "BA"), dy, None, act=K.ACT_GELU_TANH,
+                               binary=K.BIN_ADD, src=dy)
+
+        def step(i=0):
+            plan.run(x, w, y, None, r, stream=stream)
+        peak, unit = PEAK_F16_TFLOPS, "TFLOP/s"
+    else:
+        def s8(shape, seed):
+            return torch.clamp(torch.round(synth(torch, shape, seed, "uniform", -128.5, 127.5, torch.float32)),
+                               -128, 127).to(torch.int8)
+        x, w = s8((M, Kd), 0), s8((N, Kd), 1)
+        y = torch.empty(M, N, device="cuda", dtype=torch.int32)
+        plan = K.Gemm(K.desc([M, Kd], K.S8), K.desc([Kd, N], K.S8, "BA"), K.desc([M, N], K.S32))
+
+        def step(i=0):
+            plan.run(x, w, y, stream=stream)
+        peak, unit = PEAK_I8_TOPS, "TOP/s"
+    ms, _ = time_launches(step, args.steps, args.warmup, torch, stream, args.prewarm_ms)
+    rate = 2.0 * M * N * Kd / (ms * 1e-3) / 1e12
+    return {"config": name, "M": M, "K": Kd, "N": N, "plan": plan.describe(), "us": ms * 1e3, unit: rate,
+            "frac_peak": rate / peak}
+
+
 def cpu_baseline(args, np):
     """The reference tests' naive Linear loop (f32 accumulation, OpenMP over rows) on a row sample of C3."""
     import oracle as O
@@ -285,7 +324,8 @@ def main():
     only = args.only == "c3"
     decode = [] if (args.no_decode or only) else [bench_decode(args, torch, K, n, m) for n in (4096, 14336)
                                                   for m in (1, 4, 16)]
-    others = [] if (args.no_others or only) else [bench_config(args, torch, K, c) for c in ("C1", "C2", "C5")]
+    others = [] if (args.no_others or only) else ([bench_config(args, torch, K, c) for c in ("C1", "C2", "C5")] +
+                                                   [bench_c3_dtype(args, torch, K, c) for c in ("C3-f16", "C3-s8")])
     cpu = None if (args.no_cpu_baseline or only) else cpu_baseline(args, np)
 
     traffic = None
