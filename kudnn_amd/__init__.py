@@ -36,15 +36,28 @@ STANDARD_LAYOUT = {1: "A", 2: "AB", 3: "ABC", 4: "ABCD", 5: "ABCDE"}
 
 # activation kinds == KuDNN::ActivationFunction
 ACT_UNIMPLEMENTED = 0
+ACT_ABS = 1
+ACT_EXP = 2
 ACT_LINEAR = 3
+ACT_LOG = 4
 ACT_RELU = 5
+ACT_ROUND = 6
+ACT_SQRT = 7
+ACT_SQUARE = 8
 ACT_TANH = 9
 ACT_SIGMOID = 10
+ACT_POW = 11
 ACT_CLIP = 12
+ACT_CLIP_V2 = 13
+ACT_HARDSIGMOID = 14
+ACT_HARDSWISH = 15
+ACT_ELU = 19
 ACT_GELU_TANH = 20
+ACT_ELU_DST = 22
 ACT_SWISH = 25
 ACT_SRELU = 26
 ACT_GELU_ERF = 27
+ACT_MISH = 28
 
 # residual kinds == KuDNN::ResOpsFunction
 RES_EXT, RES_MUL, RES_IDENTIAL = 0, 1, 2

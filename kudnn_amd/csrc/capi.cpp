@@ -292,10 +292,20 @@ int ValidateRes(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const ku
     return KUDNN_STATUS_SUCCESS;
 }
 
+// Every kind of the reference's forward activation table (kudnn_eltwise.cpp:333-400) runs as a fused epilogue;
+// RELU, SWISH, GELU_TANH and GELU_ERF have kernels of their own, the rest run in the epilogue's generic form.
 bool ActImplemented(int kind)
 {
-    return kind == KUDNN_ACT_RELU || kind == KUDNN_ACT_SWISH || kind == KUDNN_ACT_GELU_TANH ||
-           kind == KUDNN_ACT_GELU_ERF;
+    switch (kind) {
+        case KUDNN_ACT_ABS: case KUDNN_ACT_EXP: case KUDNN_ACT_LINEAR: case KUDNN_ACT_LOG: case KUDNN_ACT_RELU:
+        case KUDNN_ACT_ROUND: case KUDNN_ACT_SQRT: case KUDNN_ACT_SQUARE: case KUDNN_ACT_TANH: case KUDNN_ACT_SIGMOID:
+        case KUDNN_ACT_POW: case KUDNN_ACT_CLIP: case KUDNN_ACT_CLIP_V2: case KUDNN_ACT_HARDSIGMOID:
+        case KUDNN_ACT_HARDSWISH: case KUDNN_ACT_ELU: case KUDNN_ACT_GELU_TANH: case KUDNN_ACT_ELU_DST:
+        case KUDNN_ACT_SWISH: case KUDNN_ACT_SRELU: case KUDNN_ACT_GELU_ERF: case KUDNN_ACT_MISH:
+            return true;
+        default:
+            return false;
+    }
 }
 
 // ---------------------------------------------------------------------------------------------------
@@ -576,6 +586,7 @@ bool Aligned(const void *p, int bytes) { return (reinterpret_cast<uintptr_t>(p) 
 struct EpiExtras {
     int act = KUDNN_ACT_UNIMPLEMENTED;
     float actAlpha = 0.0f;
+    float actBeta = 0.0f;
     int bin = KUDNN_BINARY_NONE;
     bool storeC = false;  // y is a separate tensor and C must be written too
     bool hasY = false;    // y != C
@@ -789,6 +800,7 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
     ep.beta = beta;
     ep.act = x.act;
     ep.act_alpha = x.actAlpha;
+    ep.act_beta = x.actBeta;
     ep.bin = x.bin;
     ep.gamma = gamma;
     ep.c_dt = core.C.dt;
@@ -1304,7 +1316,7 @@ int kudnn_linear_act_create(const kudnn_tensor_desc *a, const kudnn_tensor_desc 
     if (!ActImplemented(kind)) {
         return Fail(KUDNN_STATUS_UNSUPPORTED,
                     "LinearActivationLayerFWD: activation kind " + std::to_string(kind) +
-                        " is not implemented as a fused epilogue (RELU, SWISH, GELU_TANH, GELU_ERF are)");
+                        " is not a forward activation kind");
     }
     auto *p = new (std::nothrow) kudnn_linear_act_plan();
     if (p == nullptr) {
@@ -1324,6 +1336,7 @@ int kudnn_linear_act_create(const kudnn_tensor_desc *a, const kudnn_tensor_desc 
     }
     p->x.act = kind;
     p->x.actAlpha = alpha;
+    p->x.actBeta = beta;
     p->desc = DescribeCore(p->core) + " act=" + std::to_string(kind);
     *plan = p;
     return KUDNN_STATUS_SUCCESS;
@@ -1585,6 +1598,7 @@ int kudnn_linear_postops_create(const kudnn_tensor_desc *a, const kudnn_tensor_d
     }
     p->x.act = act_kind;
     p->x.actAlpha = act_alpha;
+    p->x.actBeta = act_beta;
     p->x.bin = binary_kind;
     p->desc = DescribeCore(p->core) + " act=" + std::to_string(act_kind) + " bin=" + std::to_string(binary_kind);
     *plan = p;

@@ -150,14 +150,57 @@ __device__ __forceinline__ float act_gelu_erf(float x)
     return 0.5f * x * (1.0f + erff(x * kInvSqrt2));
 }
 
-__device__ __forceinline__ float apply_act(int kind, float x, float alpha)
+// The remaining kinds of the reference's forward activation table (src/dnn/src/kudnn_eltwise.cpp:333-400), f32 math
+// from each kernel's f32 source (kernels/vml/*): alpha and beta as ActivationLayerFWD passes them.
+__device__ __forceinline__ float act_other(int kind, float x, float alpha, float beta)
 {
     switch (kind) {
+        case KUDNN_ACT_ABS: return fabsf(x);                       // abs/vml_sve_la_absf.c
+        case KUDNN_ACT_EXP: return expf(x);                        // exp/vml_sve_la_expf.c
+        case KUDNN_ACT_LINEAR: return fmaf(alpha, x, beta);        // linear.c: svmad(alpha, x, beta)
+        case KUDNN_ACT_LOG: return logf(x);                        // log/vml_sve_la_lnf.c
+        case KUDNN_ACT_ROUND: return rintf(x);                     // round/vml_sve_la_nearbyintf.c: ties to even
+        case KUDNN_ACT_SQRT: return sqrtf(x);                      // sqrt/vml_sve_la_sqrtf.c
+        case KUDNN_ACT_SQUARE: return x * x;                       // sqr/vml_sve_la_sqrf.c
+        case KUDNN_ACT_TANH: return tanhf(x);                      // tanh/vml_sve_la_tanhf.c
+        case KUDNN_ACT_SIGMOID: return 1.0f / (1.0f + expf(-x));   // logistic/sigmoid.c: sigmoid of -x negated
+        case KUDNN_ACT_POW: return powf(x, beta) * alpha;          // pow: alpha * x^beta (powx_calculations.h:506-515)
+        case KUDNN_ACT_CLIP:                                       // clip/clipf.c: <= alpha -> alpha, > beta -> beta
+            return x <= alpha ? alpha : (x > beta ? beta : x);
+        case KUDNN_ACT_CLIP_V2:                                    // clipv2/clipv2f.c: <= alpha -> alpha, >= beta -> beta
+            return x <= alpha ? alpha : (x >= beta ? beta : x);
+        case KUDNN_ACT_HARDSIGMOID:                                // hardsigmoid: minnm / maxnm (a NaN gives 1)
+            return fmaxf(fminf(fmaf(x, alpha, beta), 1.0f), 0.0f);
+        case KUDNN_ACT_HARDSWISH:                                  // hardswish: x * max(0, min(1, alpha*x + beta))
+            return x * fmaxf(fminf(fmaf(alpha, x, beta), 1.0f), 0.0f);
+        case KUDNN_ACT_ELU:                                        // elu/vml_sve_la_eluf.c: alpha*e^x - alpha, fused
+            return x > 0.0f ? x : fmaf(expf(x), alpha, -alpha);
+        case KUDNN_ACT_ELU_DST: return x > 0.0f ? x : alpha * expm1f(x);  // elu/eludstf.c
+        case KUDNN_ACT_SRELU: {                                    // soft_relu/vml_sve_la_softrelu.h: ln(1+e^(ax))/a
+            const float ax = alpha * x;
+            if (ax >= 88.7228394f) {                               // exp's upper bound: the result is x
+                return x;
+            }
+            return log1pf(expf(fmaxf(ax, -87.3365479f))) / alpha;  // ax clamped to exp's lower bound
+        }
+        case KUDNN_ACT_MISH: {                                     // mish: x * ((e^x+1)^2 - 1) / ((e^x+1)^2 + 1)
+            const float e1 = expf(fminf(x, 44.3614197f)) + 1.0f;   // exponent capped as the reference's
+            const float e2 = e1 * e1;
+            return x * ((e2 - 1.0f) / (e2 + 1.0f));
+        }
+        default: return x;
+    }
+}
+
+__device__ __forceinline__ float apply_act(int kind, float x, float alpha, float beta = 0.0f)
+{
+    switch (kind) {
+        case KUDNN_ACT_UNIMPLEMENTED: return x;
         case KUDNN_ACT_RELU: return act_relu(x, alpha);
         case KUDNN_ACT_SWISH: return act_swish(x, alpha);
         case KUDNN_ACT_GELU_TANH: return act_gelu_tanh(x);
         case KUDNN_ACT_GELU_ERF: return act_gelu_erf(x);
-        default: return x;
+        default: return act_other(kind, x, alpha, beta);
     }
 }
 
@@ -165,7 +208,16 @@ __device__ __forceinline__ float apply_act(int kind, float x, float alpha)
 __device__ __forceinline__ float act_round(int dt, int kind, float v)
 {
     if (dt == KUDNN_DT_BF16) {
-        uint16_t h = (kind == KUDNN_ACT_RELU) ? f32_to_bf16_trunc_inf(v) : f32_to_bf16_trunc(v);
+        // RELU, CLIP, CLIP_V2, ELU, LINEAR, POW, ROUND and SRELU send values at or above the largest bf16 to +-Inf
+        // before truncating (SvF32CvtBf16InfSpecial in their FWD kernels); ELU_DST rounds to nearest even
+        // (eludstbf16.c, SveCvtU32ToU16); the others truncate
+        if (kind == KUDNN_ACT_ELU_DST) {
+            return bf16_to_f32(f32_to_bf16_rne(v));
+        }
+        const bool inf = kind == KUDNN_ACT_RELU || kind == KUDNN_ACT_CLIP || kind == KUDNN_ACT_CLIP_V2 ||
+                         kind == KUDNN_ACT_ELU || kind == KUDNN_ACT_LINEAR || kind == KUDNN_ACT_POW ||
+                         kind == KUDNN_ACT_ROUND || kind == KUDNN_ACT_SRELU;
+        uint16_t h = inf ? f32_to_bf16_trunc_inf(v) : f32_to_bf16_trunc(v);
         return bf16_to_f32(h);
     }
     if (dt == KUDNN_DT_F16) {
@@ -279,7 +331,7 @@ __device__ __forceinline__ void epi_apply_pre(const EpiParams &e, const EpiBatch
         store_elem(e.c, e.c_dt, ob.c + m * e.c_sm + n * e.c_sn, v);
     }
     if (e.act != KUDNN_ACT_UNIMPLEMENTED) {
-        v = act_round(e.c_dt, e.act, apply_act(e.act, v, e.act_alpha));
+        v = act_round(e.c_dt, e.act, apply_act(e.act, v, e.act_alpha, e.act_beta));
     }
     if (e.bin != KUDNN_BINARY_NONE) {
         const float sv = raw1_to_f32(use_here(p.src), e.src_dt);
@@ -384,7 +436,7 @@ __device__ __forceinline__ void epi_apply4_pre(const EpiParams &e, const EpiBatc
             }
         }
         if (e.act != KUDNN_ACT_UNIMPLEMENTED) {
-            for (int q = 0; q < 4; ++q) v[q] = act_round(e.c_dt, e.act, apply_act(e.act, v[q], e.act_alpha));
+            for (int q = 0; q < 4; ++q) v[q] = act_round(e.c_dt, e.act, apply_act(e.act, v[q], e.act_alpha, e.act_beta));
         }
         if (e.bin != KUDNN_BINARY_NONE) {
             int64_t si = ob.src + m * e.src_sm + n;
@@ -470,7 +522,7 @@ __device__ __forceinline__ void epi_apply8(const EpiParams &e, const EpiBatch &o
         }
         if (e.act != KUDNN_ACT_UNIMPLEMENTED) {
 #pragma unroll
-            for (int q = 0; q < 8; ++q) v[q] = act_round(e.c_dt, e.act, apply_act(e.act, v[q], e.act_alpha));
+            for (int q = 0; q < 8; ++q) v[q] = act_round(e.c_dt, e.act, apply_act(e.act, v[q], e.act_alpha, e.act_beta));
         }
         if (e.bin != KUDNN_BINARY_NONE) {
             const int64_t si = ob.src + m * e.src_sm + n;

@@ -498,14 +498,13 @@ int launch_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches
                 pick(std::integral_constant<int, EPI_FORM_F16>{});
             }
         }
-        if (kernel == nullptr && form != EPI_FORM_I32 && (ep.act == KUDNN_ACT_UNIMPLEMENTED || ep.act == KUDNN_ACT_RELU ||
-                                                          ep.act == KUDNN_ACT_SWISH || ep.act == KUDNN_ACT_GELU_TANH ||
-                                                          ep.act == KUDNN_ACT_GELU_ERF)) {
-            kernel = gemm_pingpong_kernel<CT, 0, EPI_FORM_GENERIC>;  // reads the activation at run time
+        if (kernel == nullptr && form != EPI_FORM_I32) {
+            // the other activation kinds, and the other tensor types, read everything at run time
+            kernel = gemm_pingpong_kernel<CT, 0, EPI_FORM_GENERIC>;
         }
     }
     if (kernel == nullptr) {
-        return -1;  // not a fused activation
+        return -1;
     }
     hipLaunchKernelGGL(kernel, grid, dim3(512), 0, stream, op, ep, tilesM, tilesN, 8);
     return hipGetLastError() == hipSuccess ? 0 : -1;

@@ -13,6 +13,8 @@ struct EpiParams {
     float alpha;
     float beta;
     float act_alpha;
+    float act_beta;   // second activation parameter (CLIP / CLIP_V2 upper bound, LINEAR / HARDSIGMOID / HARDSWISH offset,
+                      // POW exponent)
     float gamma;
     int act;      // KUDNN_ACT_*, KUDNN_ACT_UNIMPLEMENTED = none
     int bin;      // KUDNN_BINARY_*

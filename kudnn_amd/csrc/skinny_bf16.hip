@@ -306,37 +306,35 @@ int launch_gemv(const GemmOperands &op, const EpiParams &ep, int64_t batches, hi
         } else {
             pickc(std::integral_constant<int, EPI_FORM_F32>{});
         }
-        if (ck == nullptr) {
-            return -1;
+        if (ck != nullptr) {
+            GemvArgs a{};
+            a.x = static_cast<const uint16_t *>(op.a);
+            a.w = static_cast<const uint16_t *>(op.b);
+            a.bias = ep.bias;
+            a.src = ep.src;
+            a.y = ep.y;
+            a.ldb = op.ldb;
+            a.bias_sn = ep.bias_sn;
+            a.src_sn = ep.src_sn;
+            a.y_sn = ep.y_sn;
+            a.n = static_cast<int>(op.N);
+            a.chunks = static_cast<int>((op.K + 7) / 8);
+            a.alpha = ep.alpha;
+            a.gamma = ep.gamma;
+            a.act_alpha = ep.act_alpha;
+            a.bin = ep.bin;
+            hipLaunchKernelGGL(ck, grid, dim3(256), 0, stream, a);
+            return hipGetLastError() == hipSuccess ? 0 : -1;
         }
-        GemvArgs a{};
-        a.x = static_cast<const uint16_t *>(op.a);
-        a.w = static_cast<const uint16_t *>(op.b);
-        a.bias = ep.bias;
-        a.src = ep.src;
-        a.y = ep.y;
-        a.ldb = op.ldb;
-        a.bias_sn = ep.bias_sn;
-        a.src_sn = ep.src_sn;
-        a.y_sn = ep.y_sn;
-        a.n = static_cast<int>(op.N);
-        a.chunks = static_cast<int>((op.K + 7) / 8);
-        a.alpha = ep.alpha;
-        a.gamma = ep.gamma;
-        a.act_alpha = ep.act_alpha;
-        a.bin = ep.bin;
-        hipLaunchKernelGGL(ck, grid, dim3(256), 0, stream, a);
-        return hipGetLastError() == hipSuccess ? 0 : -1;
     }
     if (form == kForm16) {
         pick(std::integral_constant<int, kForm16>{});
     } else if (form == EPI_FORM_F32) {
         pick(std::integral_constant<int, EPI_FORM_F32>{});
-    } else {
-        kernel = gemv_bf16_kernel<CT, 0, EPI_FORM_GENERIC>;  // reads the activation at run time
     }
     if (kernel == nullptr) {
-        return -1;
+        // the other activation kinds, and the other tensor types, read everything at run time
+        kernel = gemv_bf16_kernel<CT, 0, EPI_FORM_GENERIC>;
     }
     hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, op, ep);
     return hipGetLastError() == hipSuccess ? 0 : -1;

@@ -18,11 +18,17 @@ from typing import Dict, Optional, Tuple
 
 import torch
 
-from . import (ACT_GELU_ERF, ACT_GELU_TANH, ACT_RELU, ACT_SWISH, ACT_UNIMPLEMENTED, BF16, BIN_ADD, BIN_EXT, BIN_MUL,
+from . import (ACT_ABS, ACT_CLIP, ACT_CLIP_V2, ACT_ELU, ACT_ELU_DST, ACT_EXP, ACT_GELU_ERF, ACT_GELU_TANH,
+               ACT_HARDSIGMOID, ACT_HARDSWISH, ACT_LINEAR, ACT_LOG, ACT_MISH, ACT_POW, ACT_RELU, ACT_ROUND, ACT_SIGMOID,
+               ACT_SQRT, ACT_SQUARE, ACT_SRELU, ACT_SWISH, ACT_TANH, ACT_UNIMPLEMENTED, BF16, BIN_ADD, BIN_EXT, BIN_MUL,
                BIN_NONE, F32, LinearPostOps, desc, lib)
 
+# every forward kind of KuDNN's activation table; act_alpha / act_beta carry its parameters as KuDNN defines them
 _ACTS = {None: ACT_UNIMPLEMENTED, "relu": ACT_RELU, "silu": ACT_SWISH, "swish": ACT_SWISH, "gelu_tanh": ACT_GELU_TANH,
-         "gelu": ACT_GELU_ERF, "gelu_erf": ACT_GELU_ERF}
+         "gelu": ACT_GELU_ERF, "gelu_erf": ACT_GELU_ERF, "abs": ACT_ABS, "exp": ACT_EXP, "linear": ACT_LINEAR,
+         "log": ACT_LOG, "round": ACT_ROUND, "sqrt": ACT_SQRT, "square": ACT_SQUARE, "tanh": ACT_TANH,
+         "sigmoid": ACT_SIGMOID, "pow": ACT_POW, "clip": ACT_CLIP, "clip_v2": ACT_CLIP_V2, "hardsigmoid": ACT_HARDSIGMOID,
+         "hardswish": ACT_HARDSWISH, "elu": ACT_ELU, "elu_dst": ACT_ELU_DST, "srelu": ACT_SRELU, "mish": ACT_MISH}
 _BINS = {None: BIN_NONE, "add": BIN_ADD, "ext": BIN_EXT, "mul": BIN_MUL}
 _DTYPES = {torch.float32: F32, torch.bfloat16: BF16}
 
@@ -31,27 +37,31 @@ _plans_lock = threading.Lock()
 
 
 def _plan(m: int, k: int, n: int, xdt: int, wdt: int, ydt: int, has_bias: bool, act: int, act_alpha: float,
-          binary: int) -> LinearPostOps:
-    key = (m, k, n, xdt, wdt, ydt, has_bias, act, act_alpha, binary)
+          act_beta: float, binary: int) -> LinearPostOps:
+    key = (m, k, n, xdt, wdt, ydt, has_bias, act, act_alpha, act_beta, binary)
     with _plans_lock:
         plan = _plans.get(key)
         if plan is None:
             # X{M,K} AB; W{K,N} BA (physically [N][K], nn.Linear's weight); bias{1,N}; Y and the binary operand {M,N}
             dy = desc([m, n], ydt)
             plan = LinearPostOps(desc([m, k], xdt), desc([k, n], wdt, "BA"), dy, desc([1, n], ydt) if has_bias else None,
-                                 act=act, act_alpha=act_alpha, binary=binary, src=dy if binary != BIN_NONE else None)
+                                 act=act, act_alpha=act_alpha, act_beta=act_beta, binary=binary,
+                                 src=dy if binary != BIN_NONE else None)
             _plans[key] = plan
         return plan
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None, act: Optional[str] = None,
            act_alpha: Optional[float] = None, binary: Optional[str] = None, src: Optional[torch.Tensor] = None,
-           gamma: float = 1.0) -> torch.Tensor:
+           gamma: float = 1.0, act_beta: float = 0.0) -> torch.Tensor:
     """y = binary(act(x @ weight.T + bias), src) on the GPU through the KuDNN C ABI.
 
     x: [..., K] (rows are flattened to M), weight: [N, K] (nn.Linear layout), bias: [N], src: x's leading shape + [N].
-    act: None, "relu", "silu" / "swish", "gelu_tanh", "gelu" / "gelu_erf"; act_alpha defaults to 0 for relu (the
-    negative slope) and 1 for swish. binary: None, "add", "ext" (y + gamma * src), "mul". The output has x's dtype.
+    act: None, "relu", "silu" / "swish", "gelu_tanh", "gelu" / "gelu_erf", or any other forward kind of KuDNN's table
+    ("abs", "exp", "linear", "log", "round", "sqrt", "square", "tanh", "sigmoid", "pow", "clip", "clip_v2",
+    "hardsigmoid", "hardswish", "elu", "elu_dst", "srelu", "mish") with KuDNN's act_alpha / act_beta. act_alpha
+    defaults to 0 for relu (the negative slope) and 1 for swish. binary: None, "add", "ext" (y + gamma * src), "mul".
+    The output has x's dtype.
     Every rounding point is the reference's: RNE after the bias, truncating bf16 store after the activation, RNE after
     the binary op.
     """
@@ -87,7 +97,7 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
     y = torch.empty(m, n, device=x.device, dtype=x.dtype)
     if m == 0 or n == 0:
         return y.reshape(*lead, n)
-    plan = _plan(m, k, n, dt, dt, dt, b is not None, act_kind, float(alpha), bin_kind)
+    plan = _plan(m, k, n, dt, dt, dt, b is not None, act_kind, float(alpha), float(act_beta), bin_kind)
     plan.run(x2, w, y, b, s, gamma=gamma, stream=torch.cuda.current_stream())
     return y.reshape(*lead, n)
 
@@ -101,12 +111,12 @@ class KudnnLinear(torch.nn.Module):
 
     def __init__(self, in_features: int, out_features: int, bias: bool = True, act: Optional[str] = None,
                  act_alpha: Optional[float] = None, binary: Optional[str] = None, gamma: float = 1.0,
-                 device=None, dtype=torch.bfloat16):
+                 device=None, dtype=torch.bfloat16, act_beta: float = 0.0):
         super().__init__()
         if act not in _ACTS or binary not in _BINS:
             raise ValueError(f"unsupported post-op act={act!r} binary={binary!r}")
         self.in_features, self.out_features = in_features, out_features
-        self.act, self.act_alpha, self.binary, self.gamma = act, act_alpha, binary, gamma
+        self.act, self.act_alpha, self.act_beta, self.binary, self.gamma = act, act_alpha, act_beta, binary, gamma
         self.weight = torch.nn.Parameter(torch.empty(out_features, in_features, device=device, dtype=dtype),
                                          requires_grad=False)
         self.bias = torch.nn.Parameter(torch.zeros(out_features, device=device, dtype=dtype),
@@ -114,9 +124,9 @@ class KudnnLinear(torch.nn.Module):
 
     @classmethod
     def from_linear(cls, lin: torch.nn.Linear, act: Optional[str] = None, act_alpha: Optional[float] = None,
-                    binary: Optional[str] = None, gamma: float = 1.0) -> "KudnnLinear":
+                    binary: Optional[str] = None, gamma: float = 1.0, act_beta: float = 0.0) -> "KudnnLinear":
         m = cls(lin.in_features, lin.out_features, lin.bias is not None, act, act_alpha, binary, gamma,
-                device=lin.weight.device, dtype=lin.weight.dtype)
+                device=lin.weight.device, dtype=lin.weight.dtype, act_beta=act_beta)
         with torch.no_grad():
             m.weight.copy_(lin.weight)
             if lin.bias is not None:
@@ -124,7 +134,7 @@ class KudnnLinear(torch.nn.Module):
         return m
 
     def forward(self, x: torch.Tensor, src: Optional[torch.Tensor] = None) -> torch.Tensor:
-        return linear(x, self.weight, self.bias, self.act, self.act_alpha, self.binary, src, self.gamma)
+        return linear(x, self.weight, self.bias, self.act, self.act_alpha, self.binary, src, self.gamma, self.act_beta)
 
 
 _torch_linear = torch.nn.functional.linear

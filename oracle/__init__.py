@@ -21,6 +21,10 @@ LIB_PATH = _DIR / "liboracle.so"
 
 F32, F16, BF16, S32, S8, U8 = 1, 2, 3, 4, 5, 6
 ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_SWISH, ACT_GELU_ERF = 0, 5, 20, 25, 27
+# the other forward kinds (KuDNN::ActivationFunction values)
+(ACT_ABS, ACT_EXP, ACT_LINEAR, ACT_LOG, ACT_ROUND, ACT_SQRT, ACT_SQUARE, ACT_TANH, ACT_SIGMOID, ACT_POW, ACT_CLIP,
+ ACT_CLIP_V2, ACT_HARDSIGMOID, ACT_HARDSWISH, ACT_ELU, ACT_ELU_DST, ACT_SRELU, ACT_MISH) = (
+    1, 2, 3, 4, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 19, 22, 26, 28)
 RES_EXT, RES_MUL, RES_IDENTIAL = 0, 1, 2
 BIN_NONE, BIN_ADD, BIN_EXT, BIN_MUL = 0, 1, 2, 3
 
@@ -66,14 +70,14 @@ def lib() -> ctypes.CDLL:
             "oracle_bf16_to_f32": ([ctypes.c_uint16], ctypes.c_float),
             "oracle_f16_to_f32": ([ctypes.c_uint16], ctypes.c_float),
             "oracle_f32_to_f16_rne": ([ctypes.c_float], ctypes.c_uint16),
-            "oracle_act_f32": ([ctypes.c_int, ctypes.c_float, ctypes.c_float], ctypes.c_float),
-            "oracle_activation": ([T, P, ctypes.c_int, ctypes.c_float], ctypes.c_int),
+            "oracle_act_f32": ([ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_float], ctypes.c_float),
+            "oracle_activation": ([T, P, ctypes.c_int, ctypes.c_float, ctypes.c_float], ctypes.c_int),
             "oracle_gemm": ([G], ctypes.c_int),
             "oracle_res_add": ([ctypes.c_int, ctypes.c_int64, P, P, P, ctypes.c_int, ctypes.c_float], ctypes.c_int),
             "oracle_binary": ([T, P, T, P, ctypes.c_int, ctypes.c_float], ctypes.c_int),
-            "oracle_linear_act": ([G, ctypes.c_int, ctypes.c_float], ctypes.c_int),
+            "oracle_linear_act": ([G, ctypes.c_int, ctypes.c_float, ctypes.c_float], ctypes.c_int),
             "oracle_linear_res": ([G, T, P, T, P, ctypes.c_int, ctypes.c_float], ctypes.c_int),
-            "oracle_linear_postops": ([G, ctypes.c_int, ctypes.c_float, ctypes.c_int, T, P, ctypes.c_float],
+            "oracle_linear_postops": ([G, ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_int, T, P, ctypes.c_float],
                                       ctypes.c_int),
             "oracle_fill": ([P, ctypes.c_int, ctypes.c_int64, ctypes.c_uint64, ctypes.c_int, ctypes.c_double,
                              ctypes.c_double], ctypes.c_int),
@@ -197,9 +201,9 @@ def gemm(a, b, c, bias=None, alpha=1.0, beta=0.0) -> None:
     assert lib().oracle_gemm(ctypes.byref(g)) == 0
 
 
-def linear_act(a, b, c, bias=None, kind=ACT_RELU, alpha=0.0) -> None:
+def linear_act(a, b, c, bias=None, kind=ACT_RELU, alpha=0.0, beta=0.0) -> None:
     g = _gemm_struct(a, b, c, bias)
-    assert lib().oracle_linear_act(ctypes.byref(g), kind, alpha) == 0
+    assert lib().oracle_linear_act(ctypes.byref(g), kind, alpha, beta) == 0
 
 
 def linear_res(a, b, c, bias, res, lr, kind=RES_IDENTIAL, gamma=1.0) -> None:
@@ -209,15 +213,16 @@ def linear_res(a, b, c, bias, res, lr, kind=RES_IDENTIAL, gamma=1.0) -> None:
                                    gamma) == 0
 
 
-def linear_postops(a, b, y, bias=None, act=ACT_NONE, act_alpha=0.0, binary=BIN_NONE, src=None, gamma=1.0) -> None:
+def linear_postops(a, b, y, bias=None, act=ACT_NONE, act_alpha=0.0, binary=BIN_NONE, src=None, gamma=1.0,
+                   act_beta=0.0) -> None:
     g = _gemm_struct(a, b, y, bias)
     st = src.otensor() if src is not None else OTensor()
     sp = src.ptr() if src is not None else None
-    assert lib().oracle_linear_postops(ctypes.byref(g), act, act_alpha, binary, ctypes.byref(st), sp, gamma) == 0
+    assert lib().oracle_linear_postops(ctypes.byref(g), act, act_alpha, act_beta, binary, ctypes.byref(st), sp, gamma) == 0
 
 
-def act_f32(kind: int, x: float, alpha: float = 0.0) -> float:
-    return lib().oracle_act_f32(kind, x, alpha)
+def act_f32(kind: int, x: float, alpha: float = 0.0, beta: float = 0.0) -> float:
+    return lib().oracle_act_f32(kind, x, alpha, beta)
 
 
 def cpu_baseline(dt, M, N, K, X, W, bias, R, Y, act, act_alpha, threads) -> None:

@@ -46,10 +46,28 @@
 #define O_U8 6
 
 #define O_ACT_NONE 0
+#define O_ACT_ABS 1
+#define O_ACT_EXP 2
+#define O_ACT_LINEAR 3
+#define O_ACT_LOG 4
 #define O_ACT_RELU 5
+#define O_ACT_ROUND 6
+#define O_ACT_SQRT 7
+#define O_ACT_SQUARE 8
+#define O_ACT_TANH 9
+#define O_ACT_SIGMOID 10
+#define O_ACT_POW 11
+#define O_ACT_CLIP 12
+#define O_ACT_CLIP_V2 13
+#define O_ACT_HARDSIGMOID 14
+#define O_ACT_HARDSWISH 15
+#define O_ACT_ELU 19
 #define O_ACT_GELU_TANH 20
+#define O_ACT_ELU_DST 22
 #define O_ACT_SWISH 25
+#define O_ACT_SRELU 26
 #define O_ACT_GELU_ERF 27
+#define O_ACT_MISH 28
 
 #define O_RES_EXT 0
 #define O_RES_MUL 1
@@ -241,28 +259,87 @@ static float act_gelu_erf(float x)
     return s + s * erff(x * 0.70710678118654752f);
 }
 
-float oracle_act_f32(int kind, float x, float alpha)
+/* SRELU: ln(1 + e^(alpha*x)) / alpha; alpha*x at or above expf's upper bound (0x1.62e43p6) returns x, and alpha*x
+ * is clamped below at expf's lower bound (-0x1.5d58ap6) (soft_relu/vml_sve_la_softrelu.h:31-86). */
+static float act_srelu(float x, float alpha)
+{
+    const float ax = alpha * x;
+    if (ax >= 0x1.62e43p6f) {
+        return x;
+    }
+    return log1pf(expf(ax > -0x1.5d58ap6f ? ax : -0x1.5d58ap6f)) / alpha;
+}
+
+/* MISH: x * ((e^x + 1)^2 - 1) / ((e^x + 1)^2 + 1), the exponent capped at 0x1.62e42ep5 (mish/vml_sve_la_mish.h:21-35). */
+static float act_mish(float x)
+{
+    const float e1 = expf(x < 0x1.62e42ep5f ? x : 0x1.62e42ep5f) + 1.0f;
+    const float e2 = e1 * e1;
+    return x * ((e2 - 1.0f) / (e2 + 1.0f));
+}
+
+/* Every kind of the forward table (src/dnn/src/kudnn_eltwise.cpp:333-400), f32 math of the kernels' f32 sources. */
+float oracle_act_f32(int kind, float x, float alpha, float beta)
 {
     switch (kind) {
         case O_ACT_RELU: return act_relu(x, alpha);
         case O_ACT_SWISH: return act_swish(x, alpha);
         case O_ACT_GELU_TANH: return act_gelu_tanh(x);
         case O_ACT_GELU_ERF: return act_gelu_erf(x);
+        case O_ACT_ABS: return fabsf(x);                          /* abs/vml_sve_la_absf.c */
+        case O_ACT_EXP: return expf(x);                           /* exp/vml_sve_la_expf.c */
+        case O_ACT_LINEAR: return fmaf(alpha, x, beta);           /* linear.c: svmad(alpha, x, beta) */
+        case O_ACT_LOG: return logf(x);                           /* log/vml_sve_la_lnf.c */
+        case O_ACT_ROUND: return nearbyintf(x);                   /* round/vml_sve_la_nearbyintf.c (svrinti) */
+        case O_ACT_SQRT: return sqrtf(x);                         /* sqrt/vml_sve_la_sqrtf.c */
+        case O_ACT_SQUARE: return x * x;                          /* sqr/vml_sve_la_sqrf.c */
+        case O_ACT_TANH: return tanhf(x);                         /* tanh/vml_sve_la_tanhf.c */
+        case O_ACT_SIGMOID: return 1.0f / (1.0f + expf(-x));      /* logistic/sigmoid.c:71-88 */
+        case O_ACT_POW: return powf(x, beta) * alpha;             /* pow/vml_sve_powx_calculations.h:506-515 */
+        case O_ACT_CLIP:                                          /* clip/clipf.c: <= alpha, then > beta */
+            return x <= alpha ? alpha : (x > beta ? beta : x);
+        case O_ACT_CLIP_V2:                                       /* clipv2/clipv2f.c: <= alpha, then >= beta */
+            return x <= alpha ? alpha : (x >= beta ? beta : x);
+        case O_ACT_HARDSIGMOID:                                   /* hardsigmoid: maxnm(minnm(x*a + b, 1), 0) */
+            return fmaxf(fminf(fmaf(x, alpha, beta), 1.0f), 0.0f);
+        case O_ACT_HARDSWISH:                                     /* hardswish: x * max(0, min(1, a*x + b)) */
+            return x * fmaxf(fminf(fmaf(alpha, x, beta), 1.0f), 0.0f);
+        case O_ACT_ELU:                                           /* elu/vml_sve_la_eluf.c: nmls(a, e^x, a) */
+            return x > 0.0f ? x : fmaf(expf(x), alpha, -alpha);
+        case O_ACT_ELU_DST: return x > 0.0f ? x : alpha * expm1f(x);  /* elu/eludstf.c */
+        case O_ACT_SRELU: return act_srelu(x, alpha);
+        case O_ACT_MISH: return act_mish(x);
         default: return x;
+    }
+}
+
+/* bf16 store of an activation's result: RELU, CLIP, CLIP_V2, ELU, LINEAR, POW, ROUND and SRELU send finite values
+ * at or above the largest bf16 to +-Inf first (SvF32CvtBf16InfSpecial in their FWD bf16 kernels); ELU_DST rounds
+ * to nearest even (elu/eludstbf16.c, SveCvtU32ToU16); the others truncate (SvCvtBF16F32FullX). */
+static uint16_t act_store_bf16(int kind, float y)
+{
+    switch (kind) {
+        case O_ACT_RELU: case O_ACT_CLIP: case O_ACT_CLIP_V2: case O_ACT_ELU: case O_ACT_LINEAR: case O_ACT_POW:
+        case O_ACT_ROUND: case O_ACT_SRELU:
+            return oracle_f32_to_bf16_trunc_inf(y);
+        case O_ACT_ELU_DST:
+            return oracle_f32_to_bf16_rne(y);
+        default:
+            return oracle_f32_to_bf16_trunc(y);
     }
 }
 
 /* In-place activation over the tensor's elements (ActivationLayerFWD run from a copy of C back into C,
  * kudnn_linear_activationlayer.cpp:40-56). Element-wise, so the memory walk order does not matter. */
-int oracle_activation(const otensor *t, void *p, int kind, float alpha)
+int oracle_activation(const otensor *t, void *p, int kind, float alpha, float beta)
 {
     const int64_t n = total(t);
     /* dense tensor: every element sits in [0, n) */
     for (int64_t i = 0; i < n; ++i) {
         float x = ld(p, t->dtype, i);
-        float y = oracle_act_f32(kind, x, alpha);
+        float y = oracle_act_f32(kind, x, alpha, beta);
         if (t->dtype == O_BF16) {
-            ((uint16_t *)p)[i] = (kind == O_ACT_RELU) ? oracle_f32_to_bf16_trunc_inf(y) : oracle_f32_to_bf16_trunc(y);
+            ((uint16_t *)p)[i] = act_store_bf16(kind, y);
         } else {
             st(p, t->dtype, i, y);
         }
@@ -488,7 +565,7 @@ int oracle_binary(const otensor *y, void *py, const otensor *src, const void *ps
 
 /* LinearActivationLayerFWD::Run: GEMM (alpha 1, beta 0) into C, then the activation in place
  * (kudnn_linear_activationlayer.cpp:40-56). */
-int oracle_linear_act(const ogemm *g, int kind, float act_alpha)
+int oracle_linear_act(const ogemm *g, int kind, float act_alpha, float act_beta)
 {
     ogemm h = *g;
     h.alpha = 1.0f;
@@ -496,7 +573,7 @@ int oracle_linear_act(const ogemm *g, int kind, float act_alpha)
     if (oracle_gemm(&h) != 0) {
         return -1;
     }
-    return oracle_activation(&g->c, g->pc, kind, act_alpha);
+    return oracle_activation(&g->c, g->pc, kind, act_alpha, act_beta);
 }
 
 /* LinearResFWD::Run (kudnn_linear_res.cpp:184-202): GEMM into C, then RES_MUL = C x res (second GEMM) or
@@ -527,8 +604,8 @@ int oracle_linear_res(const ogemm *g, const otensor *res, const void *pres, cons
 }
 
 /* Post-op chain: GEMM stage, optional activation stage, optional binary stage, each stored in Y's dtype. */
-int oracle_linear_postops(const ogemm *g, int act_kind, float act_alpha, int bin_kind, const otensor *src,
-                          const void *psrc, float gamma)
+int oracle_linear_postops(const ogemm *g, int act_kind, float act_alpha, float act_beta, int bin_kind,
+                          const otensor *src, const void *psrc, float gamma)
 {
     ogemm h = *g;
     h.alpha = 1.0f;
@@ -537,7 +614,7 @@ int oracle_linear_postops(const ogemm *g, int act_kind, float act_alpha, int bin
         return -1;
     }
     if (act_kind != O_ACT_NONE) {
-        oracle_activation(&g->c, g->pc, act_kind, act_alpha);
+        oracle_activation(&g->c, g->pc, act_kind, act_alpha, act_beta);
     }
     if (bin_kind != O_BIN_NONE) {
         oracle_binary(&g->c, g->pc, src, psrc, bin_kind, gamma);
@@ -617,7 +694,7 @@ int oracle_cpu_baseline(int dtype, int64_t M, int64_t N, int64_t K, const void *
             if (dtype == O_BF16) {
                 v = oracle_bf16_to_f32(oracle_f32_to_bf16_rne(v));
             }
-            v = oracle_act_f32(act, v, act_alpha);
+            v = oracle_act_f32(act, v, act_alpha, 0.0f);
             if (dtype == O_BF16) {
                 v = oracle_bf16_to_f32(oracle_f32_to_bf16_trunc(v));
             }

@@ -127,10 +127,11 @@ static void TestLinearActivationNegative()
         [] { MakeLA(Ones5(), Ones5(), Ones5(), Ones5(), ActivationFunction::UNIMPLEMENTED); }));
     CHECK(Throws<Service::LogicError>(
         [] { MakeLA(Ones5(), Ones5(), Ones5(), Ones5(), ActivationFunction::UNIMPLEMENTED, -1); }));
-    // kinds KuDNN's eltwise layer accepts but that are not fused epilogues here
+    // every forward kind of KuDNN's eltwise table is a fused epilogue here; the backward-only kinds are refused
     CHECK(LinearActivationLayerFWD::ValidateInput(Ones5(), Ones5(), Ones5(), Ones5(), 1.0f, 0.0f,
                                                   ActivationFunction::TANH) == Status::SUCCESS);
-    CHECK(Throws<Service::Unsupported>([] { MakeLA(Ones5(), Ones5(), Ones5(), Ones5(), ActivationFunction::TANH); }));
+    CHECK(!Throws<Service::Unsupported>([] { MakeLA(Ones5(), Ones5(), Ones5(), Ones5(), ActivationFunction::TANH); }));
+    CHECK(Throws<Service::Unsupported>([] { MakeLA(Ones5(), Ones5(), Ones5(), Ones5(), ActivationFunction::EXP_DST); }));
     // bias pointer without a bias descriptor
     CHECK(Throws<Service::LogicError>([] {
         LinearActivationLayerFWD l(Ones5(), Ones5(), Ones5(), 1.0f, 0.0f, ActivationFunction::RELU);

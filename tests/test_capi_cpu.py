@@ -100,9 +100,16 @@ def test_linear_act_validation_and_kinds():
     a, b, c = K.desc([5, 6], F), K.desc([6, 7], F), K.desc([5, 7], F)
     v = lambda kind, alpha=0.0, beta=0.0, cc=c: K.lib().kudnn_linear_act_validate(a, b, cc, None, alpha, beta, kind, 0)
     assert v(K.ACT_RELU) == K.SUCCESS
-    assert v(K.ACT_TANH) == K.SUCCESS              # KuDNN's eltwise accepts it ...
-    with pytest.raises(K.KudnnError) as e:        # ... but it is not a fused epilogue here
-        K.LinearActivation(a, b, c, None, 0.0, 0.0, K.ACT_TANH)
+    assert v(K.ACT_TANH) == K.SUCCESS
+    # every forward kind of KuDNN's eltwise table is a fused epilogue; the backward-only kinds are refused
+    for kind in (K.ACT_ABS, K.ACT_EXP, K.ACT_LINEAR, K.ACT_LOG, K.ACT_ROUND, K.ACT_SQRT, K.ACT_SQUARE, K.ACT_TANH,
+                 K.ACT_SIGMOID, K.ACT_POW, K.ACT_CLIP, K.ACT_CLIP_V2, K.ACT_HARDSIGMOID, K.ACT_HARDSWISH, K.ACT_ELU,
+                 K.ACT_ELU_DST, K.ACT_SRELU, K.ACT_MISH):
+        K.LinearActivation(a, b, c, None, 1.0, 2.0, kind)
+    exp_dst = 16
+    assert v(exp_dst) == K.UNSUPPORTED
+    with pytest.raises(K.KudnnError) as e:
+        K.LinearActivation(a, b, c, None, 0.0, 0.0, exp_dst)
     assert e.value.status == K.UNSUPPORTED
     assert v(K.ACT_UNIMPLEMENTED) == K.UNSUPPORTED
     assert v(K.ACT_CLIP, 2.0, 1.0) == K.UNSUPPORTED  # alpha > beta

@@ -45,7 +45,7 @@ def test_cpu_and_autograd_calls_stay_with_torch():
 
 def test_argument_checks():
     with pytest.raises(ValueError):
-        T.KudnnLinear(8, 4, act="tanh")
+        T.KudnnLinear(8, 4, act="exp_dst")  # backward-only kind
     with pytest.raises(ValueError):
         T.linear(torch.randn(2, 8), torch.randn(4, 8))  # CPU tensors
 
@@ -74,6 +74,24 @@ def test_linear_matches_oracle(dtype, post):
     O.linear_postops(ox, ow, ref, ob, acts[act], alpha, bins[binary], os_, 0.5)
     got = _oracle_tensor(y.reshape(74, 80), dt).buf
     compare(got, ref.buf, dt, f"torch_linear {dtype} {post}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("act,alpha,beta,okind", [("hardswish", 1.0 / 6.0, 0.5, O.ACT_HARDSWISH),
+                                                   ("clip", -0.2, 0.3, O.ACT_CLIP), ("mish", 0.0, 0.0, O.ACT_MISH),
+                                                   ("pow", 0.5, 3.0, O.ACT_POW)])
+def test_linear_other_activation_kinds(act, alpha, beta, okind):
+    # the remaining kinds of KuDNN's table, with their act_alpha / act_beta
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(37, 96, generator=g).to(torch.bfloat16).cuda()
+    w = (torch.randn(80, 96, generator=g) * 0.1).to(torch.bfloat16).cuda()
+    y = T.linear(x, w, None, act=act, act_alpha=alpha, act_beta=beta)
+    torch.cuda.synchronize()
+    ox = _oracle_tensor(x, O.BF16)
+    ow = O.Tensor((96, 80), (1, 96), O.BF16, _oracle_tensor(w, O.BF16).buf)
+    ref = O.empty((37, 80), (80, 1), O.BF16)
+    O.linear_postops(ox, ow, ref, None, okind, alpha, O.BIN_NONE, None, 1.0, act_beta=beta)
+    compare(_oracle_tensor(y, O.BF16).buf, ref.buf, O.BF16, f"torch_linear {act}")
 
 
 @pytest.mark.gpu
