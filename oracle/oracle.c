@@ -11,8 +11,10 @@
  *                      broadcast batch loop of BatchedExtendedGemm (:767-807), bias as in AddBias (:65-149)
  *   oracle_activation  the vml FWD kernels: RELU (kernels/vml/relu/relu.c:14-49, 225-260),
  *                      SWISH (swish/vml_sve_la_swishf.c:31-47, vml_sve_la_sigmoid.h:25-47),
- *                      GELU_TANH (gelu_tanh/vml_sve_la_gelu_tanh.h:22-39), GELU_ERF (gelu_erf/vml_sve_la_gelu_erf.h:20-28);
- *                      f32 math, bf16 results truncated (vml_sve_base.h:111-118)
+ *                      GELU_TANH (gelu_tanh/vml_sve_la_gelu_tanh.h:22-39), GELU_ERF (gelu_erf/vml_sve_la_gelu_erf.h:20-28),
+ *                      and the other 18 kinds of the forward table (kudnn_eltwise.cpp:333-400), each citing its
+ *                      kernel source in oracle_act_f32; f32 math, bf16 results stored by the kind's rule
+ *                      (truncation vml_sve_base.h:111-118, overflow-to-Inf first :97-109, or RNE for ELU_DST)
  *   oracle_res_add     AddOps (src/dnn/src/kudnn_linear_res.cpp:57-122): flat element-wise over
  *                      linearRes's size, f32 math, RNE back to bf16
  *   oracle_binary      the element-wise stage of the post-op chain (ADD/EXT as AddOps; MUL element-wise)
