@@ -518,14 +518,15 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
             core.cfg = core.M == 1 ? KUDNN_CFG_GEMV_BF16 : KUDNN_CFG_SKINNY_BF16;
         } else {
             core.engine = ENGINE_MFMA_BF16;
-            auto tiles = [&](int64_t bm, int64_t bn) { return (core.M + bm - 1) / bm * ((core.N + bn - 1) / bn) * batches; };
-            if (tiles(256, 256) >= 256) {
-                core.cfg = KUDNN_CFG_BF16_PINGPONG_256x256;
-            } else if (tiles(256, 128) >= 256) {
-                core.cfg = KUDNN_CFG_BF16_256x128;
-            } else {
-                core.cfg = KUDNN_CFG_BF16_128x128;
-            }
+            // Measured on MI355X over prefill-like shapes (M 256..3072, N and K 2048..14336): the ping-pong kernel
+            // wins from about 80 tiles of 256 x 256 on, even when they fill only part of the 256 CUs (a partly busy
+            // chip runs each CU faster); with fewer tiles it still wins when K is long enough for its tail split
+            // (every tile divided over the CUs along K: at most half the CUs would be busy, at least 128 k-tiles, 24 or
+            // more per CU); otherwise the 4-wave 128 x 128 kernel, whose smaller tiles and split-K spread a small grid.
+            const int64_t t256 = (core.M + 255) / 256 * ((core.N + 255) / 256) * batches;
+            const int64_t kt = core.kp * DtSize(core.computeDt) / 128;
+            const bool tailSplit = batches == 1 && t256 * 2 <= 256 && kt >= 128 && (t256 * kt + 255) / 256 >= 24;
+            core.cfg = t256 >= 80 || tailSplit ? KUDNN_CFG_BF16_PINGPONG_256x256 : KUDNN_CFG_BF16_128x128;
         }
     } else {
         core.engine = ENGINE_MFMA_F32;
@@ -572,11 +573,24 @@ std::string DescribeCore(const GemmCore &c)
     if (ct != nullptr && at != std::string::npos) {
         cfg.replace(at, 4, ct);
     }
-    char buf[256];
-    std::snprintf(buf, sizeof(buf), "%s M=%lld N=%lld K=%lld batches=%lld%s%s%s", cfg.c_str(),
+    // the ping-pong kernel's tail split, as the launch would make it on the current device
+    char split[96] = "";
+    if (c.engine == ENGINE_MFMA_BF16 && c.cfg == KUDNN_CFG_BF16_PINGPONG_256x256) {
+        GemmOperands shape{};
+        shape.M = c.M;
+        shape.N = c.N;
+        shape.K = c.kp;
+        int dp = 0, tail = 0, iters = 0;
+        kudnn_pingpong_split(shape, c.Batches(), c.computeDt, &dp, &tail, &iters);
+        if (tail > 0) {
+            std::snprintf(split, sizeof(split), " split=%d+%d/%d", dp, tail, iters);
+        }
+    }
+    char buf[320];
+    std::snprintf(buf, sizeof(buf), "%s M=%lld N=%lld K=%lld batches=%lld%s%s%s%s", cfg.c_str(),
                   static_cast<long long>(c.M), static_cast<long long>(c.N), static_cast<long long>(c.K),
                   static_cast<long long>(c.Batches()), c.A.staticPack ? " packA" : "", c.B.staticPack ? " packB" : "",
-                  c.serial ? " serial" : "");
+                  c.serial ? " serial" : "", split);
     return buf;
 }
 
@@ -767,11 +781,14 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
     const bool mfma4 = core.engine == ENGINE_MFMA_F32 ||
                        (core.engine == ENGINE_MFMA_BF16 && core.cfg != KUDNN_CFG_BF16_PINGPONG_256x256);
     const size_t wsS = mfma4 ? align256(kudnn_gemm_workspace_bytes(shape, batches, core.cfg, core.computeDt)) : 0;
+    // the ping-pong kernel's tail split: partial tiles and arrival counters
+    const bool pingpong = core.engine == ENGINE_MFMA_BF16 && core.cfg == KUDNN_CFG_BF16_PINGPONG_256x256;
+    const size_t wsK = pingpong ? align256(kudnn_pingpong_workspace_bytes(shape, batches, core.computeDt)) : 0;
     void *ws = nullptr;
     bool acquired = false;
-    if (wsA + wsB + wsS > 0) {
+    if (wsA + wsB + wsS + wsK > 0) {
         int arc = KUDNN_STATUS_SUCCESS;
-        ws = wsp.Acquire(wsA + wsB + wsS, stream, arc);
+        ws = wsp.Acquire(wsA + wsB + wsS + wsK, stream, arc);
         if (ws == nullptr) {
             return arc;
         }
@@ -787,6 +804,7 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
         }
     } guard{wsp, stream, acquired};
     void *splitWs = wsS > 0 ? static_cast<char *>(ws) + wsA + wsB : nullptr;
+    void *tailWs = wsK > 0 ? static_cast<char *>(ws) + wsA + wsB + wsS : nullptr;
     int rc = setupOperand(core.A, a, packA, ws, op.a, op.lda, op.a_bs);
     if (rc == 0) {
         rc = setupOperand(core.B, b, packB, static_cast<char *>(ws) + wsA, op.b, op.ldb, op.b_bs);
@@ -866,7 +884,7 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
         lrc = kudnn_launch_skinny(op, ep, batches, core.computeDt, stream);
     } else if (core.engine == ENGINE_MFMA_BF16) {
         if (core.cfg == KUDNN_CFG_BF16_PINGPONG_256x256 && kudnn_pingpong_eligible(op, core.computeDt)) {
-            lrc = kudnn_launch_gemm_pingpong(op, ep, batches, core.computeDt, stream);
+            lrc = kudnn_launch_gemm_pingpong(op, ep, batches, core.computeDt, tailWs, stream);
         } else {
             // operands the ping-pong kernel cannot address (e.g. offsets beyond 2 GiB) use the 4-wave kernel
             // (no split-K workspace was reserved for the ping-pong configuration: runs unsplit)

@@ -37,6 +37,8 @@
 // argument of the kernel and the all-bf16 case has its own code, so the epilogue of a full tile is short straight-line
 // code (an epilogue that dispatched every option at run time at each of its 16 call sites made the kernel 2.2 MB and
 // spent most of its time in instruction-cache misses). Tiles that cross the matrix edge take a rolled per-element loop.
+#include <algorithm>
+#include <cstdlib>
 #include <utility>
 
 #include "device_common.h"
@@ -258,10 +260,32 @@ __device__ __forceinline__ void epilogue_int(const EpiParams &ep, const EpiBatch
     });
 }
 
-// CT: operand type, KUDNN_DT_BF16 / F16 / S8.
-template <int CT, int ACT, int FORM>
+// Tail split of the grid. Whole rounds of tiles (one tile per CU) run data-parallel, one workgroup per tile. The
+// k-iterations of the remaining tiles are divided evenly between one workgroup per CU (a second launch), so the last
+// round ends with every CU busy instead of (tiles mod CUs) of them. A tile whose iterations span several workgroups
+// is finished by the last of them to arrive: every contributor stores its accumulators (fp32, or int32 bit patterns)
+// in its slot of the workspace and takes a ticket from the tile's counter; the holder of the last ticket adds the
+// other contributors' slots to its own accumulators and runs the epilogue. No workgroup ever waits for another one.
+// The slots are written and read with agent-scope atomic stores and loads, which are coherent across the XCDs' L2
+// caches access by access, and every wave waits for its stores to complete before the ticket is taken. A device-scope
+// fence would do the same by writing back and invalidating a whole L2, which evicts the operand panels that the
+// other workgroups of that XCD are streaming.
+struct SkArgs {
+    float *part;    // nTail x maxc slots of 256 x 256 accumulators
+    uint32_t *cnt;  // nTail arrival counters, zeroed by the data-parallel launch (or by sk_zero_kernel)
+    int D;          // tiles of the data-parallel launch (whole rounds; the tail's tiles follow them in tile order)
+    int nTail;      // tiles of the tail
+    int L;          // k-iterations per tail workgroup (the last one may have fewer)
+    int maxc;       // slots per tail tile: the most workgroups any tail tile spans
+};
+
+constexpr int kSlotFloats = kBM * kBN;  // one 256 x 256 accumulator tile
+
+// CT: operand type, KUDNN_DT_BF16 / F16 / S8. SK: false for the data-parallel launch (block -> one whole tile),
+// true for the tail launch (block -> a range of k-iterations over one or more tiles).
+template <int CT, int ACT, int FORM, bool SK>
 __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, EpiParams ep, int tilesM, int tilesN,
-                                                               int group)
+                                                               int group, SkArgs sk)
 {
     constexpr uint32_t ES = CT == KUDNN_DT_S8 ? 1u : 2u;  // element size in bytes
     __shared__ uint4 a0[kTile], a1[kTile], b0[kTile], b1[kTile], b2[kTile];
@@ -276,9 +300,6 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = wave >> 2, p = wave & 3;
-    int tm, tn;
-    grouped_tile(xcd_remap(blockIdx.x, gridDim.x), tilesM, tilesN, group, tm, tn);
-    const int m0 = tm * kBM, n0 = tn * kBN;
     const int M = static_cast<int>(op.M), N = static_cast<int>(op.N), K = static_cast<int>(op.K);
 
     const int64_t batch = blockIdx.y;
@@ -289,6 +310,17 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
     const uint8_t *B = static_cast<const uint8_t *>(op.b) + (i0 * op.b_bs[0] + i1 * op.b_bs[1] + i2 * op.b_bs[2]) * ES;
     const uint32_t lda = static_cast<uint32_t>(op.lda) * ES, ldb = static_cast<uint32_t>(op.ldb) * ES;  // row pitch, bytes
     const uint32_t bytesA = static_cast<uint32_t>(op.M) * lda, bytesB = static_cast<uint32_t>(op.N) * ldb;
+    const int KT = static_cast<int>(static_cast<uint32_t>(K) * ES / kRowBytes);
+
+    // the data-parallel launch clears the tail launch's arrival counters (the tail runs after it on the stream)
+    if constexpr (!SK) {
+        if (sk.cnt != nullptr && blockIdx.x == 0 && blockIdx.y == 0) {
+            for (int i = static_cast<int>(threadIdx.x); i < sk.nTail; i += 512) sk.cnt[i] = 0u;
+        }
+    }
+
+    // the current segment: tile (m0, n0), k-tiles kb .. kb + nk - 1
+    int m0 = 0, n0 = 0, kb = 0, nk = KT;
 
     // copy addressing: a 1 KB copy covers an 8-row block q (rows 8q .. 8q+7 of the tile); lane -> row lr, LDS slot ls,
     // source chunk ls ^ ((row >> 1) & 7) = ls ^ (4 * (q & 1) + (lr >> 1))
@@ -298,11 +330,11 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
     const uint32_t loB0 = lr * ldb + static_cast<uint32_t>((ls ^ (lr >> 1)) * 16);
     const uint32_t loB1 = lr * ldb + static_cast<uint32_t>((ls ^ (4 + (lr >> 1))) * 16);
     auto copyA = [&](int q, int t, uint4 *dst) __attribute__((always_inline)) {
-        copy_block(A, bytesA, static_cast<uint32_t>(m0 + q * 8) * lda + static_cast<uint32_t>(t * kRowBytes),
+        copy_block(A, bytesA, static_cast<uint32_t>(m0 + q * 8) * lda + static_cast<uint32_t>((kb + t) * kRowBytes),
                    (q & 1) ? loA1 : loA0, dst + q * 8 * kKC);
     };
     auto copyB = [&](int q, int t, uint4 *dst) __attribute__((always_inline)) {
-        copy_block(B, bytesB, static_cast<uint32_t>(n0 + q * 8) * ldb + static_cast<uint32_t>(t * kRowBytes),
+        copy_block(B, bytesB, static_cast<uint32_t>(n0 + q * 8) * ldb + static_cast<uint32_t>((kb + t) * kRowBytes),
                    (q & 1) ? loB1 : loB0, dst + q * 8 * kKC);
     };
     // the operand this wave streams inside the loop, selected once by value (group 0: A, group 1: B)
@@ -310,7 +342,6 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
     const uint32_t sBytes = g == 0 ? bytesA : bytesB;
     const uint32_t sLd = g == 0 ? lda : ldb;
     const uint32_t sLo0 = g == 0 ? loA0 : loB0, sLo1 = g == 0 ? loA1 : loB1;
-    const int sR0 = g == 0 ? m0 : n0;
 
     // fragment addressing: rows of a 32-row block start at multiples of 32, so the swizzle term depends on lrow only
     const int lrow = lane & 31, lh = lane >> 5;
@@ -318,33 +349,7 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
     const int offA = (p * 64 + lrow) * kKC, offB = (g * 128 + lrow) * kKC;
 
     f32x16_t acc[4][2];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.0f;
-        }
-    }
     uint4 fa[4][2], fb[2][4];
-    const int KT = static_cast<int>(static_cast<uint32_t>(K) * ES / kRowBytes);
-
-    // prologue: A(0), B(0), B(1); wave w copies 8-row blocks 4w .. 4w+3 of each
-#pragma unroll
-    for (int j = 0; j < 4; ++j) copyA(wave * 4 + j, 0, a0);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) copyB(wave * 4 + j, 0, b0);
-    if (KT > 1) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) copyB(wave * 4 + j, 1, b1);
-        wait_vmcnt<4>();
-    } else {
-        wait_vmcnt<0>();
-    }
-    __builtin_amdgcn_s_barrier();
-    if (g == 1) {
-        __builtin_amdgcn_s_barrier();  // group 1 runs one phase behind
-    }
 
     auto readB = [&](const uint4 *bt, auto slotc, auto stepc) __attribute__((always_inline)) {
         constexpr int slot = decltype(slotc)::value, s = decltype(stepc)::value;
@@ -352,7 +357,7 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
 #pragma unroll
         for (int j = 0; j < 4; ++j) fb[slot][j] = bt[offB + j * 32 * kKC + sl];
     };
-    auto step = [&](auto ic, int t) __attribute__((always_inline)) {
+    auto step = [&](auto ic, int t, int sR0) __attribute__((always_inline)) {
         constexpr int I = decltype(ic)::value;
         const uint4 *at = abuf(ic);
         const uint4 *bt = bbuf(ic);
@@ -366,11 +371,11 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
         {
             const int tt = t + 1 + g;  // group 0 copies A(t+1), group 1 copies B(t+2)
             uint4 *dst = g == 0 ? abuf(std::integral_constant<int, I + 1>{}) : bbuf(std::integral_constant<int, I + 2>{});
-            if (tt < KT) {
+            if (tt < nk) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const int q = p * 8 + j;
-                    copy_block(sX, sBytes, static_cast<uint32_t>(sR0 + q * 8) * sLd + static_cast<uint32_t>(tt * kRowBytes),
+                    copy_block(sX, sBytes, static_cast<uint32_t>(sR0 + q * 8) * sLd + static_cast<uint32_t>((kb + tt) * kRowBytes),
                                (q & 1) ? sLo1 : sLo0, dst + q * 8 * kKC);
                 }
             }
@@ -411,7 +416,7 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
         // group 1's B(t+1) (B(t+2) may stay in flight)
         if (g == 0) {
             wait_vmcnt<0>();
-        } else if (t + 2 < KT) {
+        } else if (t + 2 < nk) {
             wait_vmcnt<8>();
         } else {
             wait_vmcnt<0>();
@@ -420,30 +425,174 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
     };
-    for (int t = 0; t < KT; t += 6) {
-        sfor<6>([&](auto ic) __attribute__((always_inline)) {
-            if (t + decltype(ic)::value < KT) step(ic, t + decltype(ic)::value);
-        });
-    }
-    if (g == 0) {
-        __builtin_amdgcn_s_barrier();  // matches group 1's extra barrier at the start
-    }
+
+    // Accumulates k-tiles kb .. kb + nk - 1 of tile (m0, n0) into acc (from zero) and leaves every copy landed.
+    auto mainloop = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.0f;
+            }
+        }
+        const int sR0 = g == 0 ? m0 : n0;
+        // prologue: A(0), B(0), B(1); wave w copies 8-row blocks 4w .. 4w+3 of each
+#pragma unroll
+        for (int j = 0; j < 4; ++j) copyA(wave * 4 + j, 0, a0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) copyB(wave * 4 + j, 0, b0);
+        if (nk > 1) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) copyB(wave * 4 + j, 1, b1);
+            wait_vmcnt<4>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        __builtin_amdgcn_s_barrier();
+        if (g == 1) {
+            __builtin_amdgcn_s_barrier();  // group 1 runs one phase behind
+        }
+        for (int t = 0; t < nk; t += 6) {
+            sfor<6>([&](auto ic) __attribute__((always_inline)) {
+                if (t + decltype(ic)::value < nk) step(ic, t + decltype(ic)::value, sR0);
+            });
+        }
+        if (g == 0) {
+            __builtin_amdgcn_s_barrier();  // matches group 1's extra barrier at the start
+        }
+        wait_vmcnt<0>();
+    };
 
     // ---- epilogue: wave (p, g) owns rows p*64 .. +64, columns g*128 .. +128; 4 strips of 32 columns
-    wait_vmcnt<0>();
-    // each epilogue starts with a barrier: every wave is done with the tile buffers that the staging area reuses
     // 64 x 36 floats (9 KB) per wave: waves 0-2 stage in a0, 3-5 in a1, 6-7 in b0
     float *stage = reinterpret_cast<float *>(wave < 3 ? a0 : (wave < 6 ? a1 : b0)) + (wave % 3) * (64 * kPitch);
     const EpiBatch ob = epi_batch_offsets(ep, batch);
-    const int64_t mW = m0 + p * 64, nW = n0 + g * 128;
-    if constexpr (FORM == EPI_FORM_I32) {
-        epilogue_int(ep, ob, acc, stage, lane, mW, nW, M, N);
-    } else if constexpr (FORM == EPI_FORM_GENERIC) {
-        epilogue_generic(ep, ob, acc, stage, lane, mW, nW, M, N);
-    } else if (m0 + kBM <= M && n0 + kBN <= N && (ep.bias == nullptr || ep.bias_sm == 0)) {
-        epilogue_full<ACT, FORM>(ep, ob, acc, stage, lane, mW, nW);
+    auto epilogue = [&]() __attribute__((always_inline)) {
+        // each epilogue starts with a barrier: every wave is done with the tile buffers that the staging area reuses
+        const int64_t mW = m0 + p * 64, nW = n0 + g * 128;
+        if constexpr (FORM == EPI_FORM_I32) {
+            epilogue_int(ep, ob, acc, stage, lane, mW, nW, M, N);
+        } else if constexpr (FORM == EPI_FORM_GENERIC) {
+            epilogue_generic(ep, ob, acc, stage, lane, mW, nW, M, N);
+        } else if (m0 + kBM <= M && n0 + kBN <= N && (ep.bias == nullptr || ep.bias_sm == 0)) {
+            epilogue_full<ACT, FORM>(ep, ob, acc, stage, lane, mW, nW);
+        } else {
+            epilogue_edge<ACT, FORM>(ep, ob, acc, stage, lane, mW, nW, M, N);
+        }
+    };
+
+    if constexpr (!SK) {
+        int tm, tn;
+        grouped_tile(xcd_remap(blockIdx.x, gridDim.x), tilesM, tilesN, group, tm, tn);
+        m0 = tm * kBM;
+        n0 = tn * kBN;
+        mainloop();
+        epilogue();
     } else {
-        epilogue_edge<ACT, FORM>(ep, ob, acc, stage, lane, mW, nW, M, N);
+        // this workgroup's k-iterations of the tail: [c * L, c * L + L), XCD-remapped so that the workgroups of one
+        // XCD work on neighbouring tiles
+        const int c = xcd_remap(blockIdx.x, gridDim.x);
+        const int total = sk.nTail * KT;
+        int it = c * sk.L;
+        const int end = min(it + sk.L, total);
+        // slot layout: per wave, 32 quads of 4 accumulators, 64 lanes each (1 KB per quad and wave, coalesced); a
+        // quad is two 64-bit atomic accesses
+        auto slot_at = [&](int T, int ci) __attribute__((always_inline)) {
+            return reinterpret_cast<uint64_t *>(sk.part + (static_cast<int64_t>(T) * sk.maxc + ci) * kSlotFloats) +
+                   2 * (wave * 32 * 64 + lane);
+        };
+        auto pack2 = [](float lo, float hi) __attribute__((always_inline)) {
+            return static_cast<uint64_t>(__builtin_bit_cast(uint32_t, lo)) |
+                   (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, hi)) << 32);
+        };
+        uint32_t *ticket = reinterpret_cast<uint32_t *>(b1);  // broadcast slot: b1 holds no staging area
+        while (it < end) {
+            const int T = it / KT;
+            kb = it - T * KT;
+            nk = min(KT - kb, end - it);
+            int tm, tn;
+            grouped_tile(sk.D + T, tilesM, tilesN, group, tm, tn);
+            m0 = tm * kBM;
+            n0 = tn * kBN;
+            mainloop();
+            const int cf = (T * KT) / sk.L, cl = ((T + 1) * KT - 1) / sk.L;
+            bool last = true;
+            if (cl > cf) {
+                // a shared tile: publish this workgroup's part, then take a ticket
+                uint64_t *mine = slot_at(T, c - cf);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            uint64_t *d = mine + 2 * ((j * 2 + i) * 4 + q) * 64;
+                            __hip_atomic_store(d, pack2(acc[j][i][4 * q], acc[j][i][4 * q + 1]), __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                            __hip_atomic_store(d + 1, pack2(acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]),
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        }
+                    }
+                }
+                wait_vmcnt<0>();  // this wave's part has reached the coherence point
+                __syncthreads();
+                if (threadIdx.x == 0) {
+                    // system scope: the add is performed past the XCDs' private L2 caches
+                    ticket[0] = __hip_atomic_fetch_add(&sk.cnt[T], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                }
+                __syncthreads();
+                last = ticket[0] == static_cast<uint32_t>(cl - cf);
+                if (last) {
+                    for (int ci = 0; ci <= cl - cf; ++ci) {
+                        if (ci == c - cf) continue;
+                        uint64_t *other = slot_at(T, ci);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                            for (int i = 0; i < 2; ++i) {
+#pragma unroll
+                                for (int q = 0; q < 4; ++q) {
+                                    uint64_t *src = other + 2 * ((j * 2 + i) * 4 + q) * 64;
+                                    const uint64_t v0 = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                    const uint64_t v1 = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                    const float o[4] = {__builtin_bit_cast(float, static_cast<uint32_t>(v0)),
+                                                        __builtin_bit_cast(float, static_cast<uint32_t>(v0 >> 32)),
+                                                        __builtin_bit_cast(float, static_cast<uint32_t>(v1)),
+                                                        __builtin_bit_cast(float, static_cast<uint32_t>(v1 >> 32))};
+#pragma unroll
+                                    for (int e = 0; e < 4; ++e) {
+                                        const float x = acc[j][i][4 * q + e];
+                                        if constexpr (CT == KUDNN_DT_S8) {
+                                            acc[j][i][4 * q + e] = __builtin_bit_cast(
+                                                float, __builtin_bit_cast(int, x) + __builtin_bit_cast(int, o[e]));
+                                        } else {
+                                            acc[j][i][4 * q + e] = x + o[e];
+                                        }
+                                    }
+                                }
+                            }
+                        }
+                    }
+                    if (threadIdx.x == 0) {
+                        __hip_atomic_store(&sk.cnt[T], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);  // next launch
+                    }
+                }
+            }
+            if (last) {
+                epilogue();
+            }
+            it += nk;
+            __syncthreads();  // the staging area and the ticket are tile buffers the next segment's copies overwrite
+        }
+    }
+}
+
+// Clears the tail's arrival counters when there is no data-parallel launch ahead of it.
+__global__ void sk_zero_kernel(uint32_t *cnt, int n)
+{
+    for (int i = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x); i < n; i += static_cast<int>(gridDim.x * blockDim.x)) {
+        cnt[i] = 0u;
     }
 }
 
@@ -460,29 +609,83 @@ bool kudnn_pingpong_eligible(const GemmOperands &op, int ct)
 
 namespace {
 
-template <int CT>
-int launch_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream)
+// How a launch splits into the data-parallel rounds and the tail (all zero: one data-parallel launch).
+struct SkPlan {
+    int D = 0, nTail = 0, L = 0, maxc = 0, nWG = 0;
+    size_t slotBytes = 0, bytes = 0;
+};
+
+size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
+// The tail split pays only for grids of at most half the CUs with long K (at least 128 k-tiles, 24 or more per
+// workgroup), measured on MI355X. Behind whole rounds of tiles it loses: the tail's workgroups start at k offsets
+// spread over the whole K range, so they no longer read the same A and B panels at the same time as their XCD's
+// other workgroups, and the copies that then miss the L2 cost more than the idle CUs did (C3: 441 us split against
+// 324 us unsplit). KUDNN_HIP_FORCE_STREAMK=1 forces it for any tail (tests), =0 turns it off.
+SkPlan sk_plan(const GemmOperands &op, int64_t batches, int ct)
 {
-    const int tilesM = static_cast<int>((op.M + kBM - 1) / kBM);
-    const int tilesN = static_cast<int>((op.N + kBN - 1) / kBN);
-    dim3 grid(static_cast<unsigned>(tilesM * tilesN), static_cast<unsigned>(batches));
-    // the activation and the tensor types of the epilogue select one of the compiled variants
-    decltype(&gemm_pingpong_kernel<CT, 0, EPI_FORM_GENERIC>) kernel = nullptr;
+    SkPlan s;
+    const int64_t es = ct == KUDNN_DT_S8 ? 1 : 2;
+    if (batches != 1 || op.K <= 0 || (op.K * es) % kRowBytes != 0) {
+        return s;
+    }
+    const char *f = std::getenv("KUDNN_HIP_FORCE_STREAMK");
+    const int force = f != nullptr ? std::atoi(f) : -1;
+    if (force == 0) {
+        return s;
+    }
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+        (void)hipGetLastError();
+        return s;
+    }
+    const int64_t tiles = ((op.M + kBM - 1) / kBM) * ((op.N + kBN - 1) / kBN);
+    const int KT = static_cast<int>(op.K * es / kRowBytes);
+    const int rem = static_cast<int>(tiles % cus);
+    if (rem == 0 || (force != 1 && (tiles != rem || rem * 2 > cus || KT < 128))) {
+        return s;
+    }
+    const int64_t total = static_cast<int64_t>(rem) * KT;
+    const int L = static_cast<int>((total + cus - 1) / cus);
+    if (force != 1 && L < 24) {
+        return s;
+    }
+    int maxc = 1;
+    for (int t = 0; t < rem; ++t) {
+        maxc = std::max(maxc, ((t + 1) * KT - 1) / L - (t * KT) / L + 1);
+    }
+    s.D = static_cast<int>(tiles - rem);
+    s.nTail = rem;
+    s.L = L;
+    s.maxc = maxc;
+    s.nWG = static_cast<int>((total + L - 1) / L);
+    s.slotBytes = align256(static_cast<size_t>(rem) * maxc * kSlotFloats * sizeof(float));
+    s.bytes = s.slotBytes + align256(static_cast<size_t>(rem) * sizeof(uint32_t));
+    return s;
+}
+
+using PingpongKernel = decltype(&gemm_pingpong_kernel<KUDNN_DT_BF16, 0, EPI_FORM_GENERIC, false>);
+
+// The activation and the tensor types of the epilogue select one of the compiled variants.
+template <int CT, bool SK>
+PingpongKernel select_pingpong(const EpiParams &ep)
+{
+    PingpongKernel kernel = nullptr;
     const int form = epi_form(ep);
     if constexpr (CT == KUDNN_DT_S8) {
-        if (form != EPI_FORM_I32) {
-            return -1;
+        if (form == EPI_FORM_I32) {
+            kernel = gemm_pingpong_kernel<CT, 0, EPI_FORM_I32, SK>;
         }
-        kernel = gemm_pingpong_kernel<CT, 0, EPI_FORM_I32>;
     } else {
         auto pick = [&](auto formc) {
             constexpr int F = decltype(formc)::value;
             switch (ep.act) {
-                case KUDNN_ACT_UNIMPLEMENTED: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_UNIMPLEMENTED, F>; break;
-                case KUDNN_ACT_RELU: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_RELU, F>; break;
-                case KUDNN_ACT_SWISH: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_SWISH, F>; break;
-                case KUDNN_ACT_GELU_TANH: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_GELU_TANH, F>; break;
-                case KUDNN_ACT_GELU_ERF: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_GELU_ERF, F>; break;
+                case KUDNN_ACT_UNIMPLEMENTED: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_UNIMPLEMENTED, F, SK>; break;
+                case KUDNN_ACT_RELU: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_RELU, F, SK>; break;
+                case KUDNN_ACT_SWISH: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_SWISH, F, SK>; break;
+                case KUDNN_ACT_GELU_TANH: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_GELU_TANH, F, SK>; break;
+                case KUDNN_ACT_GELU_ERF: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_GELU_ERF, F, SK>; break;
                 default: break;
             }
         };
@@ -500,27 +703,70 @@ int launch_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches
         }
         if (kernel == nullptr && form != EPI_FORM_I32) {
             // the other activation kinds, and the other tensor types, read everything at run time
-            kernel = gemm_pingpong_kernel<CT, 0, EPI_FORM_GENERIC>;
+            kernel = gemm_pingpong_kernel<CT, 0, EPI_FORM_GENERIC, SK>;
         }
     }
-    if (kernel == nullptr) {
+    return kernel;
+}
+
+template <int CT>
+int launch_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, void *ws, hipStream_t stream)
+{
+    const int tilesM = static_cast<int>((op.M + kBM - 1) / kBM);
+    const int tilesN = static_cast<int>((op.N + kBN - 1) / kBN);
+    const SkPlan s = ws != nullptr ? sk_plan(op, batches, CT) : SkPlan{};
+    SkArgs args{};
+    if (s.nTail > 0) {
+        args.part = static_cast<float *>(ws);
+        args.cnt = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + s.slotBytes);
+        args.D = s.D;
+        args.nTail = s.nTail;
+        args.L = s.L;
+        args.maxc = s.maxc;
+    }
+    PingpongKernel dp = select_pingpong<CT, false>(ep);
+    PingpongKernel tail = s.nTail > 0 ? select_pingpong<CT, true>(ep) : nullptr;
+    if (dp == nullptr || (s.nTail > 0 && tail == nullptr)) {
         return -1;
     }
-    hipLaunchKernelGGL(kernel, grid, dim3(512), 0, stream, op, ep, tilesM, tilesN, 8);
+    const int dpTiles = s.nTail > 0 ? s.D : tilesM * tilesN;
+    if (dpTiles > 0) {
+        dim3 grid(static_cast<unsigned>(dpTiles), static_cast<unsigned>(batches));
+        hipLaunchKernelGGL(dp, grid, dim3(512), 0, stream, op, ep, tilesM, tilesN, 8, args);
+    } else {
+        hipLaunchKernelGGL(sk_zero_kernel, dim3(1), dim3(256), 0, stream, args.cnt, args.nTail);
+    }
+    if (s.nTail > 0) {
+        hipLaunchKernelGGL(tail, dim3(static_cast<unsigned>(s.nWG)), dim3(512), 0, stream, op, ep, tilesM, tilesN, 8, args);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 }  // namespace
 
-int kudnn_launch_gemm_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, int ct, hipStream_t stream)
+size_t kudnn_pingpong_workspace_bytes(const GemmOperands &op, int64_t batches, int ct)
+{
+    return sk_plan(op, batches, ct).bytes;
+}
+
+void kudnn_pingpong_split(const GemmOperands &op, int64_t batches, int ct, int *dpTiles, int *tailTiles, int *iters)
+{
+    const SkPlan s = sk_plan(op, batches, ct);
+    *dpTiles = s.D;
+    *tailTiles = s.nTail;
+    *iters = s.L;
+}
+
+int kudnn_launch_gemm_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, int ct, void *ws,
+                               hipStream_t stream)
 {
     if (!kudnn_pingpong_eligible(op, ct)) {
         return -1;
     }
     switch (ct) {
-        case KUDNN_DT_BF16: return launch_pingpong<KUDNN_DT_BF16>(op, ep, batches, stream);
-        case KUDNN_DT_F16: return launch_pingpong<KUDNN_DT_F16>(op, ep, batches, stream);
-        case KUDNN_DT_S8: return launch_pingpong<KUDNN_DT_S8>(op, ep, batches, stream);
+        case KUDNN_DT_BF16: return launch_pingpong<KUDNN_DT_BF16>(op, ep, batches, ws, stream);
+        case KUDNN_DT_F16: return launch_pingpong<KUDNN_DT_F16>(op, ep, batches, ws, stream);
+        case KUDNN_DT_S8: return launch_pingpong<KUDNN_DT_S8>(op, ep, batches, ws, stream);
         default: return -1;
     }
 }

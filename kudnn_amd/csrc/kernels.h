@@ -30,7 +30,14 @@ int kudnn_launch_gemm_mfma(const GemmOperands &op, const EpiParams &ep, int64_t 
 // 8-wave ping-pong schedule, 256x256 tile (gemm_pingpong.hip). Needs K a whole number of 128-byte k-tiles, 16-byte
 // aligned rows and 32-bit operand offsets; kudnn_pingpong_eligible says whether `op` qualifies.
 bool kudnn_pingpong_eligible(const GemmOperands &op, int ct);
-int kudnn_launch_gemm_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, int ct, hipStream_t stream);
+// Bytes of workspace the launch wants for its tail split (0: one data-parallel launch); `ws` of at least that many
+// bytes, or nullptr to run without the split.
+size_t kudnn_pingpong_workspace_bytes(const GemmOperands &op, int64_t batches, int ct);
+// The split the launch would make: tiles of the data-parallel launch, tail tiles, k-iterations per tail workgroup
+// (all 0 when it makes none).
+void kudnn_pingpong_split(const GemmOperands &op, int64_t batches, int ct, int *dpTiles, int *tailTiles, int *iters);
+int kudnn_launch_gemm_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, int ct, void *ws,
+                               hipStream_t stream);
 int kudnn_launch_gemm_f32(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, void *ws,
                           hipStream_t stream);
 // M <= 16, bf16 or f16 operands (`ct`), B contiguous along K (M == 1: row-per-wave GEMV, otherwise 16-row MFMA tiles).

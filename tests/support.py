@@ -95,6 +95,13 @@ def compare(got_buf: np.ndarray, ref_buf: np.ndarray, dt: int, what: str = ""):
     return maxnorm, exact
 
 
+def dense_rows(t: O.Tensor, rows) -> O.Tensor:
+    """Rows of a dense row-major tensor viewed as [rows, last dim]."""
+    last = t.dims[-1]
+    buf = t.buf.reshape(-1, last)[rows].copy().reshape(-1)
+    return O.Tensor((len(rows), last), (last, 1), t.dtype, buf)
+
+
 def sample_rows(m: int, count: int, seed: int = 1234) -> np.ndarray:
     rng = np.random.default_rng(seed)
     fixed = [0, 1, m // 2, m - 2, m - 1]

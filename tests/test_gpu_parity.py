@@ -9,7 +9,7 @@ import pytest
 
 import kudnn_amd as K
 import oracle as O
-from support import Case, compare, from_device, sample_rows, zeros_device
+from support import Case, compare, dense_rows, from_device, sample_rows, zeros_device
 
 pytestmark = pytest.mark.gpu
 
@@ -21,13 +21,6 @@ def _gpu():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     K.lib()  # fail loudly if the HIP library is missing
-
-
-def dense_rows(t: O.Tensor, rows) -> O.Tensor:
-    """Rows of a dense row-major tensor viewed as [rows, last dim]."""
-    last = t.dims[-1]
-    buf = t.buf.reshape(-1, last)[rows].copy().reshape(-1)
-    return O.Tensor((len(rows), last), (last, 1), t.dtype, buf)
 
 
 def as2d(t: O.Tensor) -> O.Tensor:
