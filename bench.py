@@ -17,9 +17,12 @@ reports the ramp rather than the kernel (10-15 % slower per step over the first 
 For profiling, --only c3 runs just the C3 step (JSON line without decode or CPU baseline), --only decode just the
 decode lines, and --only copy runs an
 elementwise copy-like kernel (y = -x, 512 MiB bf16 in, 512 MiB out) whose known traffic calibrates the
-FETCH_SIZE / WRITE_SIZE counters against which the C3 kernel's HBM traffic is read.
+FETCH_SIZE / WRITE_SIZE counters against which the C3 kernel's HBM traffic is read. --only dispatch times a bf16
+Linear + GELU(tanh) over prefill-like shapes under every kernel configuration (forced through KUDNN_HIP_FORCE_CFG and
+KUDNN_HIP_FORCE_STREAMK) and under the planner's own choice, one JSON line per shape: the measurement the
+dispatcher's rule is drawn from.
 
-Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--prewarm-ms 300] [--only c3|copy]
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--prewarm-ms 300] [--only c3|copy|decode|dispatch]
 """
 from __future__ import annotations
 
@@ -47,7 +50,7 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--prewarm-ms", type=float, default=300.0, help="untimed run time before warmup (clock ramp)")
-    p.add_argument("--only", choices=["c3", "copy", "decode"], default=None,
+    p.add_argument("--only", choices=["c3", "copy", "decode", "dispatch"], default=None,
                    help="profiling modes (see module docstring)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-decode", action="store_true")
@@ -288,6 +291,49 @@ def cpu_baseline(args, np):
             "seconds": dt}
 
 
+def bench_dispatch(args, torch, K):
+    """Every bf16 kernel configuration against the planner's choice over prefill-like shapes (microseconds per call;
+    CUDA events around `--steps` back-to-back calls after `--warmup`)."""
+    configs = [("pingpong", "4", "0"), ("pingpong_split", "4", "1"), ("4wave_256x128", "2", "0"),
+               ("4wave_128x128", "3", "0"), ("4wave_256x256", "1", "0"), ("planner", None, None)]
+    saved = {k: os.environ.get(k) for k in ("KUDNN_HIP_FORCE_CFG", "KUDNN_HIP_FORCE_STREAMK")}
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for M in (256, 512, 1024, 2048, 3072):
+        for N, Kd in ((4096, 4096), (11008, 4096), (4096, 11008), (14336, 4096), (4096, 14336), (2048, 2048),
+                      (8192, 8192)):
+            x = torch.randn(M, Kd, device="cuda", generator=g).to(torch.bfloat16)
+            w = (torch.randn(N, Kd, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+            y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+            line = {"M": M, "N": N, "K": Kd}
+            for name, cfg, split in configs:
+                for key, val in (("KUDNN_HIP_FORCE_CFG", cfg), ("KUDNN_HIP_FORCE_STREAMK", split)):
+                    if val is None:
+                        os.environ.pop(key, None)
+                    else:
+                        os.environ[key] = val
+                plan = K.LinearPostOps(K.desc([M, Kd], K.BF16), K.desc([Kd, N], K.BF16, "BA"), K.desc([M, N], K.BF16),
+                                       None, act=K.ACT_GELU_TANH)
+                for _ in range(args.warmup):
+                    plan.run(x, w, y)
+                torch.cuda.synchronize()
+                t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                t0.record()
+                for _ in range(args.steps):
+                    plan.run(x, w, y)
+                t1.record()
+                torch.cuda.synchronize()
+                line[name] = round(t0.elapsed_time(t1) / args.steps * 1e3, 1)
+                if cfg is None:
+                    line["planner_plan"] = plan.describe()
+            print(json.dumps(line), flush=True)
+            del x, w, y
+    for key, val in saved.items():
+        if val is None:
+            os.environ.pop(key, None)
+        else:
+            os.environ[key] = val
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -312,6 +358,10 @@ def main():
         ms, _ = time_launches(lambda i=0: torch.neg(x, out=y), args.steps, args.warmup, torch, stream, 0.0)
         print(json.dumps({"kernel": "copy-like elementwise (torch.neg, bf16)", "bytes_read": 2 * n,
                           "bytes_written": 2 * n, "ms": round(ms, 4), "GB/s": round(4 * n / (ms * 1e-3) / 1e9, 1)}))
+        return
+
+    if args.only == "dispatch":
+        bench_dispatch(args, torch, K)
         return
 
     if args.only == "decode":
