@@ -701,6 +701,16 @@ __device__ __forceinline__ Pre8 epi_prefetch8(const EpiParams &e, const EpiBatch
     return Pre8{epi_prefetch8_src<FORM>(e, ob, m, n), epi_prefetch8_bias<FORM>(e, ob, m, n)};
 }
 
+// 16-byte store of a result that no later step of the kernel reads: non-temporal, so the L2 does not allocate lines
+// for it (C3: 3 % faster than an ordinary store). Loads of the binary operand stay ordinary: made non-temporal as
+// well, they were slower.
+__device__ __forceinline__ void store16_stream(void *p, uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3)
+{
+    typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+    const u32x4_t v = {w0, w1, w2, w3};
+    __builtin_nontemporal_store(v, static_cast<u32x4_t *>(p));
+}
+
 // Epilogue of the 8-column group (m, n .. n+7), all in bounds, operands from epi_prefetch8.
 template <int ACT, int FORM>
 __device__ __forceinline__ void epi_fast8(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, const float acc[8],
@@ -750,18 +760,18 @@ __device__ __forceinline__ void epi_fast8(const EpiParams &e, const EpiBatch &ob
         uint32_t w[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) w[q] = pack_bf16x2_rne(v[2 * q], v[2 * q + 1]);
-        *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(e.y) + yi) = make_uint4(w[0], w[1], w[2], w[3]);
+        store16_stream(static_cast<uint16_t *>(e.y) + yi, w[0], w[1], w[2], w[3]);
     } else if constexpr (FORM == EPI_FORM_F16) {
         uint32_t w[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             w[q] = static_cast<uint32_t>(f32_to_f16_rne(v[2 * q])) | (static_cast<uint32_t>(f32_to_f16_rne(v[2 * q + 1])) << 16);
         }
-        *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(e.y) + yi) = make_uint4(w[0], w[1], w[2], w[3]);
+        store16_stream(static_cast<uint16_t *>(e.y) + yi, w[0], w[1], w[2], w[3]);
     } else {
         float *yp = static_cast<float *>(e.y) + yi;
-        *reinterpret_cast<float4 *>(yp) = make_float4(v[0], v[1], v[2], v[3]);
-        *reinterpret_cast<float4 *>(yp + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        store16_stream(yp, f2u(v[0]), f2u(v[1]), f2u(v[2]), f2u(v[3]));
+        store16_stream(yp + 4, f2u(v[4]), f2u(v[5]), f2u(v[6]), f2u(v[7]));
     }
 }
 
