@@ -264,8 +264,9 @@ __device__ __forceinline__ void epilogue_int(const EpiParams &ep, const EpiBatch
 // k-iterations of the remaining tiles are divided evenly between one workgroup per CU (a second launch), so the last
 // round ends with every CU busy instead of (tiles mod CUs) of them. A tile whose iterations span several workgroups
 // is finished by the last of them to arrive: every contributor stores its accumulators (fp32, or int32 bit patterns)
-// in its slot of the workspace and takes a ticket from the tile's counter; the holder of the last ticket adds the
-// other contributors' slots to its own accumulators and runs the epilogue. No workgroup ever waits for another one.
+// in its slot of the workspace and takes a ticket from the tile's counter; the holder of the last ticket sums all the
+// slots, its own included, in contributor order (so the result does not depend on which workgroup arrives last) and
+// runs the epilogue. No workgroup ever waits for another one.
 // The slots are written and read with agent-scope atomic stores and loads, which are coherent across the XCDs' L2
 // caches access by access, and every wave waits for its stores to complete before the ticket is taken. A device-scope
 // fence would do the same by writing back and invalidating a whole L2, which evicts the operand panels that the
@@ -544,31 +545,30 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
                 __syncthreads();
                 last = ticket[0] == static_cast<uint32_t>(cl - cf);
                 if (last) {
+                    // acc = slot 0 + slot 1 + ... in contributor order, whoever arrived last
                     for (int ci = 0; ci <= cl - cf; ++ci) {
-                        if (ci == c - cf) continue;
-                        uint64_t *other = slot_at(T, ci);
+                        uint64_t *part = slot_at(T, ci);
 #pragma unroll
                         for (int j = 0; j < 4; ++j) {
 #pragma unroll
                             for (int i = 0; i < 2; ++i) {
 #pragma unroll
                                 for (int q = 0; q < 4; ++q) {
-                                    uint64_t *src = other + 2 * ((j * 2 + i) * 4 + q) * 64;
+                                    uint64_t *src = part + 2 * ((j * 2 + i) * 4 + q) * 64;
                                     const uint64_t v0 = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                                     const uint64_t v1 = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                                    const float o[4] = {__builtin_bit_cast(float, static_cast<uint32_t>(v0)),
-                                                        __builtin_bit_cast(float, static_cast<uint32_t>(v0 >> 32)),
-                                                        __builtin_bit_cast(float, static_cast<uint32_t>(v1)),
-                                                        __builtin_bit_cast(float, static_cast<uint32_t>(v1 >> 32))};
+                                    const uint32_t o[4] = {static_cast<uint32_t>(v0), static_cast<uint32_t>(v0 >> 32),
+                                                           static_cast<uint32_t>(v1), static_cast<uint32_t>(v1 >> 32)};
 #pragma unroll
                                     for (int e = 0; e < 4; ++e) {
                                         const float x = acc[j][i][4 * q + e];
+                                        float r;
                                         if constexpr (CT == KUDNN_DT_S8) {
-                                            acc[j][i][4 * q + e] = __builtin_bit_cast(
-                                                float, __builtin_bit_cast(int, x) + __builtin_bit_cast(int, o[e]));
+                                            r = __builtin_bit_cast(float, __builtin_bit_cast(int, x) + __builtin_bit_cast(int, o[e]));
                                         } else {
-                                            acc[j][i][4 * q + e] = x + o[e];
+                                            r = x + __builtin_bit_cast(float, o[e]);
                                         }
+                                        acc[j][i][4 * q + e] = ci == 0 ? __builtin_bit_cast(float, o[e]) : r;
                                     }
                                 }
                             }

@@ -476,29 +476,25 @@ def test_c3_plan_uses_pingpong():
     assert plan.describe().startswith("mfma_bf16_pingpong_256x256")
 
 
-@pytest.mark.parametrize("shape", ["pingpong", "split_k", "gemv"])
-def test_hip_graph_capture_replays(shape):
+@pytest.mark.parametrize("shape", ["pingpong", "split_k", "gemv", "pingpong_ksplit"])
+def test_hip_graph_capture_replays(monkeypatch, shape):
     # a plan's run captured into a HIP graph (after one eager run, which sizes the plan's workspace) and replayed
-    # three times with eager work in between; every replay must equal the eager result
+    # three times with eager work in between; every replay must equal the eager result bit for bit (the ping-pong
+    # K-split included: its last-arriving workgroup sums the partial tiles in a fixed order)
     dt = O.BF16
-    M, N, Kd = {"pingpong": (512, 512, 256), "split_k": (100, 200, 2048), "gemv": (1, 300, 1024)}[shape]
+    M, N, Kd = {"pingpong": (512, 512, 256), "split_k": (100, 200, 2048), "gemv": (1, 300, 1024),
+                "pingpong_ksplit": (300, 520, 1024)}[shape]
     x = Case([M, Kd], dt, seed=250, dist="normal", lo=0.0, hi=1.0)
     w = Case([Kd, N], dt, "BA", seed=251, dist="normal", lo=0.0, hi=0.05)
     s = Case([M, N], dt, seed=252, lo=-1.0, hi=1.0)
     y = Case([M, N], dt, zero=True)
-    force = {"pingpong": "4", "split_k": None, "gemv": None}[shape]
-    import os
-    old = os.environ.get("KUDNN_HIP_FORCE_CFG")
-    if force:
-        os.environ["KUDNN_HIP_FORCE_CFG"] = force
-    try:
-        plan = K.LinearPostOps(x.desc, w.desc, y.desc, None, act=K.ACT_GELU_TANH, binary=K.BIN_ADD, src=s.desc)
-    finally:
-        if force:
-            if old is None:
-                del os.environ["KUDNN_HIP_FORCE_CFG"]
-            else:
-                os.environ["KUDNN_HIP_FORCE_CFG"] = old
+    if shape.startswith("pingpong"):
+        monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "4")
+    if shape == "pingpong_ksplit":
+        monkeypatch.setenv("KUDNN_HIP_FORCE_STREAMK", "1")  # read at every launch: stays set for the runs
+    plan = K.LinearPostOps(x.desc, w.desc, y.desc, None, act=K.ACT_GELU_TANH, binary=K.BIN_ADD, src=s.desc)
+    if shape == "pingpong_ksplit":
+        assert " split=" in plan.describe(), plan.describe()
     dx, dw, ds = x.device(), w.device(), s.device()
     eager = zeros_device(y)
     stream = torch.cuda.Stream()
