@@ -637,17 +637,41 @@ public:
         if (ptr_ != nullptr) {
             (void)hipFree(ptr_);  // waits for work that still uses it
         }
+        if (cnt_ != nullptr) {
+            (void)hipFree(cnt_);
+        }
         if (done_ != nullptr) {
             (void)hipEventDestroy(done_);
         }
     }
 
     // Locks the workspace and returns at least `bytes` of device memory ordered after its previous use, or nullptr
-    // with `rc` set. Every successful Acquire is paired with one Release on the same stream.
-    void *Acquire(size_t bytes, hipStream_t stream, int &rc)
+    // with `rc` set. Every successful Acquire is paired with one Release on the same stream. With `counters`, also
+    // hands out the split-K arrival counters: a separate buffer of KUDNN_SPLIT_MAX_TILES uint32 that nothing else
+    // writes, zeroed on the stream when it is allocated and left zero by every split launch.
+    void *Acquire(size_t bytes, hipStream_t stream, int &rc, uint32_t **counters = nullptr)
     {
         rc = KUDNN_STATUS_SUCCESS;
         m_.lock();
+        if (counters != nullptr) {
+            if (cnt_ == nullptr) {
+                const size_t cb = KUDNN_SPLIT_MAX_TILES * sizeof(uint32_t);
+                hipError_t e = hipMalloc(&cnt_, cb);
+                if (e == hipSuccess) {
+                    e = hipMemsetAsync(cnt_, 0, cb, stream);
+                }
+                if (e != hipSuccess) {
+                    if (cnt_ != nullptr) {
+                        (void)hipFree(cnt_);
+                        cnt_ = nullptr;
+                    }
+                    m_.unlock();
+                    rc = Fail(KUDNN_STATUS_ALLOC_FAILED, std::string("split-K counters: ") + hipGetErrorString(e));
+                    return nullptr;
+                }
+            }
+            *counters = static_cast<uint32_t *>(cnt_);
+        }
         if (bytes > bytes_) {
             if (ptr_ != nullptr) {
                 (void)hipFree(ptr_);
@@ -701,6 +725,7 @@ public:
 private:
     std::mutex m_;
     void *ptr_ = nullptr;
+    void *cnt_ = nullptr;
     size_t bytes_ = 0;
     hipEvent_t done_ = nullptr;
     hipStream_t last_ = nullptr;
@@ -786,9 +811,10 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
     const size_t wsK = pingpong ? align256(kudnn_pingpong_workspace_bytes(shape, batches, core.computeDt)) : 0;
     void *ws = nullptr;
     bool acquired = false;
+    uint32_t *counters = nullptr;
     if (wsA + wsB + wsS + wsK > 0) {
         int arc = KUDNN_STATUS_SUCCESS;
-        ws = wsp.Acquire(wsA + wsB + wsS + wsK, stream, arc);
+        ws = wsp.Acquire(wsA + wsB + wsS + wsK, stream, arc, wsS > 0 ? &counters : nullptr);
         if (ws == nullptr) {
             return arc;
         }
@@ -889,10 +915,10 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
             // operands the ping-pong kernel cannot address (e.g. offsets beyond 2 GiB) use the 4-wave kernel
             // (no split-K workspace was reserved for the ping-pong configuration: runs unsplit)
             const int cfg = core.cfg == KUDNN_CFG_BF16_PINGPONG_256x256 ? KUDNN_CFG_BF16_256x256 : core.cfg;
-            lrc = kudnn_launch_gemm_mfma(op, ep, batches, cfg, core.computeDt, splitWs, stream);
+            lrc = kudnn_launch_gemm_mfma(op, ep, batches, cfg, core.computeDt, splitWs, counters, stream);
         }
     } else {
-        lrc = kudnn_launch_gemm_f32(op, ep, batches, core.cfg, splitWs, stream);
+        lrc = kudnn_launch_gemm_f32(op, ep, batches, core.cfg, splitWs, counters, stream);
     }
     hipError_t le = hipGetLastError();
     if (lrc != 0 || le != hipSuccess) {

@@ -29,9 +29,10 @@
 //  - The activation and the epilogue's tensor types are template arguments (see the forms in device_common.h):
 //    full tiles in the bf16 / f32 forms run short straight-line code; other tiles and the generic form go one
 //    element at a time.
-//  - Split-K for grids too small to fill the chip: grid.z splits the k-tiles, each split writes its raw f32 partial
-//    tile to a workspace (form EPI_FORM_PARTIAL), and splitk_reduce_kernel sums the splits in split order (the same
-//    bits on every run) and applies the epilogue.
+//  - Split-K for grids too small to fill the chip, in one launch: grid.z splits the k-tiles; every split stores its
+//    accumulators in its slot of the workspace and takes a ticket from the tile's arrival counter, and the split that
+//    draws the last ticket sums the slots in split order (the same bits whichever split finishes last) and runs the
+//    epilogue. No workgroup waits for another.
 // Requirements (the dispatcher packs operands otherwise): K a multiple of the k-tile, rows 16-byte
 // aligned. Rows past M / N are clamped (read but never stored).
 #include <algorithm>
@@ -97,13 +98,17 @@ __device__ __forceinline__ void static_for(F &&f)
     static_for_impl(std::make_integer_sequence<int, N>{}, f);
 }
 
-// Raw f32 partial tiles of a split-K launch: split z of output (m, n) at partial[z * M * N + m * N + n].
-constexpr int EPI_FORM_PARTIAL = 3;
+// Split-K state of a launch with grid.z > 1: slots of BM x BN accumulators, tile-major then split, and one arrival
+// counter per tile, zero before the launch and left at zero by it.
+struct SplitArgs {
+    float *part;
+    uint32_t *cnt;
+};
 
 // CT: compute (operand) type, KUDNN_DT_F32 / BF16 / F16 / S8.
 template <int CT, int BM, int BN, int WM, int WN, int ST, int ACT, int FORM>
 __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands op, EpiParams ep, int tilesM,
-                                                                  int tilesN, int group, float *partial)
+                                                                  int tilesN, int group, SplitArgs sa)
 {
     constexpr bool F32 = CT == KUDNN_DT_F32;
     using T = typename std::conditional<F32, float, typename std::conditional<CT == KUDNN_DT_S8, int8_t, uint16_t>::type>::type;
@@ -273,6 +278,76 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
         }
     }
 
+    // Split-K: this split's accumulators go to its slot with agent-scope atomic stores (coherent across the XCDs' L2
+    // caches access by access; a device-scope fence would write back and invalidate a whole L2), every wave waits for
+    // its stores, and one ticket per split is drawn. The holder of the last ticket rebuilds the sum in split order.
+    if constexpr (CT != KUDNN_DT_S8) {
+        if (gridDim.z > 1) {
+            constexpr int QPW = FN * FM * 4;  // 16-byte quads of accumulators per lane
+            constexpr int64_t kSlot = static_cast<int64_t>(BM) * BN / 2;  // uint64 per slot
+            uint64_t *tileSlots = reinterpret_cast<uint64_t *>(sa.part) + static_cast<int64_t>(blockIdx.x) * gridDim.z * kSlot;
+            auto at = [&](uint64_t *slot, int qd) { return slot + 2 * ((wave * QPW + qd) * 64 + lane); };
+            uint64_t *mine = tileSlots + static_cast<int64_t>(blockIdx.z) * kSlot;
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+#pragma unroll
+                for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        uint64_t *d = at(mine, (j * FM + i) * 4 + g);
+                        // the elements are copied out first: __builtin_bit_cast applied to an element of an
+                        // ext_vector_type reads element 0 with this compiler
+                        const float e0 = acc[j][i][4 * g], e1 = acc[j][i][4 * g + 1];
+                        const float e2 = acc[j][i][4 * g + 2], e3 = acc[j][i][4 * g + 3];
+                        const uint64_t lo = static_cast<uint64_t>(__builtin_bit_cast(uint32_t, e0)) |
+                                            (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, e1)) << 32);
+                        const uint64_t hi = static_cast<uint64_t>(__builtin_bit_cast(uint32_t, e2)) |
+                                            (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, e3)) << 32);
+                        __hip_atomic_store(d, lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        __hip_atomic_store(d + 1, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's part has reached the coherence point
+            __syncthreads();                     // also: every wave is past the k-loop's LDS reads
+            uint32_t *ticket = reinterpret_cast<uint32_t *>(lds);
+            if (tid == 0) {
+                // system scope: the add is performed past the XCDs' private L2 caches
+                ticket[0] = __hip_atomic_fetch_add(&sa.cnt[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+            __syncthreads();
+            if (ticket[0] != gridDim.z - 1) {
+                return;  // another split finishes this tile
+            }
+            for (int z = 0; z < static_cast<int>(gridDim.z); ++z) {
+                uint64_t *part = tileSlots + static_cast<int64_t>(z) * kSlot;
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+#pragma unroll
+                    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) {
+                            uint64_t *src = at(part, (j * FM + i) * 4 + g);
+                            const uint64_t lo = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            const uint64_t hi = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            const float o[4] = {__builtin_bit_cast(float, static_cast<uint32_t>(lo)),
+                                                __builtin_bit_cast(float, static_cast<uint32_t>(lo >> 32)),
+                                                __builtin_bit_cast(float, static_cast<uint32_t>(hi)),
+                                                __builtin_bit_cast(float, static_cast<uint32_t>(hi >> 32))};
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                acc[j][i][4 * g + e] = z == 0 ? o[e] : acc[j][i][4 * g + e] + o[e];
+                            }
+                        }
+                    }
+                }
+            }
+            if (tid == 0) {
+                __hip_atomic_store(&sa.cnt[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);  // next launch
+            }
+        }
+    }
+
     // Epilogue through LDS, one 32-column strip of each wave tile at a time. The strip index is a
     // compile-time constant (static_for) so the accumulators stay in registers. Lanes then read the strip
     // back row-major: 4 lanes per row, 8 columns per lane, 16 rows per pass.
@@ -294,23 +369,7 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
         }
         __syncthreads();
         const int64_t n = n0 + wn * TN + j * 32 + col8;
-        if constexpr (FORM == EPI_FORM_PARTIAL) {
-            float *part = partial + static_cast<int64_t>(blockIdx.z) * M * N;
-#pragma unroll 1
-            for (int r = lane >> 2; r < TM; r += 16) {
-                const int64_t m = m0 + wm * TM + r;
-                if (m >= M) {
-                    continue;
-                }
-                const float *src = stage + r * kStagePitch + col8;
-#pragma unroll 1
-                for (int q = 0; q < 8; ++q) {
-                    if (n + q < N) {
-                        part[m * N + n + q] = src[q];
-                    }
-                }
-            }
-        } else if constexpr (FORM == EPI_FORM_I32) {
+        if constexpr (FORM == EPI_FORM_I32) {
 #pragma unroll 1
             for (int r = lane >> 2; r < TM; r += 16) {
                 const int64_t m = m0 + wm * TM + r;
@@ -368,55 +427,21 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
     });
 }
 
-// Split-K reduction: y[m, n] = epilogue(sum over splits z = 0, 1, ... of partial[z][m][n]), four consecutive
-// columns of one row per thread; the sum runs in split order, so the result does not depend on timing.
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *partial, int splits, int64_t M, int64_t N,
-                                                            EpiParams ep)
-{
-    const int64_t n4 = (N + 3) / 4;
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (idx >= M * n4) {
-        return;
-    }
-    const int64_t m = idx / n4;
-    const int64_t n = (idx - m * n4) * 4;
-    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (N % 4 == 0) {  // 16-byte aligned rows (the workspace base is 256-byte aligned)
-        for (int z = 0; z < splits; ++z) {
-            const float4 t = *reinterpret_cast<const float4 *>(partial + (static_cast<int64_t>(z) * M + m) * N + n);
-            v[0] += t.x;
-            v[1] += t.y;
-            v[2] += t.z;
-            v[3] += t.w;
-        }
-    } else {
-        for (int z = 0; z < splits; ++z) {
-            const float *src = partial + (static_cast<int64_t>(z) * M + m) * N + n;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                if (n + q < N) {
-                    v[q] += src[q];
-                }
-            }
-        }
-    }
-    const EpiBatch ob = epi_batch_offsets(ep, 0);
-    epi_apply4(ep, ob, m, n, N, v);
-}
-
 // Split-K factor of a launch: the tiles cover less than half of the 256 CUs and each split keeps at least 4 k-tiles.
+// A split launch therefore has fewer than kSplitMaxTiles tiles, one arrival counter each.
 int splitk_splits(const GemmOperands &op, int64_t batches, int BM, int BN, int kBK)
 {
     const int64_t tiles = ((op.M + BM - 1) / BM) * ((op.N + BN - 1) / BN) * batches;
     const int64_t KT = op.K / kBK;
-    if (batches != 1 || tiles >= 128 || KT < 8) {
+    if (batches != 1 || tiles >= KUDNN_SPLIT_MAX_TILES || KT < 8) {
         return 1;
     }
     return static_cast<int>(std::min<int64_t>(KT / 4, (384 + tiles - 1) / tiles));
 }
 
 template <int CT, int BM, int BN, int WM, int WN, int ST>
-int launch_cfg(const GemmOperands &op, const EpiParams &ep, int64_t batches, int group, void *ws, hipStream_t stream)
+int launch_cfg(const GemmOperands &op, const EpiParams &ep, int64_t batches, int group, void *ws, uint32_t *counters,
+               hipStream_t stream)
 {
     constexpr int kBK = CT == KUDNN_DT_F32 ? 32 : (CT == KUDNN_DT_S8 ? 128 : 64);
     if (op.K % kBK != 0) {
@@ -432,19 +457,16 @@ int launch_cfg(const GemmOperands &op, const EpiParams &ep, int64_t batches, int
             return -1;
         }
         hipLaunchKernelGGL((gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, 0, EPI_FORM_I32>), grid, block, 0, stream, op, ep,
-                           tilesM, tilesN, group, static_cast<float *>(nullptr));
+                           tilesM, tilesN, group, SplitArgs{});
         return hipGetLastError() == hipSuccess ? 0 : -1;
     } else {
-        const int splits = ws != nullptr ? splitk_splits(op, batches, BM, BN, kBK) : 1;
+        // split-K: grid.z splits, slots in the workspace, one arrival counter per tile
+        const int splits = ws != nullptr && counters != nullptr ? splitk_splits(op, batches, BM, BN, kBK) : 1;
+        SplitArgs sa{};
         if (splits > 1) {
-            float *partial = static_cast<float *>(ws);
-            dim3 sgrid(static_cast<unsigned>(tilesM * tilesN), 1, static_cast<unsigned>(splits));
-            hipLaunchKernelGGL((gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, 0, EPI_FORM_PARTIAL>), sgrid, block, 0, stream, op,
-                               ep, tilesM, tilesN, group, partial);
-            const int64_t threads = op.M * ((op.N + 3) / 4);
-            hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
-                               stream, partial, splits, op.M, op.N, ep);
-            return hipGetLastError() == hipSuccess ? 0 : -1;
+            grid.z = static_cast<unsigned>(splits);
+            sa.part = static_cast<float *>(ws);
+            sa.cnt = counters;
         }
 
         // the activation and the epilogue's tensor types select one of the compiled variants
@@ -464,7 +486,7 @@ int launch_cfg(const GemmOperands &op, const EpiParams &ep, int64_t batches, int
         if (kernel == nullptr) {
             kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, 0, EPI_FORM_GENERIC>;  // reads the activation at run time
         }
-        hipLaunchKernelGGL(kernel, grid, block, 0, stream, op, ep, tilesM, tilesN, group, static_cast<float *>(nullptr));
+        hipLaunchKernelGGL(kernel, grid, block, 0, stream, op, ep, tilesM, tilesN, group, sa);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
 }
@@ -486,18 +508,20 @@ size_t kudnn_gemm_workspace_bytes(const GemmOperands &op, int64_t batches, int c
         default: return 0;
     }
     const int splits = splitk_splits(op, batches, bm, bn, bk);
-    return splits > 1 ? static_cast<size_t>(splits) * op.M * op.N * sizeof(float) : 0;
+    const int64_t tiles = ((op.M + bm - 1) / bm) * ((op.N + bn - 1) / bn);
+    return splits > 1 ? static_cast<size_t>(tiles) * splits * bm * bn * sizeof(float) : 0;
 }
 
 namespace {
 
 template <int CT>
-int launch_lowp(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, void *ws, hipStream_t stream)
+int launch_lowp(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, void *ws, uint32_t *counters,
+                hipStream_t stream)
 {
     switch (cfg) {
-        case KUDNN_CFG_BF16_256x256: return launch_cfg<CT, 256, 256, 2, 2, 2>(op, ep, batches, 8, ws, stream);
-        case KUDNN_CFG_BF16_256x128: return launch_cfg<CT, 256, 128, 2, 2, 3>(op, ep, batches, 8, ws, stream);
-        case KUDNN_CFG_BF16_128x128: return launch_cfg<CT, 128, 128, 2, 2, 4>(op, ep, batches, 8, ws, stream);
+        case KUDNN_CFG_BF16_256x256: return launch_cfg<CT, 256, 256, 2, 2, 2>(op, ep, batches, 8, ws, counters, stream);
+        case KUDNN_CFG_BF16_256x128: return launch_cfg<CT, 256, 128, 2, 2, 3>(op, ep, batches, 8, ws, counters, stream);
+        case KUDNN_CFG_BF16_128x128: return launch_cfg<CT, 128, 128, 2, 2, 4>(op, ep, batches, 8, ws, counters, stream);
         default: return -1;
     }
 }
@@ -505,24 +529,25 @@ int launch_lowp(const GemmOperands &op, const EpiParams &ep, int64_t batches, in
 }  // namespace
 
 int kudnn_launch_gemm_mfma(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, int ct, void *ws,
-                           hipStream_t stream)
+                           uint32_t *counters, hipStream_t stream)
 {
     switch (ct) {
-        case KUDNN_DT_BF16: return launch_lowp<KUDNN_DT_BF16>(op, ep, batches, cfg, ws, stream);
-        case KUDNN_DT_F16: return launch_lowp<KUDNN_DT_F16>(op, ep, batches, cfg, ws, stream);
-        case KUDNN_DT_S8: return launch_lowp<KUDNN_DT_S8>(op, ep, batches, cfg, nullptr, stream);
+        case KUDNN_DT_BF16: return launch_lowp<KUDNN_DT_BF16>(op, ep, batches, cfg, ws, counters, stream);
+        case KUDNN_DT_F16: return launch_lowp<KUDNN_DT_F16>(op, ep, batches, cfg, ws, counters, stream);
+        case KUDNN_DT_S8: return launch_lowp<KUDNN_DT_S8>(op, ep, batches, cfg, nullptr, nullptr, stream);
         default: return -1;
     }
 }
 
 int kudnn_launch_gemm_f32(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, void *ws,
-                          hipStream_t stream)
+                          uint32_t *counters, hipStream_t stream)
 {
     switch (cfg) {
         // 128 x 128 serves grids of >= 256 tiles: two stages keep two workgroups per CU, which hides latency better
         // than a deeper ring at one workgroup per CU
-        case KUDNN_CFG_F32_128x128: return launch_cfg<KUDNN_DT_F32, 128, 128, 2, 2, 2>(op, ep, batches, 8, ws, stream);
-        case KUDNN_CFG_F32_64x64: return launch_cfg<KUDNN_DT_F32, 64, 64, 2, 2, 4>(op, ep, batches, 8, ws, stream);
+        case KUDNN_CFG_F32_128x128:
+            return launch_cfg<KUDNN_DT_F32, 128, 128, 2, 2, 2>(op, ep, batches, 8, ws, counters, stream);
+        case KUDNN_CFG_F32_64x64: return launch_cfg<KUDNN_DT_F32, 64, 64, 2, 2, 4>(op, ep, batches, 8, ws, counters, stream);
         default: return -1;
     }
 }

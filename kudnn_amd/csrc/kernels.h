@@ -21,12 +21,14 @@ enum {
 // Returns 0 on success, -1 if the launch failed or cfg is unknown. `ct` is the operand (compute) type of the 16- and
 // 8-bit kernels: KUDNN_DT_BF16, KUDNN_DT_F16 (f32 accumulation) or KUDNN_DT_S8 (int32 accumulation, integer
 // epilogue only). Their tile configurations keep the bf16 names; an s8 k-tile is 128 elements instead of 64.
-// 4-wave MFMA kernels (gemm_mfma.hip). A grid too small for the chip is split along K when `ws` (device memory of at
-// least kudnn_gemm_workspace_bytes bytes, 256-byte aligned) is given; with ws == nullptr it runs unsplit. s8 launches
-// are never split.
+// 4-wave MFMA kernels (gemm_mfma.hip). A grid too small for the chip is split along K, in the same launch, when `ws`
+// (device memory of at least kudnn_gemm_workspace_bytes bytes, 256-byte aligned) and `counters` (at least
+// KUDNN_SPLIT_MAX_TILES uint32, zero; a split launch leaves them zero) are given; with nullptr it runs unsplit. s8
+// launches are never split.
+constexpr int KUDNN_SPLIT_MAX_TILES = 128;
 size_t kudnn_gemm_workspace_bytes(const GemmOperands &op, int64_t batches, int cfg, int ct);
 int kudnn_launch_gemm_mfma(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, int ct, void *ws,
-                           hipStream_t stream);
+                           uint32_t *counters, hipStream_t stream);
 // 8-wave ping-pong schedule, 256x256 tile (gemm_pingpong.hip). Needs K a whole number of 128-byte k-tiles, 16-byte
 // aligned rows and 32-bit operand offsets; kudnn_pingpong_eligible says whether `op` qualifies.
 bool kudnn_pingpong_eligible(const GemmOperands &op, int ct);
@@ -39,7 +41,7 @@ void kudnn_pingpong_split(const GemmOperands &op, int64_t batches, int ct, int *
 int kudnn_launch_gemm_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, int ct, void *ws,
                                hipStream_t stream);
 int kudnn_launch_gemm_f32(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, void *ws,
-                          hipStream_t stream);
+                          uint32_t *counters, hipStream_t stream);
 // M <= 16, bf16 or f16 operands (`ct`), B contiguous along K (M == 1: row-per-wave GEMV, otherwise 16-row MFMA tiles).
 int kudnn_launch_skinny(const GemmOperands &op, const EpiParams &ep, int64_t batches, int ct, hipStream_t stream);
 
