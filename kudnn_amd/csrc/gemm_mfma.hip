@@ -105,8 +105,14 @@ struct SplitArgs {
     uint32_t *cnt;
 };
 
-// CT: compute (operand) type, KUDNN_DT_F32 / BF16 / F16 / S8.
-template <int CT, int BM, int BN, int WM, int WN, int ST, int ACT, int FORM>
+// The configurations a launch may split along K: the ones the dispatcher gives small grids. The split code is a
+// separate instance of the kernel (SPLIT), so it adds no register pressure to the kernels of large grids.
+template <int CT, int BM, int BN>
+constexpr bool kSplittable = (CT == KUDNN_DT_F32 && BM == 64 && BN == 64) ||
+                             ((CT == KUDNN_DT_BF16 || CT == KUDNN_DT_F16) && BM == 128 && BN == 128);
+
+// CT: compute (operand) type, KUDNN_DT_F32 / BF16 / F16 / S8. SPLIT: grid.z splits K (see SplitArgs).
+template <int CT, int BM, int BN, int WM, int WN, int ST, int ACT, int FORM, bool SPLIT = false>
 __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands op, EpiParams ep, int tilesM,
                                                                   int tilesN, int group, SplitArgs sa)
 {
@@ -281,8 +287,8 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
     // Split-K: this split's accumulators go to its slot with agent-scope atomic stores (coherent across the XCDs' L2
     // caches access by access; a device-scope fence would write back and invalidate a whole L2), every wave waits for
     // its stores, and one ticket per split is drawn. The holder of the last ticket rebuilds the sum in split order.
-    if constexpr (CT != KUDNN_DT_S8) {
-        if (gridDim.z > 1) {
+    if constexpr (SPLIT) {
+        {
             constexpr int QPW = FN * FM * 4;  // 16-byte quads of accumulators per lane
             constexpr int64_t kSlot = static_cast<int64_t>(BM) * BN / 2;  // uint64 per slot
             uint64_t *tileSlots = reinterpret_cast<uint64_t *>(sa.part) + static_cast<int64_t>(blockIdx.x) * gridDim.z * kSlot;
@@ -319,24 +325,49 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
             if (ticket[0] != gridDim.z - 1) {
                 return;  // another split finishes this tile
             }
-            for (int z = 0; z < static_cast<int>(gridDim.z); ++z) {
-                uint64_t *part = tileSlots + static_cast<int64_t>(z) * kSlot;
+            // CH slots are loaded together (as many as the registers allow), then added in split order
+            constexpr int NACC = FN * FM * 16;
+            constexpr int CH = NACC <= 16 ? 4 : (NACC <= 64 ? 2 : 1);
+            const int splits = static_cast<int>(gridDim.z);
+            for (int z0 = 0; z0 < splits; z0 += CH) {
+                uint64_t buf[CH][FN][FM][4][2];
 #pragma unroll
-                for (int j = 0; j < FN; ++j) {
+                for (int c = 0; c < CH; ++c) {
+                    if (z0 + c < splits) {
+                        uint64_t *part = tileSlots + static_cast<int64_t>(z0 + c) * kSlot;
 #pragma unroll
-                    for (int i = 0; i < FM; ++i) {
+                        for (int j = 0; j < FN; ++j) {
 #pragma unroll
-                        for (int g = 0; g < 4; ++g) {
-                            uint64_t *src = at(part, (j * FM + i) * 4 + g);
-                            const uint64_t lo = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                            const uint64_t hi = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                            const float o[4] = {__builtin_bit_cast(float, static_cast<uint32_t>(lo)),
-                                                __builtin_bit_cast(float, static_cast<uint32_t>(lo >> 32)),
-                                                __builtin_bit_cast(float, static_cast<uint32_t>(hi)),
-                                                __builtin_bit_cast(float, static_cast<uint32_t>(hi >> 32))};
+                            for (int i = 0; i < FM; ++i) {
 #pragma unroll
-                            for (int e = 0; e < 4; ++e) {
-                                acc[j][i][4 * g + e] = z == 0 ? o[e] : acc[j][i][4 * g + e] + o[e];
+                                for (int g = 0; g < 4; ++g) {
+                                    uint64_t *src = at(part, (j * FM + i) * 4 + g);
+                                    buf[c][j][i][g][0] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                    buf[c][j][i][g][1] = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                }
+                            }
+                        }
+                    }
+                }
+#pragma unroll
+                for (int c = 0; c < CH; ++c) {
+                    if (z0 + c < splits) {
+#pragma unroll
+                        for (int j = 0; j < FN; ++j) {
+#pragma unroll
+                            for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                                for (int g = 0; g < 4; ++g) {
+                                    const uint64_t lo = buf[c][j][i][g][0], hi = buf[c][j][i][g][1];
+                                    const float o[4] = {__builtin_bit_cast(float, static_cast<uint32_t>(lo)),
+                                                        __builtin_bit_cast(float, static_cast<uint32_t>(lo >> 32)),
+                                                        __builtin_bit_cast(float, static_cast<uint32_t>(hi)),
+                                                        __builtin_bit_cast(float, static_cast<uint32_t>(hi >> 32))};
+#pragma unroll
+                                    for (int e = 0; e < 4; ++e) {
+                                        acc[j][i][4 * g + e] = z0 + c == 0 ? o[e] : acc[j][i][4 * g + e] + o[e];
+                                    }
+                                }
                             }
                         }
                     }
@@ -439,6 +470,37 @@ int splitk_splits(const GemmOperands &op, int64_t batches, int BM, int BN, int k
     return static_cast<int>(std::min<int64_t>(KT / 4, (384 + tiles - 1) / tiles));
 }
 
+// Launches the variant of the kernel that the epilogue's activation and tensor types select.
+template <int CT, int BM, int BN, int WM, int WN, int ST, bool SPLIT>
+int launch_kernel(const GemmOperands &op, const EpiParams &ep, dim3 grid, int group, int tilesM, int tilesN,
+                  const SplitArgs &sa, hipStream_t stream)
+{
+    decltype(&gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, 0, EPI_FORM_GENERIC, SPLIT>) kernel = nullptr;
+    // the fixed form compiled for this compute type
+    constexpr int kForm = CT == KUDNN_DT_F32 ? EPI_FORM_F32 : (CT == KUDNN_DT_F16 ? EPI_FORM_F16 : EPI_FORM_BF16);
+    if (epi_form(ep) == kForm) {
+        switch (ep.act) {
+            case KUDNN_ACT_UNIMPLEMENTED:
+                kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_UNIMPLEMENTED, kForm, SPLIT>;
+                break;
+            case KUDNN_ACT_RELU: kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_RELU, kForm, SPLIT>; break;
+            case KUDNN_ACT_SWISH: kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_SWISH, kForm, SPLIT>; break;
+            case KUDNN_ACT_GELU_TANH:
+                kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_GELU_TANH, kForm, SPLIT>;
+                break;
+            case KUDNN_ACT_GELU_ERF:
+                kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_GELU_ERF, kForm, SPLIT>;
+                break;
+            default: break;
+        }
+    }
+    if (kernel == nullptr) {
+        kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, 0, EPI_FORM_GENERIC, SPLIT>;  // activation read at run time
+    }
+    hipLaunchKernelGGL(kernel, grid, dim3(WM * WN * 64), 0, stream, op, ep, tilesM, tilesN, group, sa);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 template <int CT, int BM, int BN, int WM, int WN, int ST>
 int launch_cfg(const GemmOperands &op, const EpiParams &ep, int64_t batches, int group, void *ws, uint32_t *counters,
                hipStream_t stream)
@@ -461,33 +523,20 @@ int launch_cfg(const GemmOperands &op, const EpiParams &ep, int64_t batches, int
         return hipGetLastError() == hipSuccess ? 0 : -1;
     } else {
         // split-K: grid.z splits, slots in the workspace, one arrival counter per tile
-        const int splits = ws != nullptr && counters != nullptr ? splitk_splits(op, batches, BM, BN, kBK) : 1;
+        const int splits = kSplittable<CT, BM, BN> && ws != nullptr && counters != nullptr
+                               ? splitk_splits(op, batches, BM, BN, kBK) : 1;
         SplitArgs sa{};
         if (splits > 1) {
             grid.z = static_cast<unsigned>(splits);
             sa.part = static_cast<float *>(ws);
             sa.cnt = counters;
         }
-
-        // the activation and the epilogue's tensor types select one of the compiled variants
-        decltype(&gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, 0, EPI_FORM_GENERIC>) kernel = nullptr;
-        // the fixed form compiled for this compute type
-        constexpr int kForm = CT == KUDNN_DT_F32 ? EPI_FORM_F32 : (CT == KUDNN_DT_F16 ? EPI_FORM_F16 : EPI_FORM_BF16);
-        if (epi_form(ep) == kForm) {
-            switch (ep.act) {
-                case KUDNN_ACT_UNIMPLEMENTED: kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_UNIMPLEMENTED, kForm>; break;
-                case KUDNN_ACT_RELU: kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_RELU, kForm>; break;
-                case KUDNN_ACT_SWISH: kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_SWISH, kForm>; break;
-                case KUDNN_ACT_GELU_TANH: kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_GELU_TANH, kForm>; break;
-                case KUDNN_ACT_GELU_ERF: kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_GELU_ERF, kForm>; break;
-                default: break;
+        if constexpr (kSplittable<CT, BM, BN>) {
+            if (splits > 1) {
+                return launch_kernel<CT, BM, BN, WM, WN, ST, true>(op, ep, grid, group, tilesM, tilesN, sa, stream);
             }
         }
-        if (kernel == nullptr) {
-            kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, 0, EPI_FORM_GENERIC>;  // reads the activation at run time
-        }
-        hipLaunchKernelGGL(kernel, grid, block, 0, stream, op, ep, tilesM, tilesN, group, sa);
-        return hipGetLastError() == hipSuccess ? 0 : -1;
+        return launch_kernel<CT, BM, BN, WM, WN, ST, false>(op, ep, grid, group, tilesM, tilesN, sa, stream);
     }
 }
 
@@ -499,13 +548,13 @@ size_t kudnn_gemm_workspace_bytes(const GemmOperands &op, int64_t batches, int c
         return 0;  // integer launches are never split
     }
     int bm = 0, bn = 0, bk = 0;
-    switch (cfg) {
-        case KUDNN_CFG_BF16_256x256: bm = 256; bn = 256; bk = 64; break;
-        case KUDNN_CFG_BF16_256x128: bm = 256; bn = 128; bk = 64; break;
+    switch (cfg) {  // the configurations that may split (kSplittable)
         case KUDNN_CFG_BF16_128x128: bm = 128; bn = 128; bk = 64; break;
-        case KUDNN_CFG_F32_128x128: bm = 128; bn = 128; bk = 32; break;
         case KUDNN_CFG_F32_64x64: bm = 64; bn = 64; bk = 32; break;
         default: return 0;
+    }
+    if ((ct == KUDNN_DT_F32) != (cfg == KUDNN_CFG_F32_64x64)) {
+        return 0;
     }
     const int splits = splitk_splits(op, batches, bm, bn, bk);
     const int64_t tiles = ((op.M + bm - 1) / bm) * ((op.N + bn - 1) / bn);
