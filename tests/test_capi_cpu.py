@@ -149,6 +149,23 @@ def test_dispatcher_choices():
     assert "packA" in plan_of(300, 200, 260).describe()
 
 
+@pytest.mark.parametrize("M,Kd,N,cfg", [
+    (512, 4096, 11008, "pingpong"),   # 2 x 43 = 86 tiles of 256 x 256: from 80 on, the ping-pong kernel
+    (3072, 14336, 4096, "pingpong"),  # 192 tiles: a partial round still goes to the ping-pong kernel
+    (1024, 4096, 4096, "128x128"),    # 64 tiles, 64 k-tiles: too short for the K-split
+    (1024, 11008, 4096, "pingpong"),  # 64 tiles, 172 k-tiles (43 per CU): the K-split
+    (512, 14336, 4096, "pingpong"),   # 32 tiles, 224 k-tiles (28 per CU): the K-split
+    (512, 11008, 4096, "128x128"),    # 32 tiles, 172 k-tiles: 21.5 per CU, below the 24 the K-split needs
+    (256, 8192, 8192, "128x128"),     # 32 tiles, 128 k-tiles: 16 per CU
+    (2048, 2048, 2048, "128x128"),    # 64 tiles, 32 k-tiles
+])
+def test_dispatch_rule(M, Kd, N, cfg):
+    # the planner's measured rule (bench.py --only dispatch): ping-pong from 80 tiles of 256 x 256, or with long K on
+    # at most half the CUs (the K-split itself is decided at launch, on the device's CU count); else 4-wave 128 x 128
+    assert plan_of(M, Kd, N).describe().startswith(f"mfma_bf16_{cfg}"), plan_of(M, Kd, N).describe()
+    assert plan_of(M, Kd, N, K.F16).describe().startswith(f"mfma_f16_{cfg}")
+
+
 def test_run_rejects_null_pointers_without_gpu():
     p = plan_of(64, 64, 64)
     with pytest.raises(K.KudnnError) as e:
