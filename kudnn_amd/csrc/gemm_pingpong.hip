@@ -38,6 +38,7 @@
 // code (an epilogue that dispatched every option at run time at each of its 16 call sites made the kernel 2.2 MB and
 // spent most of its time in instruction-cache misses). Tiles that cross the matrix edge take a rolled per-element loop.
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 #include <utility>
 
@@ -617,6 +618,26 @@ struct SkPlan {
 
 size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
+// CUs of the current device, queried once per device (0 when there is none).
+int cu_count()
+{
+    static std::atomic<int> cache[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    int cus = cache[dev].load(std::memory_order_relaxed);
+    if (cus == 0) {
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+            (void)hipGetLastError();
+            return 0;
+        }
+        cache[dev].store(cus, std::memory_order_relaxed);
+    }
+    return cus;
+}
+
 // The tail split pays only for grids of at most half the CUs with long K (at least 128 k-tiles, 24 or more per
 // workgroup), measured on MI355X. Behind whole rounds of tiles it loses: the tail's workgroups start at k offsets
 // spread over the whole K range, so they no longer read the same A and B panels at the same time as their XCD's
@@ -634,10 +655,8 @@ SkPlan sk_plan(const GemmOperands &op, int64_t batches, int ct)
     if (force == 0) {
         return s;
     }
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
-        (void)hipGetLastError();
+    const int cus = cu_count();
+    if (cus <= 0) {
         return s;
     }
     const int64_t tiles = ((op.M + kBM - 1) / kBM) * ((op.N + kBN - 1) / kBN);
