@@ -1,7 +1,7 @@
 """Python (ctypes) binding of the MI355X KuDNN Linear/GEMM C ABI (``include/kudnn_hip.h``).
 
 The product is the pair of native libraries under ``kudnn_amd/lib``; this module only binds the C ABI
-the way a ctypes caller would (the same stub INTEGRATION.md shows), for the tests and the benchmark.
+the way a ctypes caller would, for the tests and the benchmark.
 Pointers passed to ``run`` may be device pointers (torch CUDA/HIP tensors, the fast path) or host
 pointers (staged by the library). There is no fallback: if ``libkudnn_hip.so`` is missing, ``lib()``
 raises.

@@ -19,7 +19,7 @@
  *                      linearRes's size, f32 math, RNE back to bf16
  *   oracle_binary      the element-wise stage of the post-op chain (ADD/EXT as AddOps; MUL element-wise)
  *
- * Deliberate restatement choices (each also stated in DESIGN.md):
+ * Deliberate restatement choices:
  *   - GEMM sums are accumulated in double and rounded once to f32 (KML's f32 summation order is closed
  *     and not restatable); fp32 parity is then judged against this correctly-rounded value.
  *   - cblas_bgemm (bf16 C without bias) has KML-internal rounding; it is restated as RNE of the f32 value.
