@@ -400,18 +400,22 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
     //  - bf16 x bf16: bf16 MFMA (cblas_sbgemm / cblas_bgemm);
     //  - f16 x f16, f16 x s8, f16 x u8: f16 MFMA (cblas_hgemm / cblas_shgemm; an 8-bit weight is converted to f16
     //    exactly, as the reference's MatrixConverter does before hgemm, :341-372);
-    //  - s8 x s8 -> s32 (bias s32 or none): int8 MFMA into exact int32 (cblas_gemm_s8s8s32, :243-264);
+    //  - s8 / u8 x s8 / u8 -> s32 (bias s32 or none): int8 MFMA into exact int32 (cblas_gemm_s8s8s32, s8u8s32, u8s8s32,
+    //    u8u8s32 with zero operand offsets, :243-324); a u8 operand is packed shifted by -128 and the epilogue adds
+    //    back the shifted-out terms;
     //  - integer operands with a floating output: the all-f32 fallback (the operands are converted exactly);
-    //  - the u8 and mixed-sign integer GEMMs into s32, and a floating GEMM into an integer output, have no restatable
-    //    semantics here (closed KML routines, or ConvertFp32ToS32 of a rounded f32 sum) and are refused;
+    //  - a floating GEMM into an integer output (ConvertFp32ToS32 / ToS8 / ToU8 of a rounded f32 sum) and integer
+    //    GEMMs into s8 / u8 are refused;
     //  - everything else computes in f32.
     const int biasDt = IsNone(bias) ? c.dtype : bias->dtype;
     const bool intOut = !IsFp(c.dtype) || !IsFp(biasDt);
     if (intOut) {
-        if (!(a.dtype == KUDNN_DT_S8 && b.dtype == KUDNN_DT_S8 && c.dtype == KUDNN_DT_S32 && biasDt == KUDNN_DT_S32)) {
+        const bool int8a = a.dtype == KUDNN_DT_S8 || a.dtype == KUDNN_DT_U8;
+        const bool int8b = b.dtype == KUDNN_DT_S8 || b.dtype == KUDNN_DT_U8;
+        if (!(int8a && int8b && c.dtype == KUDNN_DT_S32 && biasDt == KUDNN_DT_S32)) {
             return Fail(KUDNN_STATUS_UNSUPPORTED,
-                        std::string(op) + ": the only integer output implemented on the MI355X path is s8 x s8 -> s32 "
-                                          "(with an s32 bias or none)");
+                        std::string(op) + ": the integer outputs implemented on the MI355X path are s8 / u8 x s8 / u8 "
+                                          "-> s32 (with an s32 bias or none)");
         }
         core.computeDt = KUDNN_DT_S8;
     } else if (a.dtype == KUDNN_DT_BF16 && b.dtype == KUDNN_DT_BF16) {
@@ -508,6 +512,10 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
     };
     core.A.staticPack = needsPack(core.A);
     core.B.staticPack = needsPack(core.B);
+    if (core.computeDt == KUDNN_DT_S8 && (core.A.dt == KUDNN_DT_U8 || core.B.dt == KUDNN_DT_U8)) {
+        // the correction terms are row sums over the packed layout: both operands are packed
+        core.A.staticPack = core.B.staticPack = true;
+    }
     core.kp = (core.K + bk - 1) / bk * bk;
 
     // engine and tile configuration
@@ -778,6 +786,7 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
         p.dst = dst;
         p.dst_dt = core.computeDt;
         p.kp = core.kp;
+        p.shift = core.computeDt == KUDNN_DT_S8 && o.dt == KUDNN_DT_U8 ? 128 : 0;
         const bool bc = allBroadcast(o);
         p.dst_bstride = bc ? 0 : o.rows * core.kp;
         int64_t packBatches = bc ? 1 : batches;
@@ -811,10 +820,16 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
     const size_t wsK = pingpong ? align256(kudnn_pingpong_workspace_bytes(shape, batches, core.computeDt)) : 0;
     void *ws = nullptr;
     bool acquired = false;
+    // u8 operands of an integer GEMM: correction vectors (row sums of the other packed operand, scaled by 128)
+    const bool aU8 = core.computeDt == KUDNN_DT_S8 && core.A.dt == KUDNN_DT_U8;
+    const bool bU8 = core.computeDt == KUDNN_DT_S8 && core.B.dt == KUDNN_DT_U8;
+    const int64_t copiesA = allBroadcast(core.A) ? 1 : batches, copiesB = allBroadcast(core.B) ? 1 : batches;
+    const size_t wsCm = bU8 ? align256(static_cast<size_t>(copiesA * core.M) * sizeof(int32_t)) : 0;
+    const size_t wsCn = aU8 ? align256(static_cast<size_t>(copiesB * core.N) * sizeof(int32_t)) : 0;
     uint32_t *counters = nullptr;
-    if (wsA + wsB + wsS + wsK > 0) {
+    if (wsA + wsB + wsS + wsK + wsCm + wsCn > 0) {
         int arc = KUDNN_STATUS_SUCCESS;
-        ws = wsp.Acquire(wsA + wsB + wsS + wsK, stream, arc, wsS > 0 ? &counters : nullptr);
+        ws = wsp.Acquire(wsA + wsB + wsS + wsK + wsCm + wsCn, stream, arc, wsS > 0 ? &counters : nullptr);
         if (ws == nullptr) {
             return arc;
         }
@@ -838,6 +853,17 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
     if (rc != 0) {
         return HipFail(hipGetLastError(), "pack launch");
     }
+    int32_t *corrM = wsCm > 0 ? reinterpret_cast<int32_t *>(static_cast<char *>(ws) + wsA + wsB + wsS + wsK) : nullptr;
+    int32_t *corrN = wsCn > 0 ? reinterpret_cast<int32_t *>(static_cast<char *>(ws) + wsA + wsB + wsS + wsK + wsCm)
+                              : nullptr;
+    if (corrM != nullptr && kudnn_launch_rowsum_s8(static_cast<const int8_t *>(op.a), core.M, core.kp, copiesA,
+                                                   copiesA > 1 ? core.M * core.kp : 0, 128u, corrM, stream) != 0) {
+        return HipFail(hipGetLastError(), "row-sum launch");
+    }
+    if (corrN != nullptr && kudnn_launch_rowsum_s8(static_cast<const int8_t *>(op.b), core.N, core.kp, copiesB,
+                                                   copiesB > 1 ? core.N * core.kp : 0, 128u, corrN, stream) != 0) {
+        return HipFail(hipGetLastError(), "row-sum launch");
+    }
 
     EpiParams ep{};
     ep.alpha = alpha;
@@ -847,6 +873,12 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
     ep.act_beta = x.actBeta;
     ep.bin = x.bin;
     ep.gamma = gamma;
+    ep.corr_m = corrM;
+    ep.corr_n = corrN;
+    ep.corr_m_bs = copiesA > 1 ? core.M : 0;
+    ep.corr_n_bs = copiesB > 1 ? core.N : 0;
+    ep.corr_c = aU8 && bU8 ? static_cast<int32_t>(static_cast<uint32_t>(128u * 128u) * static_cast<uint32_t>(core.K))
+                           : 0;
     ep.c_dt = core.C.dt;
     ep.c = c;
     ep.c_sm = core.C.sm;

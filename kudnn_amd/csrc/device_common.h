@@ -232,6 +232,7 @@ __device__ __forceinline__ float act_round(int dt, int kind, float v)
 // Per-batch base offsets (in elements) of the epilogue tensors for a flattened batch index.
 struct EpiBatch {
     int64_t c, bias, src, y;
+    int64_t corr_m, corr_n;
 };
 
 __device__ __forceinline__ EpiBatch epi_batch_offsets(const EpiParams &e, int64_t b)
@@ -245,6 +246,8 @@ __device__ __forceinline__ EpiBatch epi_batch_offsets(const EpiParams &e, int64_
     o.bias = i0 * e.bias_bs[0] + i1 * e.bias_bs[1] + i2 * e.bias_bs[2];
     o.src = i0 * e.src_bs[0] + i1 * e.src_bs[1] + i2 * e.src_bs[2];
     o.y = i0 * e.y_bs[0] + i1 * e.y_bs[1] + i2 * e.y_bs[2];
+    o.corr_m = b * e.corr_m_bs;
+    o.corr_n = b * e.corr_n_bs;
     return o;
 }
 
@@ -834,7 +837,15 @@ __device__ __forceinline__ void epi_elem(const EpiParams &e, const EpiBatch &ob,
 // rejects anything else). The accumulators arrive as the bit patterns of the MFMA's int32 results.
 __device__ __forceinline__ uint32_t i32_bias(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n)
 {
-    return e.bias == nullptr ? 0u : static_cast<const uint32_t *>(e.bias)[ob.bias + m * e.bias_sm + n * e.bias_sn];
+    uint32_t v = e.bias == nullptr ? 0u : static_cast<const uint32_t *>(e.bias)[ob.bias + m * e.bias_sm + n * e.bias_sn];
+    // u8 operands: the terms of the -128 shift (all in wrapping 32-bit arithmetic, like the accumulators)
+    if (e.corr_m != nullptr) {
+        v += static_cast<uint32_t>(e.corr_m[ob.corr_m + m]);
+    }
+    if (e.corr_n != nullptr) {
+        v += static_cast<uint32_t>(e.corr_n[ob.corr_n + n]);
+    }
+    return v + static_cast<uint32_t>(e.corr_c);
 }
 
 // 8 consecutive columns (m, n .. n+7), all in bounds, y contiguous along n with 16-byte aligned groups (fast8; callers

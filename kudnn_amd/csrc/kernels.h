@@ -59,7 +59,12 @@ struct PackArgs {
     int dst_dt;
     int64_t kp;              // destination row pitch (elements), >= cols
     int64_t dst_bstride;     // destination batch stride (elements)
+    int shift;               // subtracted from every element (128: u8 -> s8 for the integer MFMA); padding stays 0
 };
 int kudnn_launch_pack(const PackArgs &p, int64_t batches, hipStream_t stream);
+// out[c * rows + r] = scale * (sum over the kp int8 of row r of copy c of a packed operand), in wrapping 32-bit
+// arithmetic: the correction terms of an integer GEMM whose other operand was a shifted u8.
+int kudnn_launch_rowsum_s8(const int8_t *p, int64_t rows, int64_t kp, int64_t copies, int64_t bstride, uint32_t scale,
+                           int32_t *out, hipStream_t stream);
 
 #endif  // KUDNN_KERNELS_H

@@ -32,6 +32,13 @@ struct EpiParams {
     int64_t c_sm, c_sn, bias_sm, bias_sn, src_sm, src_sn, y_sm, y_sn;
     int64_t bdim[3];      // batch dims (right-aligned), product = number of batches in grid.y
     int64_t c_bs[3], bias_bs[3], src_bs[3], y_bs[3];
+    // Integer GEMMs with a u8 operand run on the s8 MFMA with that operand shifted by -128; the terms the shift
+    // removes come back here: y += corr_m[b * corr_m_bs + m] + corr_n[b * corr_n_bs + n] + corr_c (int32, wrapping;
+    // b the linear batch index, a null vector adds nothing).
+    const int32_t *corr_m;
+    const int32_t *corr_n;
+    int64_t corr_m_bs, corr_n_bs;
+    int32_t corr_c;
 };
 
 // Operands of the MFMA / skinny kernels: A is [M][K] with row stride lda, B is [N][K] with row stride ldb,

@@ -468,10 +468,14 @@ int oracle_gemm(const ogemm *g)
     return 0;
 }
 
+/* The integer GEMMs into s32 of the registry (src/dnn/src/kudnn_gemm.cpp:243-324): cblas_gemm_s8s8s32, s8u8s32,
+ * u8s8s32 and u8u8s32, all called with zero operand offsets, so the result is the exact integer sum (plus the s32
+ * bias), wrapped to int32. alpha = 1 and beta = 0 only. */
 static int oracle_gemm_s8(const ogemm *g)
 {
     const int nd = g->a.ndims;
-    if (g->a.dtype != O_S8 || g->b.dtype != O_S8 || g->alpha != 1.0f || g->beta != 0.0f) {
+    const int ai = g->a.dtype == O_S8 || g->a.dtype == O_U8, bi = g->b.dtype == O_S8 || g->b.dtype == O_U8;
+    if (!ai || !bi || g->alpha != 1.0f || g->beta != 0.0f) {
         return -3;
     }
     const int64_t M = g->a.dims[nd - 2], K = g->a.dims[nd - 1], N = g->b.dims[nd - 1];
@@ -506,7 +510,8 @@ static int oracle_gemm_s8(const ogemm *g)
                     for (int64_t n = 0; n < N; ++n) {
                         int64_t acc = 0;
                         for (int64_t k = 0; k < K; ++k) {
-                            acc += ld_int(g->pa, O_S8, ao + m * a_sm + k * a_sk) * ld_int(g->pb, O_S8, bo + k * b_sk + n * b_sn);
+                            acc += ld_int(g->pa, g->a.dtype, ao + m * a_sm + k * a_sk) *
+                                   ld_int(g->pb, g->b.dtype, bo + k * b_sk + n * b_sn);
                         }
                         if (hasBias) {
                             acc += ld_int(g->pbias, O_S32, xo + m * x_sm + n * x_sn);

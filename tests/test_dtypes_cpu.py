@@ -14,18 +14,24 @@ def _s8(rng, shape):
     return rng.integers(-128, 128, size=shape).astype(np.int8)
 
 
+def _int8(rng, shape, dt):
+    return _s8(rng, shape) if dt == O.S8 else rng.integers(0, 256, size=shape).astype(np.uint8)
+
+
+@pytest.mark.parametrize("adt,bdt", [(O.S8, O.S8), (O.U8, O.S8), (O.S8, O.U8), (O.U8, O.U8)])
 @pytest.mark.parametrize("wlayout", ["BA", "AB"])
 @pytest.mark.parametrize("bias", [None, "1N", "M1", "MN"])
-def test_oracle_s8s8s32_matches_int64_matmul(wlayout, bias):
+def test_oracle_int8_gemm_matches_int64_matmul(adt, bdt, wlayout, bias):
+    # cblas_gemm_s8s8s32 / s8u8s32 / u8s8s32 / u8u8s32 with zero offsets: the exact integer sum, wrapped to int32
     rng = np.random.default_rng(7)
     M, Kd, N = 23, 301, 19
-    a = _s8(rng, (M, Kd))
-    w = _s8(rng, (Kd, N))  # logical [K][N]
-    A = O.Tensor((M, Kd), (Kd, 1), O.S8, a.reshape(-1).copy())
+    a = _int8(rng, (M, Kd), adt)
+    w = _int8(rng, (Kd, N), bdt)  # logical [K][N]
+    A = O.Tensor((M, Kd), (Kd, 1), adt, a.reshape(-1).copy())
     if wlayout == "BA":
-        B = O.Tensor((Kd, N), (1, Kd), O.S8, w.T.reshape(-1).copy())
+        B = O.Tensor((Kd, N), (1, Kd), bdt, w.T.reshape(-1).copy())
     else:
-        B = O.Tensor((Kd, N), (N, 1), O.S8, w.reshape(-1).copy())
+        B = O.Tensor((Kd, N), (N, 1), bdt, w.reshape(-1).copy())
     want = a.astype(np.int64) @ w.astype(np.int64)
     X = None
     if bias:
@@ -74,6 +80,9 @@ def _plan(adt, bdt, cdt, biasdt=None, M=64, Kd=128, N=96, blay="BA"):
     ((K.F16, K.U8, K.F16, K.F32), "mfma_f16"),
     ((K.S8, K.S8, K.S32, K.S32), "mfma_s8"),
     ((K.S8, K.S8, K.S32, None), "mfma_s8"),
+    ((K.U8, K.S8, K.S32, K.S32), "mfma_s8"),
+    ((K.S8, K.U8, K.S32, K.S32), "mfma_s8"),
+    ((K.U8, K.U8, K.S32, None), "mfma_s8"),
     ((K.F32, K.F32, K.F32, K.F32), "mfma_f32"),
     ((K.S8, K.S8, K.F32, K.F32), "mfma_f32"),
     ((K.BF16, K.F16, K.F32, None), "mfma_f32"),
@@ -84,17 +93,23 @@ def test_planner_compute_type(combo, expect):
 
 
 @pytest.mark.parametrize("combo", [
-    (K.U8, K.S8, K.S32, K.S32),
-    (K.S8, K.U8, K.S32, K.S32),
-    (K.U8, K.U8, K.S32, K.S32),
     (K.S8, K.S8, K.S8, None),
+    (K.U8, K.U8, K.U8, None),
     (K.F32, K.F32, K.S32, None),
     (K.S8, K.S8, K.S32, K.F32),
 ])
-def test_planner_refuses_unrestated_integer_combos(combo):
+def test_planner_refuses_integer_outputs_other_than_s32(combo):
     with pytest.raises(K.KudnnError) as e:
         _plan(*combo)
     assert e.value.status == K.UNSUPPORTED
+
+
+def test_u8_operands_are_packed_shifted():
+    # a u8 operand runs on the s8 MFMA shifted by -128: both operands are packed (the correction terms are row sums
+    # over the packed layout)
+    for combo in ((K.U8, K.S8, K.S32, K.S32), (K.S8, K.U8, K.S32, None), (K.U8, K.U8, K.S32, K.S32)):
+        d = _plan(*combo).describe()
+        assert "mfma_s8" in d and "packA" in d and "packB" in d, d
 
 
 def test_integer_gemm_only_through_gemm():

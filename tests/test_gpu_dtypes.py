@@ -103,6 +103,88 @@ def test_s8s8s32_extremes_exact():
 
 
 # ---------------------------------------------------------------------------------------------------
+# u8 operands (cblas_gemm_s8u8s32 / u8s8s32 / u8u8s32): s8 MFMA on the operand shifted by -128, plus the shifted-out
+# terms in the epilogue
+
+
+def _int8_case(dims, dt, seed, layout=None):
+    lo, hi = (-128, 127) if dt == O.S8 else (0, 255)
+    return Case(dims, dt, layout, seed=seed, lo=lo, hi=hi)
+
+
+def run_int8(M, N, Kd, adt, bdt, wlayout="BA", bias_dims=None, seed=0, expect="mfma_s8"):
+    x = _int8_case([M, Kd], adt, seed)
+    w = _int8_case([Kd, N], bdt, seed + 1, wlayout)
+    c = Case([M, N], O.S32, zero=True)
+    b = Case(bias_dims, O.S32, seed=seed + 2, lo=-(1 << 24), hi=1 << 24) if bias_dims else None
+    plan = K.Gemm(x.desc, w.desc, c.desc, b.desc if b else None)
+    assert expect in plan.describe(), plan.describe()
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc, b.device() if b else None)
+    torch.cuda.synchronize()
+    ref = c.clone_empty()
+    O.gemm(x.t, w.t, ref, b.t if b else None)
+    compare(from_device(dc, O.S32), ref.buf, O.S32, plan.describe())
+
+
+COMBOS = [(O.U8, O.S8), (O.S8, O.U8), (O.U8, O.U8)]
+
+
+@pytest.mark.parametrize("adt,bdt", COMBOS)
+@pytest.mark.parametrize("mnk", [(64, 64, 128), (300, 260, 256), (17, 33, 24), (1, 70, 300)])
+@pytest.mark.parametrize("wlayout", ["BA", "AB"])
+def test_u8_operand_gemms(adt, bdt, mnk, wlayout):
+    M, N, Kd = mnk
+    run_int8(M, N, Kd, adt, bdt, wlayout, bias_dims=[1, N], seed=300)
+
+
+@pytest.mark.parametrize("adt,bdt", COMBOS)
+@pytest.mark.parametrize("bias", [None, "M1", "MN"])
+def test_u8_operand_bias_kinds(adt, bdt, bias):
+    M, N, Kd = 96, 80, 256
+    dims = {"M1": [M, 1], "MN": [M, N]}.get(bias)
+    run_int8(M, N, Kd, adt, bdt, bias_dims=dims, seed=310)
+
+
+@pytest.mark.parametrize("adt,bdt", COMBOS)
+def test_u8_operand_pingpong(force_pingpong, adt, bdt):
+    run_int8(300, 520, 384, adt, bdt, bias_dims=[1, 520], seed=320, expect="mfma_s8_pingpong")
+
+
+@pytest.mark.parametrize("adt,bdt", COMBOS)
+def test_u8_operand_batched_broadcast_weight(adt, bdt):
+    # A batched (a correction vector per batch), W broadcast over the batch (one vector for all)
+    x = _int8_case([3, 40, 256], adt, 330)
+    w = _int8_case([1, 256, 72], bdt, 331)
+    c = Case([3, 40, 72], O.S32, zero=True)
+    plan = K.Gemm(x.desc, w.desc, c.desc)
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc)
+    torch.cuda.synchronize()
+    ref = c.clone_empty()
+    O.gemm(x.t, w.t, ref)
+    compare(from_device(dc, O.S32), ref.buf, O.S32, plan.describe())
+
+
+def test_u8u8_extremes_exact():
+    # every product 255 x 255 over K = 4096 (the constant term 128 * 128 * K and both row-sum terms at their largest)
+    M, N, Kd = 64, 64, 4096
+    x = Case([M, Kd], O.U8, zero=True)
+    w = Case([Kd, N], O.U8, "BA", zero=True)
+    x.t.buf[:] = 255
+    w.t.buf[:] = 255
+    w.t.buf[::5] = 0
+    c = Case([M, N], O.S32, zero=True)
+    plan = K.Gemm(x.desc, w.desc, c.desc)
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc)
+    torch.cuda.synchronize()
+    got = from_device(dc, O.S32).reshape(M, N)
+    want = (x.t.buf.astype(np.int64).reshape(M, Kd) @ w.t.buf.astype(np.int64).reshape(N, Kd).T).astype(np.int32)
+    assert np.array_equal(got, want)
+
+
+# ---------------------------------------------------------------------------------------------------
 # f16 x f16 and f16 x s8
 
 
