@@ -349,8 +349,10 @@ int launch_gemv(const GemmOperands &op, const EpiParams &ep, int64_t batches, hi
 // it back in the operand layout of v_mfma_f32_16x16x32_bf16, weight rows first, X (rows m < M, cache-resident) second.
 // Loads go through buffer resources and are issued by every lane: a lane with nothing to load (a chunk past K, an X
 // row m >= M) gets an offset past the resource's range, which reads zero, so no branch separates the loads of a block.
-// The KW partial 16 x 16 tiles are summed through LDS and wave 0 runs the epilogue on runs of 4 consecutive columns.
-template <int CT, int KW>
+// With PIPE, a wave issues the weight loads of its next block before the current block goes through LDS and the MFMAs,
+// into a second set of registers (the two sets alternate). The KW partial 16 x 16 tiles are summed through LDS and
+// wave 0 runs the epilogue on runs of 4 consecutive columns.
+template <int CT, int KW, bool PIPE>
 __global__ __launch_bounds__(KW * 64) void skinny_rows_kernel(GemmOperands op, EpiParams ep)
 {
     constexpr int kPitch = 33;  // chunks per LDS row
@@ -402,23 +404,30 @@ __global__ __launch_bounds__(KW * 64) void skinny_rows_kernel(GemmOperands op, E
     EpiPre4 pre{make_uint2(0u, 0u), make_uint2(0u, 0u), make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
     const bool epiLane = wave == 0 && r16 < M && nq < N;
 
-    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int b = wave; b < blocks; b += KW) {
+    // weight loads of block b (a block past the last one loads nothing: every lane gets the out-of-range offset)
+    auto load_w = [&](int b, u32x4_t (&wv)[8]) {
         const int c0 = b * 32;
-        const bool win = c0 + c32 < chunks;
-        u32x4_t wv[8], xv[8];
+        const bool win = b < blocks && c0 + c32 < chunks;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             wv[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, win ? wrow[i] + static_cast<uint32_t>(c0 + c32) * 16u : kOut, 0, 0);
         }
+    };
+    // one block: X's loads of block b, then the weight loads of the wave's next block into wn (so they stay in flight
+    // through this block's LDS pass and MFMAs: the waits for wv and xv leave the 8 younger loads outstanding), then wv
+    // through the LDS tile into the MFMAs
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto block = [&](int b, const u32x4_t (&wv)[8], u32x4_t (&wn)[8]) {
+        const int c0 = b * 32;
+        u32x4_t xv[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) {  // k-step k of the block: chunk c0 + 4k + q
             const int kc = c0 + 4 * k + q;
             const bool in = r16 < M && kc < chunks;
             xv[k] = __builtin_amdgcn_raw_buffer_load_b128(xrs, in ? xrow + static_cast<uint32_t>(kc) * 16u : kOut, 0, 0);
         }
-        if (b == 0 && epiLane) {
-            pre = epi_prefetch4(ep, ob, r16, nq, N);
+        if constexpr (PIPE) {
+            load_w(b + KW, wn);
         }
         // the previous block's tile reads have returned (their MFMAs consumed them); order the rewrite after them
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -433,6 +442,28 @@ __global__ __launch_bounds__(KW * 64) void skinny_rows_kernel(GemmOperands op, E
         for (int k = 0; k < 8; ++k) {
             const u32x4_t wf = tw[r16 * kPitch + 4 * k + q];
             acc = mfma16<CT>(wf, xv[k], acc);
+        }
+    };
+    u32x4_t w0[8], w1[8];
+    load_w(wave, w0);
+    if (epiLane) {
+        pre = epi_prefetch4(ep, ob, r16, nq, N);
+    }
+    if constexpr (PIPE) {
+        // two named buffers alternate, so no register copy waits on a load in flight
+        for (int b = wave; b < blocks; b += 2 * KW) {
+            block(b, w0, w1);
+            if (b + KW >= blocks) {
+                break;
+            }
+            block(b + KW, w1, w0);
+        }
+    } else {
+        for (int b = wave; b < blocks; b += KW) {
+            if (b != wave) {
+                load_w(b, w0);
+            }
+            block(b, w0, w1);
         }
     }
 
@@ -483,10 +514,15 @@ int launch_skinny(const GemmOperands &op, const EpiParams &ep, int64_t batches, 
         // fewer than 2 row groups per CU: split K over 16 waves (one workgroup per CU); otherwise 8 (two per CU)
         const int64_t groups = (op.N + 15) / 16 * batches;
         dim3 grid(static_cast<unsigned>((op.N + 15) / 16), static_cast<unsigned>(batches));
-        if (groups < 512) {
-            hipLaunchKernelGGL((skinny_rows_kernel<CT, 16>), grid, dim3(16 * 64), 0, stream, op, ep);
+        // measured at M = 4 and 16, N = 4096 and 14336, K = 4096: with more than 8 rows of X, 2-wave workgroups with
+        // the next block's weights in flight (145 VGPRs, 12 waves and 6 workgroups per CU, one round of workgroups)
+        // beat the 8- and 16-wave forms by 8-9 %; at M = 4 they lose 1-4 %, and with few row groups they leave CUs idle
+        if (op.M > 8 && groups >= 256) {
+            hipLaunchKernelGGL((skinny_rows_kernel<CT, 2, true>), grid, dim3(2 * 64), 0, stream, op, ep);
+        } else if (groups < 512) {
+            hipLaunchKernelGGL((skinny_rows_kernel<CT, 16, false>), grid, dim3(16 * 64), 0, stream, op, ep);
         } else {
-            hipLaunchKernelGGL((skinny_rows_kernel<CT, 8>), grid, dim3(8 * 64), 0, stream, op, ep);
+            hipLaunchKernelGGL((skinny_rows_kernel<CT, 8, false>), grid, dim3(8 * 64), 0, stream, op, ep);
         }
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
