@@ -215,6 +215,29 @@ def test_c4_skinny_mul(M, N):
     compare(from_device(dy, O.BF16), ref.buf, O.BF16, f"C4 M={M} N={N}")
 
 
+@pytest.mark.parametrize("M,N,Kd", [(9, 4112, 2100), (12, 4096, 2304), (16, 4104, 4096), (12, 1024, 2100)])
+def test_skinny_rows_forms(M, N, Kd):
+    # M > 8 with >= 256 row groups runs 2-wave workgroups with the next weight block in flight: an odd count of
+    # 256-element K blocks (K = 2100 packs to 9 blocks, 2304 is exactly 9) ends one wave on a block with no successor;
+    # N not a multiple of 16 leaves a ragged last row group. N = 1024 (64 row groups) stays on the 16-wave form.
+    # The chain is bias + ReLU + add: a 1-ULP difference of the bf16 GEMM result (f32 summation order) stays 1 ULP,
+    # where GELU's extra rounding could double it; a lost or repeated K block would move almost every element.
+    x = Case([M, Kd], O.BF16, seed=210, dist="normal", lo=0.0, hi=1.0)
+    w = Case([Kd, N], O.BF16, "BA", seed=211, dist="normal", lo=0.0, hi=0.03)
+    b = Case([1, N], O.BF16, seed=212, lo=-0.2, hi=0.2)
+    s = Case([M, N], O.BF16, seed=213, lo=-1.0, hi=1.0)
+    y = Case([M, N], O.BF16, zero=True)
+    plan = K.LinearPostOps(x.desc, w.desc, y.desc, b.desc, act=K.ACT_RELU, binary=K.BIN_ADD, src=s.desc)
+    assert plan.describe().startswith("skinny_bf16_16xK"), plan.describe()
+    dy = zeros_device(y)
+    plan.run(x.device(), w.device(), dy, b.device(), s.device())
+    torch.cuda.synchronize()
+    ref = y.clone_empty()
+    O.linear_postops(x.t, w.t, ref, b.t, O.ACT_RELU, 0.0, O.BIN_ADD, s.t)
+    _, exact = compare(from_device(dy, O.BF16), ref.buf, O.BF16, f"skinny M={M} N={N} K={Kd} {plan.describe()}")
+    assert exact > 0.99, f"only {exact:.4f} of the elements are bit-exact"
+
+
 @pytest.mark.parametrize("Kd", [40, 1001, 1024, 2048, 4096, 9000])
 @pytest.mark.parametrize("post", ["bias_gelu_add", "swish_f32", "gemm_beta"])
 def test_m1_row_gemv(Kd, post):
