@@ -238,6 +238,31 @@ def test_skinny_rows_forms(M, N, Kd):
     assert exact > 0.99, f"only {exact:.4f} of the elements are bit-exact"
 
 
+def _random_skinny_shapes(count=20, seed=2024):
+    # seeded (M, N, K) draws over the decode kernels: M in [2, 16] (both sides of M > 8), N in [16, 10000] (row-group
+    # counts either side of 256 and 512), K in [8, 3000] (K tails that pack, odd and even K-block counts)
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(2, 17)), int(rng.integers(16, 10001)), int(rng.integers(8, 3001))) for _ in range(count)]
+
+
+@pytest.mark.parametrize("M,N,Kd", _random_skinny_shapes())
+def test_skinny_random_shapes(M, N, Kd):
+    x = Case([M, Kd], O.BF16, seed=220, dist="normal", lo=0.0, hi=1.0)
+    w = Case([Kd, N], O.BF16, "BA", seed=221, dist="normal", lo=0.0, hi=0.03)
+    b = Case([1, N], O.BF16, seed=222, lo=-0.2, hi=0.2)
+    s = Case([M, N], O.BF16, seed=223, lo=-1.0, hi=1.0)
+    y = Case([M, N], O.BF16, zero=True)
+    plan = K.LinearPostOps(x.desc, w.desc, y.desc, b.desc, act=K.ACT_RELU, binary=K.BIN_ADD, src=s.desc)
+    assert plan.describe().startswith("skinny"), plan.describe()
+    dy = zeros_device(y)
+    plan.run(x.device(), w.device(), dy, b.device(), s.device())
+    torch.cuda.synchronize()
+    ref = y.clone_empty()
+    O.linear_postops(x.t, w.t, ref, b.t, O.ACT_RELU, 0.0, O.BIN_ADD, s.t)
+    _, exact = compare(from_device(dy, O.BF16), ref.buf, O.BF16, f"skinny M={M} N={N} K={Kd} {plan.describe()}")
+    assert exact > 0.99, f"only {exact:.4f} of the elements are bit-exact"
+
+
 @pytest.mark.parametrize("Kd", [40, 1001, 1024, 2048, 4096, 9000])
 @pytest.mark.parametrize("post", ["bias_gelu_add", "swish_f32", "gemm_beta"])
 def test_m1_row_gemv(Kd, post):
