@@ -197,6 +197,40 @@ def test_c3_bf16_gelu_residual_rows():
     print(f"C3 max-normalised error {maxnorm:.3e}, bit-exact fraction {exact:.5f}")
 
 
+def _random_gemm_cases(count=24, seed=4051):
+    # seeded draws over the prefill kernels: M in [17, 2500], N in [16, 8000], K in [8, 2000] (tile counts either side
+    # of the ping-pong threshold, ragged edges, K tails that pack); dtype and weight layout alternate
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(17, 2501)), int(rng.integers(16, 8001)), int(rng.integers(8, 2001)),
+             O.BF16 if i % 2 == 0 else O.F32, "BA" if i % 4 < 2 else "AB") for i in range(count)]
+
+
+@pytest.mark.parametrize("M,N,Kd,dt,wl", _random_gemm_cases())
+def test_gemm_random_shapes(M, N, Kd, dt, wl):
+    # bf16: bias + ReLU + residual add, where a 1-ULP difference of the GEMM result stays 1 ULP; f32: bias + SiLU
+    x = Case([M, Kd], dt, seed=230, dist="normal", lo=0.0, hi=1.0)
+    w = Case([Kd, N], dt, wl, seed=231, dist="normal", lo=0.0, hi=0.03)
+    b = Case([1, N], dt, seed=232, lo=-0.2, hi=0.2)
+    y = Case([M, N], dt, zero=True)
+    rows = sample_rows(M, 12)
+    dy = zeros_device(y)
+    ref = O.empty((len(rows), N), (N, 1), dt)
+    if dt == O.BF16:
+        s = Case([M, N], dt, seed=233, lo=-1.0, hi=1.0)
+        plan = K.LinearPostOps(x.desc, w.desc, y.desc, b.desc, act=K.ACT_RELU, binary=K.BIN_ADD, src=s.desc)
+        plan.run(x.device(), w.device(), dy, b.device(), s.device())
+        O.linear_postops(dense_rows(x.t, rows), w.t, ref, b.t, O.ACT_RELU, 0.0, O.BIN_ADD, dense_rows(s.t, rows))
+    else:
+        plan = K.LinearActivation(x.desc, w.desc, y.desc, b.desc, 1.0, 0.0, K.ACT_SWISH)
+        plan.run(x.device(), w.device(), dy, b.device())
+        O.linear_act(dense_rows(x.t, rows), w.t, ref, b.t, O.ACT_SWISH, 1.0)
+    torch.cuda.synchronize()
+    got = from_device(dy, dt).reshape(M, N)
+    _, exact = compare(got[rows].reshape(-1), ref.buf, dt, f"M={M} N={N} K={Kd} {wl} {plan.describe()}")
+    if dt == O.BF16:
+        assert exact > 0.99, f"only {exact:.4f} of the elements are bit-exact"
+
+
 @pytest.mark.parametrize("M", [1, 4, 16])
 @pytest.mark.parametrize("N", [4096, 14336])
 def test_c4_skinny_mul(M, N):
