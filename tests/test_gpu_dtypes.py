@@ -138,6 +138,21 @@ def test_u8_operand_gemms(adt, bdt, mnk, wlayout):
     run_int8(M, N, Kd, adt, bdt, wlayout, bias_dims=[1, N], seed=300)
 
 
+def _random_int8_cases(count=16, seed=77):
+    # seeded draws over all four operand-sign combinations: M in [1, 600], N in [1, 1200], K in [4, 1500] (ragged
+    # tiles, K tails that pack), weight layout and a [1, N] bias alternating
+    rng = np.random.default_rng(seed)
+    combos = [(O.S8, O.S8)] + COMBOS
+    return [(int(rng.integers(1, 601)), int(rng.integers(1, 1201)), int(rng.integers(4, 1501)), *combos[i % 4],
+             "BA" if i % 8 < 4 else "AB", i % 2 == 0) for i in range(count)]
+
+
+@pytest.mark.parametrize("M,N,Kd,adt,bdt,wl,bias", _random_int8_cases())
+def test_int8_random_shapes(M, N, Kd, adt, bdt, wl, bias):
+    # bit-exact against the oracle's int64 sum wrapped to int32
+    run_int8(M, N, Kd, adt, bdt, wl, bias_dims=[1, N] if bias else None, seed=340)
+
+
 @pytest.mark.parametrize("adt,bdt", COMBOS)
 @pytest.mark.parametrize("bias", [None, "M1", "MN"])
 def test_u8_operand_bias_kinds(adt, bdt, bias):
