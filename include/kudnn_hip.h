@@ -17,8 +17,11 @@
  *  - Pointers passed to *_run may be device memory (hipMalloc, the fast path) or ordinary host memory;
  *    host pointers are staged through device buffers and the call then returns synchronously.
  *  - *_run is asynchronous on `stream` (a hipStream_t; NULL = the default stream) when every pointer is
- *    device memory. A plan (handle) holds no mutable state after *_create, so one plan may be run
- *    concurrently on several streams.
+ *    device memory. The kernel plan is fixed by *_create; the one mutable part of a handle is its device
+ *    workspace (packed operands, split-K partials), which grows with hipMalloc on the first runs that need it
+ *    and is then reused. Runs of one handle on several streams are correct: a run on another stream than the
+ *    previous one waits (on the GPU) for that run, so they are serialised on the workspace. A cloned handle has
+ *    a workspace of its own.
  */
 #ifndef KUDNN_HIP_H
 #define KUDNN_HIP_H
@@ -174,7 +177,9 @@ KUDNN_HIP_API int kudnn_linear_act_validate(const kudnn_tensor_desc *a, const ku
                                             const kudnn_tensor_desc *c, const kudnn_tensor_desc *bias, float alpha,
                                             float beta, int kind, int num_threads);
 /* Replaces the LinearActivationLayerFWD constructor (kudnn_linear_activationlayer.hpp:43-51,
- * kudnn_linear_activationlayer.cpp:30-38). `alpha` is the activation parameter (RELU slope, SWISH alpha). */
+ * kudnn_linear_activationlayer.cpp:30-38). `alpha` is the activation parameter (RELU slope, SWISH alpha). As in the
+ * reference, `beta` is only validated: the activation is built with (kind, alpha) (:33) and runs with its second
+ * parameter 0, so e.g. CLIP's upper bound is 0 here; kudnn_linear_postops_* takes both parameters. */
 KUDNN_HIP_API int kudnn_linear_act_create(const kudnn_tensor_desc *a, const kudnn_tensor_desc *b,
                                           const kudnn_tensor_desc *c, const kudnn_tensor_desc *bias, float alpha,
                                           float beta, int kind, int num_threads, kudnn_linear_act_t *plan);

@@ -434,6 +434,14 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
     BatchStrides(c, core.C.bs, cDims);
     for (int s = 0; s < 3; ++s) {
         core.bdim[s] = std::max(aDims[s], bDims[s]);
+        // The reference's validation (kudnn_gemm.cpp:420-432) checks a weight batch dim against src only when src's
+        // dim is not 1, so src [1,M,K] x wei [4,K,N] -> dst [2,M,N] passes it; its CPU loop then walks dst and a
+        // dst-shaped bias past their ends. On the GPU that would be an out-of-bounds write, so a C batch dim must be
+        // 1 (C broadcast: the serial loop) or the batch count itself. Bias dims are 1 or dst's (validated).
+        if (cDims[s] != 1 && cDims[s] != core.bdim[s]) {
+            return Fail(KUDNN_STATUS_BAD_ARGUMENTS,
+                        std::string(op) + ": a batch dim of the output is neither 1 nor the operands' batch count");
+        }
         if (core.bdim[s] > 1 && cDims[s] == 1) {
             core.serial = true;
         }
@@ -543,9 +551,12 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
     }
     if (const char *force = std::getenv("KUDNN_HIP_FORCE_CFG")) {
         int f = std::atoi(force);
+        // The 4-wave and ping-pong configurations need K in whole k-tiles, which the pack guarantees only when the
+        // plan was made for them (M > 16 for 16-bit operands): an override is accepted where it keeps that true.
+        const bool mfmaOk = !(core.M <= 16 && lowp16);
         bool okBf16 = core.computeDt != KUDNN_DT_F32 &&
-                      (f == KUDNN_CFG_BF16_256x256 || f == KUDNN_CFG_BF16_256x128 || f == KUDNN_CFG_BF16_128x128 ||
-                       (f == KUDNN_CFG_BF16_PINGPONG_256x256 && core.M > 16) ||
+                      (((f == KUDNN_CFG_BF16_256x256 || f == KUDNN_CFG_BF16_256x128 || f == KUDNN_CFG_BF16_128x128 ||
+                         f == KUDNN_CFG_BF16_PINGPONG_256x256) && mfmaOk) ||
                        (f == KUDNN_CFG_SKINNY_BF16 && core.M <= 16 && lowp16));
         bool okF32 = core.computeDt == KUDNN_DT_F32 && (f == KUDNN_CFG_F32_128x128 || f == KUDNN_CFG_F32_64x64);
         if (okBf16 || okF32) {
@@ -1379,15 +1390,20 @@ int kudnn_linear_act_create(const kudnn_tensor_desc *a, const kudnn_tensor_desc 
         return Fail(KUDNN_STATUS_NULL_POINTER, "LinearActivationLayerFWD: null argument");
     }
     *plan = nullptr;
-    // Same order of checks as the reference constructor: the Gemm member, then the activation member
-    // (kudnn_linear_activationlayer.cpp:30-38).
+    // Same order of checks as the reference constructor (kudnn_linear_activationlayer.cpp:30-38): the Gemm member,
+    // then the activation member, which is built as activationlayerfwd(cInfo, cInfo, kind, alpha) and so validates
+    // with its default second parameter 0, then the layer's own ValidateInput with the caller's beta.
     int s = ValidateGemm(*a, *b, *c, bias, num_threads);
     if (s != KUDNN_STATUS_SUCCESS) {
         return FailStatus(s, "GEMM");
     }
-    s = ValidateActivation(*c, kind, alpha, beta);
+    s = ValidateActivation(*c, kind, alpha, 0.0f);
     if (s != KUDNN_STATUS_SUCCESS) {
         return FailStatus(s, "Activation layer");
+    }
+    s = ValidateActivation(*c, kind, alpha, beta);
+    if (s != KUDNN_STATUS_SUCCESS) {
+        return FailStatus(s, "LinearActivationLayerFWD");
     }
     if (!ActImplemented(kind)) {
         return Fail(KUDNN_STATUS_UNSUPPORTED,
@@ -1410,9 +1426,10 @@ int kudnn_linear_act_create(const kudnn_tensor_desc *a, const kudnn_tensor_desc 
         delete p;
         return s;
     }
+    // the layer's beta never reaches the activation (kudnn_linear_activationlayer.cpp:33): it runs with 0
     p->x.act = kind;
     p->x.actAlpha = alpha;
-    p->x.actBeta = beta;
+    p->x.actBeta = 0.0f;
     p->desc = DescribeCore(p->core) + " act=" + std::to_string(kind);
     *plan = p;
     return KUDNN_STATUS_SUCCESS;

@@ -9,12 +9,16 @@ float32 or bfloat16 that do not require gradients: the call goes through the C A
 ``linear``. Enabling fails loudly if the HIP library is missing; nothing falls back to a CPU path.
 
 Plans are built once per (M, K, N, dtypes, post-ops) and cached; a plan's kernel choice, tile configuration and
-workspace are fixed at construction, as the KuDNN primitive descriptor's are.
+workspace are fixed at construction, as the KuDNN primitive descriptor's are. The cache holds at most
+``MAX_CACHED_PLANS`` plans and drops the least recently used one beyond that (prefill with many distinct sequence
+lengths would otherwise keep one device workspace per length); a dropped plan is destroyed, and its workspace freed,
+once no caller holds it any more.
 """
 from __future__ import annotations
 
 import threading
-from typing import Dict, Optional, Tuple
+from collections import OrderedDict
+from typing import Optional, Tuple
 
 import torch
 
@@ -32,7 +36,8 @@ _ACTS = {None: ACT_UNIMPLEMENTED, "relu": ACT_RELU, "silu": ACT_SWISH, "swish": 
 _BINS = {None: BIN_NONE, "add": BIN_ADD, "ext": BIN_EXT, "mul": BIN_MUL}
 _DTYPES = {torch.float32: F32, torch.bfloat16: BF16}
 
-_plans: Dict[Tuple, LinearPostOps] = {}
+MAX_CACHED_PLANS = 64
+_plans: "OrderedDict[Tuple, LinearPostOps]" = OrderedDict()
 _plans_lock = threading.Lock()
 
 
@@ -41,13 +46,19 @@ def _plan(m: int, k: int, n: int, xdt: int, wdt: int, ydt: int, has_bias: bool, 
     key = (m, k, n, xdt, wdt, ydt, has_bias, act, act_alpha, act_beta, binary)
     with _plans_lock:
         plan = _plans.get(key)
-        if plan is None:
+        if plan is not None:
+            _plans.move_to_end(key)
+        else:
             # X{M,K} AB; W{K,N} BA (physically [N][K], nn.Linear's weight); bias{1,N}; Y and the binary operand {M,N}
             dy = desc([m, n], ydt)
             plan = LinearPostOps(desc([m, k], xdt), desc([k, n], wdt, "BA"), dy, desc([1, n], ydt) if has_bias else None,
                                  act=act, act_alpha=act_alpha, act_beta=act_beta, binary=binary,
                                  src=dy if binary != BIN_NONE else None)
             _plans[key] = plan
+            while len(_plans) > MAX_CACHED_PLANS:
+                # dropped, not closed: a caller on another thread may still be running it; the plan's destructor
+                # frees its workspace when the last reference goes
+                _plans.popitem(last=False)
         return plan
 
 

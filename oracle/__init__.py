@@ -75,7 +75,7 @@ def lib() -> ctypes.CDLL:
             "oracle_gemm": ([G], ctypes.c_int),
             "oracle_res_add": ([ctypes.c_int, ctypes.c_int64, P, P, P, ctypes.c_int, ctypes.c_float], ctypes.c_int),
             "oracle_binary": ([T, P, T, P, ctypes.c_int, ctypes.c_float], ctypes.c_int),
-            "oracle_linear_act": ([G, ctypes.c_int, ctypes.c_float, ctypes.c_float], ctypes.c_int),
+            "oracle_linear_act": ([G, ctypes.c_int, ctypes.c_float], ctypes.c_int),
             "oracle_linear_res": ([G, T, P, T, P, ctypes.c_int, ctypes.c_float], ctypes.c_int),
             "oracle_linear_postops": ([G, ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_int, T, P, ctypes.c_float],
                                       ctypes.c_int),
@@ -201,9 +201,11 @@ def gemm(a, b, c, bias=None, alpha=1.0, beta=0.0) -> None:
     assert lib().oracle_gemm(ctypes.byref(g)) == 0
 
 
-def linear_act(a, b, c, bias=None, kind=ACT_RELU, alpha=0.0, beta=0.0) -> None:
+def linear_act(a, b, c, bias=None, kind=ACT_RELU, alpha=0.0) -> None:
+    """LinearActivationLayerFWD::Run: the activation gets the layer's alpha; its second parameter is 0 whatever the
+    layer's beta (kudnn_linear_activationlayer.cpp:33)."""
     g = _gemm_struct(a, b, c, bias)
-    assert lib().oracle_linear_act(ctypes.byref(g), kind, alpha, beta) == 0
+    assert lib().oracle_linear_act(ctypes.byref(g), kind, alpha) == 0
 
 
 def linear_res(a, b, c, bias, res, lr, kind=RES_IDENTIAL, gamma=1.0) -> None:
@@ -219,6 +221,18 @@ def linear_postops(a, b, y, bias=None, act=ACT_NONE, act_alpha=0.0, binary=BIN_N
     st = src.otensor() if src is not None else OTensor()
     sp = src.ptr() if src is not None else None
     assert lib().oracle_linear_postops(ctypes.byref(g), act, act_alpha, act_beta, binary, ctypes.byref(st), sp, gamma) == 0
+
+
+def activation(t: Tensor, kind: int, alpha: float = 0.0, beta: float = 0.0) -> None:
+    """In place over a dense tensor: the activation stage with the kind's bf16 store rule."""
+    ot = t.otensor()
+    assert lib().oracle_activation(ctypes.byref(ot), t.ptr(), kind, alpha, beta) == 0
+
+
+def binary(y: Tensor, src: Tensor, kind: int, gamma: float = 1.0) -> None:
+    """In place into y: the binary stage of the post-op chain against a same-shaped src."""
+    yt, st = y.otensor(), src.otensor()
+    assert lib().oracle_binary(ctypes.byref(yt), y.ptr(), ctypes.byref(st), src.ptr(), kind, gamma) == 0
 
 
 def act_f32(kind: int, x: float, alpha: float = 0.0, beta: float = 0.0) -> float:

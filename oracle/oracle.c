@@ -571,8 +571,10 @@ int oracle_binary(const otensor *y, void *py, const otensor *src, const void *ps
 /* composed operators                                                                              */
 
 /* LinearActivationLayerFWD::Run: GEMM (alpha 1, beta 0) into C, then the activation in place
- * (kudnn_linear_activationlayer.cpp:40-56). */
-int oracle_linear_act(const ogemm *g, int kind, float act_alpha, float act_beta)
+ * (kudnn_linear_activationlayer.cpp:40-56). The layer's activation member is built as
+ * activationlayerfwd(cInfo, cInfo, kind, alpha) (:33): the layer's beta is validated but never reaches the activation,
+ * which runs with its default second parameter 0 (kudnn_eltwise.hpp:68-69). */
+int oracle_linear_act(const ogemm *g, int kind, float act_alpha)
 {
     ogemm h = *g;
     h.alpha = 1.0f;
@@ -580,7 +582,7 @@ int oracle_linear_act(const ogemm *g, int kind, float act_alpha, float act_beta)
     if (oracle_gemm(&h) != 0) {
         return -1;
     }
-    return oracle_activation(&g->c, g->pc, kind, act_alpha, act_beta);
+    return oracle_activation(&g->c, g->pc, kind, act_alpha, 0.0f);
 }
 
 /* LinearResFWD::Run (kudnn_linear_res.cpp:184-202): GEMM into C, then RES_MUL = C x res (second GEMM) or

@@ -62,9 +62,85 @@ def from_device(x, dt) -> np.ndarray:
     return a.view(O.storage_dtype(dt))
 
 
-def compare(got_buf: np.ndarray, ref_buf: np.ndarray, dt: int, what: str = ""):
+def _bf16_neighbours(bits: np.ndarray):
+    """The bf16 patterns one ulp above and one ulp below each finite pattern (through zero and subnormals)."""
+    u = bits.astype(np.int32)
+    neg = (u & 0x8000) != 0
+    mag = u & 0x7FFF
+    zero = mag == 0
+    # towards +inf: a positive value grows, a negative one shrinks; zero steps to the smallest subnormal
+    up = np.where(neg, np.where(mag == 0, 0x0001, u - 1), u + 1)
+    down = np.where(neg, u + 1, np.where(zero, 0x8001, u - 1))
+    return up.astype(np.uint16), down.astype(np.uint16)
+
+
+class PostOpsExplainer:
+    """Explains bf16 outputs that fall outside 1e-2 rel / 1e-2 abs of the oracle.
+
+    The GPU sums in another order than the oracle, so its GEMM-stage value can land one bf16 ulp away from the
+    oracle's where the f32 sum sits next to a rounding boundary; its activation can likewise land one ulp away where
+    the activation's f32 value sits next to the store's boundary. Behind a residual add the cancellation can make that
+    one ulp larger than 1e-2 absolute (GELU + residual at |x| > 2, where one ulp is 2^-6). An element outside the
+    tolerance is accepted only if it equals, bit for bit, the oracle's own stages recomputed from the GEMM-stage value
+    or from the activation's stored value moved by one bf16 ulp.
+
+    x, w, bias: the oracle inputs of the rows checked; dims: their output shape; src: the binary operand of those rows.
+    """
+
+    def __init__(self, x, w, bias, dims, act=None, act_alpha=0.0, act_beta=0.0, binary=None, src=None, gamma=1.0):
+        self.x, self.w, self.bias, self.dims = x, w, bias, tuple(dims)
+        self.act = O.ACT_NONE if act is None else act
+        self.act_alpha, self.act_beta = act_alpha, act_beta
+        self.binary = O.BIN_NONE if binary is None else binary
+        self.src, self.gamma = src, gamma
+        self._c = None
+        self.counts = {"gemm stage": 0, "activation stage": 0}
+
+    def _stage0(self) -> np.ndarray:
+        if self._c is None:
+            n = self.dims[-1]
+            c = O.empty(self.dims, tuple(int(np.prod(self.dims[i + 1:])) for i in range(len(self.dims))), O.BF16)
+            O.gemm(self.x, self.w, c, self.bias)
+            self._c = c.buf
+            assert n == self.dims[-1]
+        return self._c
+
+    def _after_act(self, bits: np.ndarray) -> np.ndarray:
+        t = O.Tensor((bits.size,), (1,), O.BF16, bits.copy())
+        if self.act != O.ACT_NONE:
+            O.activation(t, self.act, self.act_alpha, self.act_beta)
+        return t.buf
+
+    def _after_bin(self, bits: np.ndarray, idx: np.ndarray) -> np.ndarray:
+        t = O.Tensor((bits.size,), (1,), O.BF16, bits.copy())
+        if self.binary != O.BIN_NONE:
+            s = O.Tensor((idx.size,), (1,), self.src.dtype, self.src.buf[idx].copy())
+            O.binary(t, s, self.binary, self.gamma)
+        return t.buf
+
+    def __call__(self, idx: np.ndarray, got: np.ndarray) -> np.ndarray:
+        """Boolean mask over idx: which of those elements the one-ulp moves explain (and the counts per stage)."""
+        c = self._stage0()[idx]
+        ok = np.zeros(idx.size, dtype=bool)
+        for moved in _bf16_neighbours(c):
+            hit = self._after_bin(self._after_act(moved), idx) == got
+            self.counts["gemm stage"] += int(np.count_nonzero(hit & ~ok))
+            ok |= hit
+        if self.act != O.ACT_NONE:
+            for moved in _bf16_neighbours(self._after_act(c)):
+                hit = self._after_bin(moved, idx) == got
+                self.counts["activation stage"] += int(np.count_nonzero(hit & ~ok))
+                ok |= hit
+        return ok
+
+
+def compare(got_buf: np.ndarray, ref_buf: np.ndarray, dt: int, what: str = "", explain=None):
     """Asserts the north-star tolerance (bit-exact for integer outputs); returns (max-normalised error, bit-exact
-    fraction)."""
+    fraction).
+
+    Non-finite oracle values must be matched in kind: NaN by NaN, +Inf by +Inf, -Inf by -Inf. bf16: every element must
+    be within 1e-2 rel + 1e-2 abs, except elements that `explain` (a PostOpsExplainer) shows to be the oracle's own
+    result with one intermediate moved by one bf16 ulp; their number is printed."""
     if dt in (O.S32, O.S8, O.U8):
         bad = np.nonzero(got_buf != ref_buf)[0]
         assert bad.size == 0, (f"{what}: {bad.size} of {got_buf.size} integer outputs differ, first at {bad[0]}: "
@@ -73,8 +149,12 @@ def compare(got_buf: np.ndarray, ref_buf: np.ndarray, dt: int, what: str = ""):
     g = O.to_f32(got_buf, dt).astype(np.float64)
     r = O.to_f32(ref_buf, dt).astype(np.float64)
     assert g.shape == r.shape
-    assert np.all(np.isfinite(g) == np.isfinite(r)), f"{what}: non-finite mismatch"
     fin = np.isfinite(r)
+    nan_r, nan_g = np.isnan(r), np.isnan(g)
+    assert np.array_equal(nan_r, nan_g), f"{what}: NaN mismatch at {np.nonzero(nan_r != nan_g)[0][:8]}"
+    inf_r = np.isinf(r)
+    assert np.array_equal(inf_r, np.isinf(g)), f"{what}: Inf mismatch at {np.nonzero(inf_r != np.isinf(g))[0][:8]}"
+    assert np.array_equal(np.sign(r[inf_r]), np.sign(g[inf_r])), f"{what}: an infinity has the wrong sign"
     d = np.abs(g[fin] - r[fin])
     scale = max(np.max(np.abs(r[fin])) if r[fin].size else 0.0, 1e-30)
     maxnorm = float(np.max(d) / scale) if d.size else 0.0
@@ -87,11 +167,17 @@ def compare(got_buf: np.ndarray, ref_buf: np.ndarray, dt: int, what: str = ""):
         assert float(np.mean(bad)) <= 1e-4 if bad.size else True, f"{what}: {np.count_nonzero(bad)} elements outside 2e-3"
     else:
         assert maxnorm <= BF16_MAXNORM_TOL, f"{what}: max-normalised error {maxnorm:.3e} > {BF16_MAXNORM_TOL}"
-        bad = d > (BF16_ATOL + BF16_RTOL * np.abs(r[fin]))
-        frac = float(np.mean(bad)) if bad.size else 0.0
-        # element-wise 1e-2 rel / 1e-2 abs; a handful of elements may differ by one bf16 ulp of an
-        # intermediate where f32 summation order lands on the other side of a rounding boundary
-        assert frac <= 1e-4, f"{what}: {np.count_nonzero(bad)} of {bad.size} elements outside 1e-2 rel/abs"
+        bad = np.nonzero(fin)[0][d > (BF16_ATOL + BF16_RTOL * np.abs(r[fin]))]
+        if bad.size:
+            assert explain is not None, (f"{what}: {bad.size} of {got_buf.size} elements outside 1e-2 rel/abs, first at "
+                                         f"{bad[0]}: got {g[bad[0]]} want {r[bad[0]]}")
+            ok = explain(bad, got_buf[bad])
+            left = bad[~ok]
+            assert left.size == 0, (f"{what}: {left.size} of {bad.size} elements outside 1e-2 rel/abs are not one "
+                                    f"bf16 ulp of an intermediate away, first at {left[0]}: got {g[left[0]]} "
+                                    f"want {r[left[0]]}")
+            print(f"{what}: {bad.size} of {got_buf.size} elements outside 1e-2 rel/abs, each the oracle with one "
+                  f"intermediate moved by one bf16 ulp ({explain.counts})")
     return maxnorm, exact
 
 
@@ -102,8 +188,12 @@ def dense_rows(t: O.Tensor, rows) -> O.Tensor:
     return O.Tensor((len(rows), last), (last, 1), t.dtype, buf)
 
 
-def sample_rows(m: int, count: int, seed: int = 1234) -> np.ndarray:
+def sample_rows(m: int, count: int, seed: int = 1234, band: int = 256) -> np.ndarray:
+    """Rows to check of an m-row output: the edge rows, one row at a random offset inside every `band`-row band (so
+    every 256-row tile row of the GEMM kernels is looked at), and random rows up to `count` in all."""
     rng = np.random.default_rng(seed)
     fixed = [0, 1, m // 2, m - 2, m - 1]
-    rest = rng.choice(m, size=max(0, min(count, m) - len(fixed)), replace=False)
-    return np.unique(np.clip(np.concatenate([fixed, rest]), 0, m - 1))
+    strata = [b + int(rng.integers(0, min(band, m - b))) for b in range(0, m, band)]
+    picked = np.unique(np.clip(np.array(fixed + strata), 0, m - 1))
+    rest = rng.choice(m, size=max(0, min(count, m) - picked.size), replace=False)
+    return np.unique(np.concatenate([picked, rest]))

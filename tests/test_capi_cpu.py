@@ -105,7 +105,9 @@ def test_linear_act_validation_and_kinds():
     for kind in (K.ACT_ABS, K.ACT_EXP, K.ACT_LINEAR, K.ACT_LOG, K.ACT_ROUND, K.ACT_SQRT, K.ACT_SQUARE, K.ACT_TANH,
                  K.ACT_SIGMOID, K.ACT_POW, K.ACT_CLIP, K.ACT_CLIP_V2, K.ACT_HARDSIGMOID, K.ACT_HARDSWISH, K.ACT_ELU,
                  K.ACT_ELU_DST, K.ACT_SRELU, K.ACT_MISH):
-        K.LinearActivation(a, b, c, None, 1.0, 2.0, kind)
+        # CLIP's lower bound must not exceed the activation member's upper bound, which is 0 (see below)
+        alpha = -1.0 if kind in (K.ACT_CLIP, K.ACT_CLIP_V2) else 1.0
+        K.LinearActivation(a, b, c, None, alpha, 2.0, kind)
     exp_dst = 16
     assert v(exp_dst) == K.UNSUPPORTED
     with pytest.raises(K.KudnnError) as e:
@@ -115,6 +117,50 @@ def test_linear_act_validation_and_kinds():
     assert v(K.ACT_CLIP, 2.0, 1.0) == K.UNSUPPORTED  # alpha > beta
     assert v(K.ACT_SRELU, 0.0) == K.UNSUPPORTED
     assert v(K.ACT_SWISH, cc=K.desc([5, 7], K.S8)) == K.UNSUPPORTED
+
+
+def test_linear_act_beta_reaches_validation_only():
+    # The reference builds the layer's activation as activationlayerfwd(cInfo, cInfo, kind, alpha)
+    # (kudnn_linear_activationlayer.cpp:33): that member validates with beta = 0 and runs with beta = 0, while the
+    # layer's own ValidateInput sees the caller's beta.
+    F = K.F32
+    a, b, c = K.desc([5, 6], F), K.desc([6, 7], F), K.desc([5, 7], F)
+    lib = K.lib()
+    # CLIP with 0 < alpha <= beta: the static check passes, the constructor refuses (alpha > the member's beta 0)
+    assert lib.kudnn_linear_act_validate(a, b, c, None, 0.5, 1.0, K.ACT_CLIP, 0) == K.SUCCESS
+    with pytest.raises(K.KudnnError) as e:
+        K.LinearActivation(a, b, c, None, 0.5, 1.0, K.ACT_CLIP)
+    assert e.value.status == K.UNSUPPORTED and "Activation layer" in str(e.value)
+    # CLIP with alpha <= 0 < ... but alpha > beta: the member passes (alpha <= 0), the layer's own check refuses
+    with pytest.raises(K.KudnnError) as e:
+        K.LinearActivation(a, b, c, None, -0.5, -1.0, K.ACT_CLIP)
+    assert e.value.status == K.UNSUPPORTED and "LinearActivationLayerFWD" in str(e.value)
+    K.LinearActivation(a, b, c, None, -0.5, 1.0, K.ACT_CLIP)
+
+
+def test_batch_dim_of_output_must_match_operands():
+    # src [1,M,K] x wei [4,K,N] -> dst [2,M,N] passes the reference's validation (a weight dim is compared with src's
+    # only when src's is not 1) but would address 4 batches of a 2-batch output: refused at plan creation
+    F = K.F32
+    a, b = K.desc([1, 64, 128], F), K.desc([4, 128, 64], F)
+    assert K.lib().kudnn_gemm_validate(a, b, K.desc([2, 64, 64], F), None, 0) == K.SUCCESS
+    with pytest.raises(K.KudnnError) as e:
+        K.Gemm(a, b, K.desc([2, 64, 64], F))
+    assert e.value.status == K.BAD_ARGUMENTS
+    with pytest.raises(K.KudnnError):
+        K.LinearActivation(a, b, K.desc([2, 64, 64], F), K.desc([2, 1, 64], F), 0.0, 0.0, K.ACT_RELU)
+    # dst batch = the operands' batch count (src broadcast) and dst batch 1 (the serial loop) stay accepted
+    assert "batches=4" in K.Gemm(a, b, K.desc([4, 64, 64], F)).describe()
+    assert "serial" in K.Gemm(a, b, K.desc([1, 64, 64], F)).describe()
+
+
+def test_forced_mfma_config_keeps_decode_plans(monkeypatch):
+    # a forced 4-wave or ping-pong configuration needs whole k-tiles, which only the prefill plans pack for: a
+    # 16-bit plan with M <= 16 keeps its decode kernel
+    for cfg in ("1", "2", "3", "4"):
+        monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", cfg)
+        assert plan_of(4, 200, 64).describe().startswith("skinny_bf16"), cfg
+        assert plan_of(64, 256, 64).describe().startswith("mfma_bf16")
 
 
 def test_linear_res_validation():

@@ -1,6 +1,10 @@
 """GPU parity of every forward activation kind of the reference (src/dnn/src/kudnn_eltwise.cpp:333-400) as a fused
-Linear epilogue (LinearActivationLayerFWD), f32 and bf16, on the 4-wave MFMA kernels, the ping-pong kernel, the
-M = 1 GEMV and the 2 <= M <= 16 skinny kernel, against the CPU oracle.
+Linear epilogue, f32 and bf16, on the 4-wave MFMA kernels, the ping-pong kernel, the M = 1 GEMV and the 2 <= M <= 16
+skinny kernel, against the CPU oracle.
+
+Kinds with a second parameter (LINEAR, POW, CLIP, CLIP_V2, HARDSIGMOID, HARDSWISH) run through the post-op chain,
+which passes both parameters; LinearActivationLayerFWD passes only alpha (its activation's second parameter is 0,
+kudnn_linear_activationlayer.cpp:33), which test_linear_act_drops_beta checks.
 """
 import numpy as np
 import pytest
@@ -51,12 +55,17 @@ def run_act(name, dt, M, N, Kd, force=None, monkeypatch=None):
     w = Case([Kd, N], dt, "BA", seed=301, lo=lo, hi=1.0)
     b = Case([1, N], dt, seed=302, lo=0.0 if dom == "positive" else -0.1, hi=0.1)
     c = Case([M, N], dt, zero=True)
-    plan = K.LinearActivation(x.desc, w.desc, c.desc, b.desc, alpha, beta, kind)
     dc = zeros_device(c)
-    plan.run(x.device(), w.device(), dc, b.device())
-    torch.cuda.synchronize()
     ref = c.clone_empty()
-    O.linear_act(x.t, w.t, ref, b.t, kind, alpha, beta)
+    if beta == 0.0:
+        plan = K.LinearActivation(x.desc, w.desc, c.desc, b.desc, alpha, 0.0, kind)
+        plan.run(x.device(), w.device(), dc, b.device())
+        O.linear_act(x.t, w.t, ref, b.t, kind, alpha)
+    else:
+        plan = K.LinearPostOps(x.desc, w.desc, c.desc, b.desc, act=kind, act_alpha=alpha, act_beta=beta)
+        plan.run(x.device(), w.device(), dc, b.device())
+        O.linear_postops(x.t, w.t, ref, b.t, kind, alpha, act_beta=beta)
+    torch.cuda.synchronize()
     compare(from_device(dc, dt), ref.buf, dt, f"{plan.describe()} {name}")
     return plan
 
@@ -100,8 +109,25 @@ def test_round_ties_to_even(dt):
     plan.run(x.device(), w.device(), dc, b.device())
     torch.cuda.synchronize()
     ref = c.clone_empty()
-    O.linear_act(x.t, w.t, ref, b.t, O.ACT_ROUND, 0.0, 0.0)
+    O.linear_act(x.t, w.t, ref, b.t, O.ACT_ROUND, 0.0)
     got = from_device(dc, dt)
     assert np.array_equal(got, ref.buf), plan.describe()
     vals = O.to_f32(ref.buf, dt)
     assert np.all(vals == np.rint(vals)) and np.any(np.abs(vals) % 2 == 0)
+
+
+@pytest.mark.parametrize("name", ["linear", "hardsigmoid", "pow3"])
+def test_linear_act_drops_beta(name):
+    # the same kinds through LinearActivationLayerFWD: the layer's beta is validated, then the activation runs with 0
+    kind, alpha, beta, _ = KINDS[name]
+    M, N, Kd = 64, 48, 32
+    x = Case([M, Kd], O.BF16, seed=310)
+    w = Case([Kd, N], O.BF16, "BA", seed=311)
+    c = Case([M, N], O.BF16, zero=True)
+    plan = K.LinearActivation(x.desc, w.desc, c.desc, None, alpha, beta, kind)
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc)
+    torch.cuda.synchronize()
+    ref = c.clone_empty()
+    O.linear_act(x.t, w.t, ref, None, kind, alpha)
+    compare(from_device(dc, O.BF16), ref.buf, O.BF16, f"{plan.describe()} {name}")

@@ -9,7 +9,7 @@ import pytest
 
 import kudnn_amd as K
 import oracle as O
-from support import Case, compare, dense_rows, from_device, sample_rows, zeros_device
+from support import Case, PostOpsExplainer, compare, dense_rows, from_device, sample_rows, zeros_device
 
 pytestmark = pytest.mark.gpu
 
@@ -172,7 +172,7 @@ def test_c2_fp32_silu_rows():
     plan.run(x.device(), w.device(), dc, b.device())
     torch.cuda.synchronize()
     got = from_device(dc, O.F32).reshape(M, N)
-    rows = sample_rows(M, 24)
+    rows = sample_rows(M, 24)  # every 256-row tile row, the edges, and random rows
     ref = O.empty((len(rows), N), (N, 1), O.F32)
     O.linear_act(dense_rows(x.t, rows), w.t, ref, b.t, O.ACT_SWISH, 1.0)
     compare(got[rows].reshape(-1), ref.buf, O.F32, "C2 " + plan.describe())
@@ -190,11 +190,14 @@ def test_c3_bf16_gelu_residual_rows():
     plan.run(x.device(), w.device(), dy, b.device(), r.device())
     torch.cuda.synchronize()
     got = from_device(dy, O.BF16).reshape(M, N)
-    rows = sample_rows(M, 24)
+    rows = sample_rows(M, 32)  # every 256-row tile row, the edges, and random rows
+    xr, rr = dense_rows(x.t, rows), dense_rows(r.t, rows)
     ref = O.empty((len(rows), N), (N, 1), O.BF16)
-    O.linear_postops(dense_rows(x.t, rows), w.t, ref, b.t, O.ACT_GELU_TANH, 0.0, O.BIN_ADD, dense_rows(r.t, rows))
-    maxnorm, exact = compare(got[rows].reshape(-1), ref.buf, O.BF16, "C3 " + plan.describe())
-    print(f"C3 max-normalised error {maxnorm:.3e}, bit-exact fraction {exact:.5f}")
+    O.linear_postops(xr, w.t, ref, b.t, O.ACT_GELU_TANH, 0.0, O.BIN_ADD, rr)
+    why = PostOpsExplainer(xr, w.t, b.t, (len(rows), N), act=O.ACT_GELU_TANH, binary=O.BIN_ADD, src=rr)
+    maxnorm, exact = compare(got[rows].reshape(-1), ref.buf, O.BF16, "C3 " + plan.describe(), explain=why)
+    print(f"C3 rows {len(rows)}: max-normalised error {maxnorm:.3e}, bit-exact fraction {exact:.5f}, "
+          f"one-ulp exceptions {why.counts}")
 
 
 def _random_gemm_cases(count=24, seed=4051):
@@ -219,14 +222,17 @@ def test_gemm_random_shapes(M, N, Kd, dt, wl):
         s = Case([M, N], dt, seed=233, lo=-1.0, hi=1.0)
         plan = K.LinearPostOps(x.desc, w.desc, y.desc, b.desc, act=K.ACT_RELU, binary=K.BIN_ADD, src=s.desc)
         plan.run(x.device(), w.device(), dy, b.device(), s.device())
-        O.linear_postops(dense_rows(x.t, rows), w.t, ref, b.t, O.ACT_RELU, 0.0, O.BIN_ADD, dense_rows(s.t, rows))
+        xr, sr = dense_rows(x.t, rows), dense_rows(s.t, rows)
+        O.linear_postops(xr, w.t, ref, b.t, O.ACT_RELU, 0.0, O.BIN_ADD, sr)
+        why = PostOpsExplainer(xr, w.t, b.t, (len(rows), N), act=O.ACT_RELU, binary=O.BIN_ADD, src=sr)
     else:
+        why = None
         plan = K.LinearActivation(x.desc, w.desc, y.desc, b.desc, 1.0, 0.0, K.ACT_SWISH)
         plan.run(x.device(), w.device(), dy, b.device())
         O.linear_act(dense_rows(x.t, rows), w.t, ref, b.t, O.ACT_SWISH, 1.0)
     torch.cuda.synchronize()
     got = from_device(dy, dt).reshape(M, N)
-    _, exact = compare(got[rows].reshape(-1), ref.buf, dt, f"M={M} N={N} K={Kd} {wl} {plan.describe()}")
+    _, exact = compare(got[rows].reshape(-1), ref.buf, dt, f"M={M} N={N} K={Kd} {wl} {plan.describe()}", explain=why)
     if dt == O.BF16:
         assert exact > 0.99, f"only {exact:.4f} of the elements are bit-exact"
 
@@ -405,10 +411,11 @@ def test_c5_bf16_3d_silu_kmajor_rows():
     plan.run(x.device(), w.device(), dy, b.device())
     torch.cuda.synchronize()
     got = from_device(dy, O.BF16).reshape(B * S, N)
-    rows = sample_rows(B * S, 24)
+    rows = sample_rows(B * S, 24)  # 64 bands of 256 rows: one row of each, the edges, and random rows
     ref = O.empty((len(rows), N), (N, 1), O.BF16)
     O.linear_act(dense_rows(x.t, rows), as2d(w.t), ref, as2d(b.t), O.ACT_SWISH, 1.0)
     compare(got[rows].reshape(-1), ref.buf, O.BF16, "C5 " + plan.describe())
+    assert len(rows) >= B * S // 256
 
 
 # ---------------------------------------------------------------------------------------------------
@@ -443,7 +450,9 @@ def test_pingpong_shapes_and_epilogues(force_pingpong, mnk, post):
     torch.cuda.synchronize()
     ref = y.clone_empty()
     O.linear_postops(x.t, w.t, ref, b.t if b else None, act, aa, binary, s.t if s else None, 0.75)
-    compare(from_device(dy, dt), ref.buf, dt, f"{plan.describe()} {post}")
+    why = PostOpsExplainer(x.t, w.t, b.t if b else None, (M, N), act=act, act_alpha=aa, binary=binary,
+                           src=s.t if s else None, gamma=0.75)
+    compare(from_device(dy, dt), ref.buf, dt, f"{plan.describe()} {post}", explain=why)
 
 
 @pytest.mark.parametrize("mnk", [(512, 512, 128), (300, 520, 192)])
@@ -465,7 +474,9 @@ def test_pingpong_epilogue_forms(force_pingpong, mnk, ydt, bias_rows):
     torch.cuda.synchronize()
     ref = y.clone_empty()
     O.linear_postops(x.t, w.t, ref, b.t, O.ACT_GELU_ERF, 0.0, O.BIN_ADD, s.t, 1.0)
-    compare(from_device(dy, ydt), ref.buf, ydt, f"{plan.describe()} ydt={ydt} bias_rows={bias_rows}")
+    why = PostOpsExplainer(x.t, w.t, b.t, (M, N), act=O.ACT_GELU_ERF, binary=O.BIN_ADD, src=s.t) \
+        if ydt == O.BF16 else None
+    compare(from_device(dy, ydt), ref.buf, ydt, f"{plan.describe()} ydt={ydt} bias_rows={bias_rows}", explain=why)
 
 
 def _rounding_boundary_values(seed: int = 7, nans: bool = False) -> np.ndarray:
@@ -532,7 +543,9 @@ def test_pingpong_linear_res_stores_c(force_pingpong, kind):
     rc, rlr = c.clone_empty(), lr.clone_empty()
     O.linear_res(x.t, w.t, rc, b.t, res.t, rlr, kind, 0.625)
     compare(from_device(dc, O.BF16), rc.buf, O.BF16, plan.describe() + " C")
-    compare(from_device(dlr, O.BF16), rlr.buf, O.BF16, plan.describe() + " linearRes")
+    why = PostOpsExplainer(x.t, w.t, b.t, (M, N), binary=O.BIN_ADD if kind == O.RES_IDENTIAL else O.BIN_EXT,
+                           src=res.t, gamma=0.625)
+    compare(from_device(dlr, O.BF16), rlr.buf, O.BF16, plan.describe() + " linearRes", explain=why)
 
 
 def test_pingpong_batched_and_strided_weight(force_pingpong):

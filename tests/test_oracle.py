@@ -294,6 +294,26 @@ def test_linear_act_bf16_rounding_points():
         np.testing.assert_array_equal(c.buf, trunc_bf16(stage1).reshape(-1))
 
 
+def test_linear_act_runs_activation_without_beta():
+    # LinearActivationLayerFWD builds its activation from (kind, alpha) only (kudnn_linear_activationlayer.cpp:33):
+    # LINEAR is alpha * x + 0 and HARDSIGMOID clip(alpha * x + 0, 0, 1), whereas the post-op chain applies beta.
+    # Integer-valued f32 GEMM: every product and sum is exact, so the expected values are closed forms.
+    rng = np.random.default_rng(9)
+    M, K, N = 6, 8, 5
+    A = rng.integers(-3, 4, size=(M, K)).astype(np.float32)
+    B = rng.integers(-3, 4, size=(K, N)).astype(np.float32)
+    a, b = tensor_from(A, F32), tensor_from(B, F32, "BA")
+    G = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    c = O.empty((M, N), (N, 1), F32)
+    O.linear_act(a, b, c, None, O.ACT_LINEAR, 2.0)
+    np.testing.assert_array_equal(c.buf.reshape(M, N), 2.0 * G)
+    O.linear_act(a, b, c, None, O.ACT_HARDSIGMOID, 0.125)
+    np.testing.assert_array_equal(c.buf.reshape(M, N), np.clip(0.125 * G, 0.0, 1.0))
+    y = O.empty((M, N), (N, 1), F32)
+    O.linear_postops(a, b, y, None, O.ACT_LINEAR, 2.0, act_beta=0.5)
+    np.testing.assert_array_equal(y.buf.reshape(M, N), 2.0 * G + 0.5)
+
+
 @pytest.mark.parametrize("dt", [F32, BF16])
 def test_linear_res_kinds(dt):
     rng = np.random.default_rng(8)
