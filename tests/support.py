@@ -134,6 +134,13 @@ class PostOpsExplainer:
         return ok
 
 
+def explainer(dt, x, w, bias, dims, act=None, act_alpha=0.0, act_beta=0.0, binary=None, src=None, gamma=1.0):
+    """A PostOpsExplainer for a bf16 output of the Linear chain (None for other output types)."""
+    if dt != O.BF16:
+        return None
+    return PostOpsExplainer(x, w, bias, dims, act, act_alpha, act_beta, binary, src, gamma)
+
+
 def compare(got_buf: np.ndarray, ref_buf: np.ndarray, dt: int, what: str = "", explain=None):
     """Asserts the north-star tolerance (bit-exact for integer outputs); returns (max-normalised error, bit-exact
     fraction).

@@ -11,7 +11,7 @@ import pytest
 
 import kudnn_amd as K
 import oracle as O
-from support import Case, compare, from_device, zeros_device
+from support import Case, compare, explainer, from_device, zeros_device
 
 pytestmark = pytest.mark.gpu
 
@@ -66,7 +66,8 @@ def run_act(name, dt, M, N, Kd, force=None, monkeypatch=None):
         plan.run(x.device(), w.device(), dc, b.device())
         O.linear_postops(x.t, w.t, ref, b.t, kind, alpha, act_beta=beta)
     torch.cuda.synchronize()
-    compare(from_device(dc, dt), ref.buf, dt, f"{plan.describe()} {name}")
+    why = explainer(dt, x.t, w.t, b.t, (M, N), act=kind, act_alpha=alpha, act_beta=beta)
+    compare(from_device(dc, dt), ref.buf, dt, f"{plan.describe()} {name}", explain=why)
     return plan
 
 
@@ -130,4 +131,5 @@ def test_linear_act_drops_beta(name):
     torch.cuda.synchronize()
     ref = c.clone_empty()
     O.linear_act(x.t, w.t, ref, None, kind, alpha)
-    compare(from_device(dc, O.BF16), ref.buf, O.BF16, f"{plan.describe()} {name}")
+    why = explainer(O.BF16, x.t, w.t, None, (M, N), act=kind, act_alpha=alpha)
+    compare(from_device(dc, O.BF16), ref.buf, O.BF16, f"{plan.describe()} {name}", explain=why)

@@ -9,7 +9,7 @@ import pytest
 
 import kudnn_amd as K
 import oracle as O
-from support import Case, PostOpsExplainer, compare, dense_rows, from_device, sample_rows, zeros_device
+from support import Case, PostOpsExplainer, compare, dense_rows, explainer, from_device, sample_rows, zeros_device
 
 pytestmark = pytest.mark.gpu
 
@@ -49,7 +49,8 @@ def test_linear_act_small(dt, wlayout, mnk, act):
     torch.cuda.synchronize()
     ref = c.clone_empty()
     O.linear_act(x.t, w.t, ref, b.t, act, alpha)
-    compare(from_device(dc, dt), ref.buf, dt, f"{plan.describe()}")
+    why = explainer(dt, x.t, w.t, b.t, (M, N), act=act, act_alpha=alpha)
+    compare(from_device(dc, dt), ref.buf, dt, f"{plan.describe()}", explain=why)
 
 
 @pytest.mark.parametrize("dt", [O.F32, O.BF16])
@@ -109,7 +110,9 @@ def test_linear_res(dt, kind):
     rc, rlr = c.clone_empty(), lr.clone_empty()
     O.linear_res(x.t, w.t, rc, b.t, res.t, rlr, kind, gamma)
     compare(from_device(dc, dt), rc.buf, dt, plan.describe() + " C")
-    compare(from_device(dlr, dt), rlr.buf, dt, plan.describe() + " linearRes")
+    why = None if kind == O.RES_MUL else explainer(dt, x.t, w.t, b.t, (M, N), src=res.t, gamma=gamma,
+                                                   binary=O.BIN_ADD if kind == O.RES_IDENTIAL else O.BIN_EXT)
+    compare(from_device(dlr, dt), rlr.buf, dt, plan.describe() + " linearRes", explain=why)
 
 
 @pytest.mark.parametrize("dt", [O.F32, O.BF16])
@@ -274,7 +277,9 @@ def test_skinny_rows_forms(M, N, Kd):
     torch.cuda.synchronize()
     ref = y.clone_empty()
     O.linear_postops(x.t, w.t, ref, b.t, O.ACT_RELU, 0.0, O.BIN_ADD, s.t)
-    _, exact = compare(from_device(dy, O.BF16), ref.buf, O.BF16, f"skinny M={M} N={N} K={Kd} {plan.describe()}")
+    why = explainer(O.BF16, x.t, w.t, b.t, (M, N), act=O.ACT_RELU, binary=O.BIN_ADD, src=s.t)
+    _, exact = compare(from_device(dy, O.BF16), ref.buf, O.BF16, f"skinny M={M} N={N} K={Kd} {plan.describe()}",
+                       explain=why)
     assert exact > 0.99, f"only {exact:.4f} of the elements are bit-exact"
 
 
@@ -299,7 +304,9 @@ def test_skinny_random_shapes(M, N, Kd):
     torch.cuda.synchronize()
     ref = y.clone_empty()
     O.linear_postops(x.t, w.t, ref, b.t, O.ACT_RELU, 0.0, O.BIN_ADD, s.t)
-    _, exact = compare(from_device(dy, O.BF16), ref.buf, O.BF16, f"skinny M={M} N={N} K={Kd} {plan.describe()}")
+    why = explainer(O.BF16, x.t, w.t, b.t, (M, N), act=O.ACT_RELU, binary=O.BIN_ADD, src=s.t)
+    _, exact = compare(from_device(dy, O.BF16), ref.buf, O.BF16, f"skinny M={M} N={N} K={Kd} {plan.describe()}",
+                       explain=why)
     assert exact > 0.99, f"only {exact:.4f} of the elements are bit-exact"
 
 
@@ -321,6 +328,7 @@ def test_m1_row_gemv(Kd, post):
         plan = K.LinearPostOps(x.desc, w.desc, y.desc, b.desc, act=K.ACT_GELU_TANH, binary=K.BIN_ADD, src=s.desc)
         plan.run(x.device(), w.device(), dy, b.device(), s.device())
         O.linear_postops(x.t, w.t, ref, b.t, O.ACT_GELU_TANH, 0.0, O.BIN_ADD, s.t)
+        why = explainer(ydt, x.t, w.t, b.t, (1, N), act=O.ACT_GELU_TANH, binary=O.BIN_ADD, src=s.t)
     elif post == "swish_f32":
         plan = K.LinearActivation(x.desc, w.desc, y.desc, b.desc, 1.0, 0.0, K.ACT_SWISH)
         plan.run(x.device(), w.device(), dy, b.device())
@@ -331,7 +339,8 @@ def test_m1_row_gemv(Kd, post):
         O.gemm(x.t, w.t, ref, b.t, 0.5, 0.25)
     assert plan.describe().startswith("skinny")
     torch.cuda.synchronize()
-    compare(from_device(dy, ydt), ref.buf, ydt, f"M=1 K={Kd} {post} {plan.describe()}")
+    compare(from_device(dy, ydt), ref.buf, ydt, f"M=1 K={Kd} {post} {plan.describe()}",
+            explain=why if post == "bias_gelu_add" else None)
 
 
 def test_m1_row_gemv_batched_broadcast_weight():
@@ -373,8 +382,10 @@ def test_split_k_small_grids(dt, mnk, post):
         plan = K.LinearPostOps(x.desc, w.desc, y.desc, b.desc, act=act, act_alpha=1.0, binary=binary, src=s.desc)
         plan.run(x.device(), w.device(), dy, b.device(), s.device())
         O.linear_postops(x.t, w.t, ref, b.t, act, 1.0, binary, s.t)
+    why = None if post == "gemm_beta" else explainer(dt, x.t, w.t, b.t, (M, N), act=act, act_alpha=1.0,
+                                                     binary=binary, src=s.t)
     torch.cuda.synchronize()
-    compare(from_device(dy, dt), ref.buf, dt, f"split-K {post} {plan.describe()}")
+    compare(from_device(dy, dt), ref.buf, dt, f"split-K {post} {plan.describe()}", explain=why)
 
 
 def test_plan_workspace_across_streams():

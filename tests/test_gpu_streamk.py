@@ -10,7 +10,7 @@ import pytest
 
 import kudnn_amd as K
 import oracle as O
-from support import Case, compare, dense_rows, from_device, sample_rows, zeros_device
+from support import Case, compare, dense_rows, explainer, from_device, sample_rows, zeros_device
 
 pytestmark = pytest.mark.gpu
 
@@ -65,7 +65,11 @@ def run_linear(M, N, Kd, dt=O.BF16, ydt=None, act=O.ACT_GELU_TANH, alpha=0.0, be
             assert np.array_equal(got, first), f"{plan.describe()}: run {r} differs from run 0"
         if rows is not None:
             got = got.reshape(M, N)[rows].reshape(-1)
-        compare(got, ref.buf, ydt, f"{plan.describe()} run {r}")
+        xr = dense_rows(x.t, rows) if rows is not None else x.t
+        sr = (dense_rows(s.t, rows) if rows is not None else s.t) if s else None
+        why = explainer(ydt, xr, w.t, b.t if b else None, (len(rows) if rows is not None else M, N), act=act,
+                        act_alpha=alpha, act_beta=beta, binary=O.BIN_ADD if binary else None, src=sr)
+        compare(got, ref.buf, ydt, f"{plan.describe()} run {r}", explain=why)
     return plan
 
 

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from support import compare
+from support import compare, explainer
 
 torch = pytest.importorskip("torch")
 import kudnn_amd.torch_linear as T  # noqa: E402
@@ -73,7 +73,8 @@ def test_linear_matches_oracle(dtype, post):
     alpha = 1.0 if act == "silu" else 0.0
     O.linear_postops(ox, ow, ref, ob, acts[act], alpha, bins[binary], os_, 0.5)
     got = _oracle_tensor(y.reshape(74, 80), dt).buf
-    compare(got, ref.buf, dt, f"torch_linear {dtype} {post}")
+    why = explainer(dt, ox, ow, ob, (74, 80), act=acts[act], act_alpha=alpha, binary=bins[binary], src=os_, gamma=0.5)
+    compare(got, ref.buf, dt, f"torch_linear {dtype} {post}", explain=why)
 
 
 @pytest.mark.gpu
@@ -91,7 +92,8 @@ def test_linear_other_activation_kinds(act, alpha, beta, okind):
     ow = O.Tensor((96, 80), (1, 96), O.BF16, _oracle_tensor(w, O.BF16).buf)
     ref = O.empty((37, 80), (80, 1), O.BF16)
     O.linear_postops(ox, ow, ref, None, okind, alpha, O.BIN_NONE, None, 1.0, act_beta=beta)
-    compare(_oracle_tensor(y, O.BF16).buf, ref.buf, O.BF16, f"torch_linear {act}")
+    why = explainer(O.BF16, ox, ow, None, (37, 80), act=okind, act_alpha=alpha, act_beta=beta)
+    compare(_oracle_tensor(y, O.BF16).buf, ref.buf, O.BF16, f"torch_linear {act}", explain=why)
 
 
 @pytest.mark.gpu
