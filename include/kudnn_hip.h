@@ -225,6 +225,17 @@ KUDNN_HIP_API int kudnn_linear_postops_create(const kudnn_tensor_desc *a, const 
 KUDNN_HIP_API int kudnn_linear_postops_run(kudnn_linear_postops_t plan, const void *a, const void *b, void *y,
                                            const void *bias, const void *src, float gamma, void *stream);
 KUDNN_HIP_API int kudnn_linear_postops_destroy(kudnn_linear_postops_t plan);
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc): runs a plan made by kudnn_linear_postops_create exactly as
+ * kudnn_linear_postops_run does (same kernels, same results), but calls no hipMalloc, hipFree or other allocating
+ * routine. Its workspace (operand packs, split-K partials and arrival counters) is a static device array of 64 MiB
+ * per GPU, held from library load until the process ends; a plan that needs more than 64 MiB - 512 bytes of
+ * workspace (e.g. a pack of a weight larger than that) is refused with KUDNN_STATUS_UNSUPPORTED, and every buffer
+ * must be device memory (host pointers: KUDNN_STATUS_BAD_ARGUMENTS). All calls on one GPU share that array: calls
+ * that overlap on one GPU (several streams, or several threads) race and must be serialised by the caller. */
+KUDNN_HIP_API int kudnn_linear_postops_run_noalloc(kudnn_linear_postops_t plan, const void *a, const void *b,
+                                                   void *y, const void *bias, const void *src, float gamma,
+                                                   void *stream);
 
 /* ---- introspection ---------------------------------------------------------------------------------- */
 /* Name of the kernel family the dispatcher chose for a plan ("mfma_bf16_256x256", "skinny_bf16_nt", ...).

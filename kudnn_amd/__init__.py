@@ -130,6 +130,7 @@ _SIGS = {
                                      ctypes.c_float, ctypes.c_int, ctypes.POINTER(_P)], ctypes.c_int),
     "kudnn_linear_postops_run": ([_P, _P, _P, _P, _P, _P, ctypes.c_float, _P], ctypes.c_int),
     "kudnn_linear_postops_destroy": ([_P], ctypes.c_int),
+    "kudnn_linear_postops_run_noalloc": ([_P, _P, _P, _P, _P, _P, ctypes.c_float, _P], ctypes.c_int),
     "kudnn_plan_describe": ([_P, ctypes.c_char_p, ctypes.c_int], ctypes.c_int),
 }
 

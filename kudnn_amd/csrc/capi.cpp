@@ -649,6 +649,13 @@ bool Vec4Ok(const void *p, int dt, const TensorSpec &t, bool needAlign16)
 class Workspace {
 public:
     Workspace() = default;
+    // Fixed memory (the allocation-free entry point): `fixed` holds `fixedBytes` of workspace and `counters` the
+    // split-K arrival counters (zero, and left zero by every split launch). Acquire never allocates, waits or locks;
+    // a request beyond fixedBytes is refused.
+    Workspace(void *fixed, size_t fixedBytes, uint32_t *counters)
+        : fixed_(fixed), fixedBytes_(fixedBytes), fixedCnt_(counters)
+    {
+    }
     Workspace(const Workspace &) {}
     Workspace &operator=(const Workspace &) { return *this; }
     ~Workspace()
@@ -671,6 +678,18 @@ public:
     void *Acquire(size_t bytes, hipStream_t stream, int &rc, uint32_t **counters = nullptr)
     {
         rc = KUDNN_STATUS_SUCCESS;
+        if (fixed_ != nullptr) {
+            if (bytes > fixedBytes_) {
+                rc = Fail(KUDNN_STATUS_UNSUPPORTED, "this plan needs " + std::to_string(bytes) +
+                                                        " bytes of device workspace; the allocation-free entry point "
+                                                        "has " + std::to_string(fixedBytes_));
+                return nullptr;
+            }
+            if (counters != nullptr) {
+                *counters = fixedCnt_;
+            }
+            return fixed_;
+        }
         m_.lock();
         if (counters != nullptr) {
             if (cnt_ == nullptr) {
@@ -730,6 +749,9 @@ public:
 
     void Release(hipStream_t stream)
     {
+        if (fixed_ != nullptr) {
+            return;
+        }
         if (hipEventRecord(done_, stream) == hipSuccess) {
             last_ = stream;
             used_ = true;
@@ -742,6 +764,9 @@ public:
     }
 
 private:
+    void *fixed_ = nullptr;
+    size_t fixedBytes_ = 0;
+    uint32_t *fixedCnt_ = nullptr;
     std::mutex m_;
     void *ptr_ = nullptr;
     void *cnt_ = nullptr;
@@ -1153,6 +1178,49 @@ TensorSpec SpecOf(const kudnn_tensor_desc &d)
     return t;
 }
 
+
+}  // namespace
+
+// =====================================================================================================
+// device scratch of the allocation-free entry point (kudnn_linear_postops_run_noalloc)
+
+namespace {
+
+// Layout: the split-K arrival counters (KUDNN_SPLIT_MAX_TILES uint32, padded to 512 bytes), then the workspace.
+constexpr size_t kScratchBytes = size_t(64) << 20;
+constexpr size_t kScratchCounterBytes = 512;
+static_assert(KUDNN_SPLIT_MAX_TILES * sizeof(uint32_t) <= kScratchCounterBytes, "counter region");
+
+}  // namespace
+
+// One copy per GPU, zero when the code object is loaded, held until the process ends. In host code `scratch` is
+// only the runtime's handle for the symbol: its device address comes from hipGetSymbolAddress (ScratchOf).
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+// The device address of `scratch` on the current device, looked up once per device (with that device current).
+void *ScratchOf(int &rc)
+{
+    static std::atomic<void *> addr[64] = {};
+    rc = KUDNN_STATUS_SUCCESS;
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= 64) {
+        rc = e != hipSuccess ? HipFail(e, "hipGetDevice") : Fail(KUDNN_STATUS_INTERNAL, "device index out of range");
+        return nullptr;
+    }
+    void *p = addr[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            rc = HipFail(e, "hipGetSymbolAddress(scratch)");
+            return nullptr;
+        }
+        addr[dev].store(p, std::memory_order_release);
+    }
+    return p;
+}
 
 }  // namespace
 
@@ -1724,6 +1792,37 @@ int kudnn_linear_postops_run(kudnn_linear_postops_t plan, const void *a, const v
         rc = RunCore(plan->core, plan->x, da, db, dy, dbias, dsrc, nullptr, 1.0f, 0.0f, gamma, plan->ws, st);
     }
     return stg.Finish(rc);
+}
+
+int kudnn_linear_postops_run_noalloc(kudnn_linear_postops_t plan, const void *a, const void *b, void *y,
+                                     const void *bias, const void *src, float gamma, void *stream)
+{
+    if (plan == nullptr) {
+        return Fail(KUDNN_STATUS_NULL_POINTER, "LinearPostOpsFWD: null plan");
+    }
+    if (a == nullptr || b == nullptr || y == nullptr || (plan->core.hasBias && bias == nullptr) ||
+        (plan->x.hasSrc && src == nullptr)) {
+        return Fail(KUDNN_STATUS_NULL_POINTER, "LinearPostOpsFWD: one of input matrices is nullptr");
+    }
+    if (!plan->core.hasBias && bias != nullptr) {
+        return Fail(KUDNN_STATUS_NULL_POINTER, "LinearPostOpsFWD: bias isn't nullptr, but bias TensorInfo has 0 total size");
+    }
+    // host buffers would need staging copies in allocated device memory
+    for (const void *p : {a, b, static_cast<const void *>(y), bias, src}) {
+        if (!IsDevicePtr(p)) {
+            return Fail(KUDNN_STATUS_BAD_ARGUMENTS,
+                        "LinearPostOpsFWD (no allocation): every buffer must be device memory");
+        }
+    }
+    int rc = KUDNN_STATUS_SUCCESS;
+    void *base = ScratchOf(rc);
+    if (base == nullptr) {
+        return rc;
+    }
+    Workspace fixed(static_cast<char *>(base) + kScratchCounterBytes, kScratchBytes - kScratchCounterBytes,
+                    static_cast<uint32_t *>(base));
+    return RunCore(plan->core, plan->x, a, b, y, bias, src, nullptr, 1.0f, 0.0f, gamma, fixed,
+                   static_cast<hipStream_t>(stream));
 }
 
 int kudnn_linear_postops_destroy(kudnn_linear_postops_t plan)

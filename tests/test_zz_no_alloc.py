@@ -1,0 +1,72 @@
+"""GPU test of kudnn_linear_postops_run_noalloc, the entry point that allocates nothing: through the C ABI its
+results equal kudnn_linear_postops_run's bit for bit (same kernels) on two calls in a row, the second smaller, with
+plans that use the workspace (operand packs and split-K partials, which it takes from its static device scratch)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import kudnn_amd as K
+import oracle as O
+from support import Case, from_device, zeros_device
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    K.lib()
+
+
+def _run_both(M, N, Kd, seed):
+    # weight in layout AB (K-major [K][N]): the MFMA kernels read [N][K], so every run packs it into the workspace
+    x = Case([M, Kd], O.BF16, seed=seed, dist="normal", lo=0.0, hi=1.0)
+    w = Case([Kd, N], O.BF16, "AB", seed=seed + 1, dist="normal", lo=0.0, hi=0.03)
+    b = Case([1, N], O.BF16, seed=seed + 2, lo=-0.1, hi=0.1)
+    s = Case([M, N], O.BF16, seed=seed + 3, lo=-1.0, hi=1.0)
+    y = Case([M, N], O.BF16, zero=True)
+    plan = K.LinearPostOps(x.desc, w.desc, y.desc, b.desc, act=K.ACT_GELU_TANH, binary=K.BIN_ADD, src=s.desc)
+    assert "packB" in plan.describe(), plan.describe()
+    dx, dw, db, ds = x.device(), w.device(), b.device(), s.device()
+    want, got = zeros_device(y), zeros_device(y)
+    plan.run(dx, dw, want, db, ds, gamma=1.0)
+    stream = torch.cuda.current_stream().cuda_stream
+    st = K.lib().kudnn_linear_postops_run_noalloc(plan.handle, dx.data_ptr(), dw.data_ptr(), got.data_ptr(),
+                                                  db.data_ptr(), ds.data_ptr(), ctypes.c_float(1.0), stream)
+    assert st == K.SUCCESS, K.last_error()
+    torch.cuda.synchronize()
+    a, r = from_device(got, O.BF16), from_device(want, O.BF16)
+    assert np.array_equal(a, r), f"{plan.describe()}: {np.count_nonzero(a != r)} outputs differ"
+    assert np.count_nonzero(a) > a.size // 2
+    return plan
+
+
+def test_noalloc_matches_run_on_two_calls():
+    # 256 x 1024 x 2048 (4-wave kernel, split along K, packed weight) then a smaller 64 x 512 x 1000 (K tail: both
+    # operands packed with zero padding); the second call reuses the scratch the first left behind
+    p1 = _run_both(256, 1024, 2048, seed=500)
+    p2 = _run_both(64, 512, 1000, seed=510)
+    assert "packA" in p2.describe()
+
+
+def test_noalloc_refuses_what_it_cannot_do():
+    # a packed weight of 128 MiB exceeds the scratch: refused before anything runs
+    M, N, Kd = 64, 16384, 4096
+    plan = K.LinearPostOps(K.desc([M, Kd], K.BF16), K.desc([Kd, N], K.BF16, "AB"), K.desc([M, N], K.BF16))
+    x = torch.zeros(M * Kd, dtype=torch.int16, device="cuda")
+    w = torch.zeros(Kd * N, dtype=torch.int16, device="cuda")
+    y = torch.zeros(M * N, dtype=torch.int16, device="cuda")
+    lib = K.lib()
+    st = lib.kudnn_linear_postops_run_noalloc(plan.handle, x.data_ptr(), w.data_ptr(), y.data_ptr(), None, None,
+                                              ctypes.c_float(1.0), None)
+    assert st == K.UNSUPPORTED and "workspace" in K.last_error()
+    # host buffers would need staging allocations
+    hx = np.zeros(M * Kd, np.uint16)
+    st = lib.kudnn_linear_postops_run_noalloc(plan.handle, hx.ctypes.data, w.data_ptr(), y.data_ptr(), None, None,
+                                              ctypes.c_float(1.0), None)
+    assert st == K.BAD_ARGUMENTS
+    torch.cuda.synchronize()
