@@ -26,10 +26,18 @@
 // vmcnt(0) wait in front of every LDS read.
 //
 // Rows are 128 bytes per k-tile with a XOR swizzle (chunk ^ ((row >> 1) & 7)) so the 16 lanes of a ds_read_b128
-// quarter-wave hit 16 distinct 16-byte slots of the 64 LDS banks. Copies use raw buffer resources: the per-lane part
-// of the source offset (row within an 8-row block, chunk) is one VGPR and the resource itself starts at the block, so
-// rows past the end of the operand fall outside the resource's range and read as zero. Wave-uniform values are made
-// explicit with readfirstlane.
+// quarter-wave hit 16 distinct 16-byte slots of the 64 LDS banks.
+//
+// Copies are issued from inline asm, so the compiler inserts no waits for them (its alias analysis cannot tell which
+// buffer a copy writes and would otherwise wait for every copy of a memory phase before the next LDS read); the
+// kernel's own s_waitcnt vmcnt(N) calls order each buffer's copies before its first read: group 1 waits at the end of
+// its memory phase for the previous memory phase's copies, group 0 at the end of its compute phase for its A copies.
+// A tile that lies wholly inside the matrix copies through one buffer resource over the whole operand, the lane's row
+// and chunk in the vector offset and the 8-row block and k-tile in the scalar offset: three scalar instructions per
+// 1 KB copy. (Building a resource per copy, as the edge tiles do, took VALU work and SGPR hazards per copy and made the
+// memory phase, 32 copies per group, as long as the compute phase: about 1,080 cycles against 580.) A tile that
+// crosses the matrix edge builds a resource per copy that starts at the copied 8-row block, so rows past the end of
+// the operand fall outside its range and read as zero.
 //
 // Epilogue: the accumulators pass through LDS one 32-column strip at a time and are read back row-major, 8
 // consecutive columns per lane, so bias / activation / residual run on 8 values and the result is one 16-byte store;
@@ -79,17 +87,65 @@ __device__ __forceinline__ void wait_vmcnt()
 }
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-// One 1 KB copy global -> LDS of an 8-row block through a raw buffer resource. The resource starts at the block's
-// first byte (wave-uniform byte offset `off` from `base`) and covers the bytes of the operand that remain after it,
-// so the hardware range check, which applies to the per-lane offset `voff` only, turns rows past the end of the
-// operand into zeros instead of reads outside the allocation.
+// The split (SK) instances keep compiler-visible copies: the intrinsic below, whose waits the compiler inserts (a
+// vmcnt(0) at the end of each memory phase). Their extra live state leaves no registers for the asm copy path.
+// One 1 KB copy global -> LDS of an 8-row block through a raw buffer resource that starts at the block's first byte
+// (wave-uniform byte offset `off` from `base`) and covers the bytes of the operand after it.
 __device__ __forceinline__ void copy_block(const uint8_t *base, uint32_t totalBytes, uint32_t off, uint32_t voff, uint4 *dst)
 {
-    // the clamped difference is a saturating subtract, which only the vector ALU has; without readfirstlane the
-    // resource would look divergent and every copy would be wrapped in a waterfall loop
     const uint32_t remain = __builtin_amdgcn_readfirstlane(off < totalBytes ? totalBytes - off : 0u);
     __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)(base + off), (short)0, (int)remain, 0x00020000);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)dst, 16, voff, 0, 0, 0);
+}
+
+typedef int i32x4_rs_t __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource words: base address, no stride, `bytes` in range, 32-bit data format.
+__device__ __forceinline__ i32x4_rs_t make_rsrc(const uint8_t *base, uint32_t bytes)
+{
+    const uint64_t p = reinterpret_cast<uint64_t>(base);
+    i32x4_rs_t rs;
+    rs.x = __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(p)));
+    rs.y = __builtin_amdgcn_readfirstlane(static_cast<int>((p >> 32) & 0xffffu));
+    rs.z = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes));
+    rs.w = 0x00020000;
+    return rs;
+}
+
+// LDS byte address of a __shared__ buffer.
+__device__ __forceinline__ uint32_t lds_addr(const uint4 *p)
+{
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void *)p));
+}
+
+// One 1 KB copy global -> LDS (64 lanes x 16 bytes written to lds .. lds + 1023): lane bytes at voff + soff of the
+// resource. The s_nop before the copy covers the wait states a copy needs after VALU writes of the SGPRs it reads
+// (the resource words may come from v_readfirstlane) and after the write of M0, which inline asm hides from the
+// compiler's hazard tracking.
+__device__ __forceinline__ void copy_lds(i32x4_rs_t rs, uint32_t voff, uint32_t soff, uint32_t lds)
+{
+    soff = __builtin_amdgcn_readfirstlane(soff);
+    lds = __builtin_amdgcn_readfirstlane(lds);
+    asm volatile("s_nop 4\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %3 offen lds"
+                 ::"v"(voff), "s"(rs), "s"(lds), "s"(soff) : "memory");
+}
+
+// The same without the leading wait states, for copies whose SGPR operands were written by scalar instructions.
+__device__ __forceinline__ void copy_lds_fast(i32x4_rs_t rs, uint32_t voff, uint32_t soff, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %3 offen lds"
+                 ::"v"(voff), "s"(rs), "s"(lds), "s"(soff) : "memory");
+}
+
+// A copy of an 8-row block of a tile that may cross the matrix edge: the resource starts at the block's first byte
+// (`off` from `base`) and covers the bytes of the operand after it, so the hardware range check on the per-lane
+// offset `voff` turns rows past the end of the operand into zeros instead of reads outside the allocation.
+__device__ __forceinline__ void copy_block_edge(const uint8_t *base, uint32_t totalBytes, uint32_t off, uint32_t voff,
+                                                uint32_t lds)
+{
+    // the clamped difference is a saturating subtract, which only the vector ALU has; readfirstlane makes it scalar
+    const uint32_t remain = __builtin_amdgcn_readfirstlane(off < totalBytes ? totalBytes - off : 0u);
+    copy_lds(make_rsrc(base + off, remain), voff, 0u, lds);
 }
 
 // Writes strip j of a wave's accumulators (64 rows x 32 columns) to its staging area, row pitch kPitch floats.
@@ -332,12 +388,20 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
     const uint32_t loB0 = lr * ldb + static_cast<uint32_t>((ls ^ (lr >> 1)) * 16);
     const uint32_t loB1 = lr * ldb + static_cast<uint32_t>((ls ^ (4 + (lr >> 1))) * 16);
     auto copyA = [&](int q, int t, uint4 *dst) __attribute__((always_inline)) {
-        copy_block(A, bytesA, static_cast<uint32_t>(m0 + q * 8) * lda + static_cast<uint32_t>((kb + t) * kRowBytes),
-                   (q & 1) ? loA1 : loA0, dst + q * 8 * kKC);
+        const uint32_t off = static_cast<uint32_t>(m0 + q * 8) * lda + static_cast<uint32_t>((kb + t) * kRowBytes);
+        if constexpr (SK) {
+            copy_block(A, bytesA, off, (q & 1) ? loA1 : loA0, dst + q * 8 * kKC);
+        } else {
+            copy_block_edge(A, bytesA, off, (q & 1) ? loA1 : loA0, lds_addr(dst + q * 8 * kKC));
+        }
     };
     auto copyB = [&](int q, int t, uint4 *dst) __attribute__((always_inline)) {
-        copy_block(B, bytesB, static_cast<uint32_t>(n0 + q * 8) * ldb + static_cast<uint32_t>((kb + t) * kRowBytes),
-                   (q & 1) ? loB1 : loB0, dst + q * 8 * kKC);
+        const uint32_t off = static_cast<uint32_t>(n0 + q * 8) * ldb + static_cast<uint32_t>((kb + t) * kRowBytes);
+        if constexpr (SK) {
+            copy_block(B, bytesB, off, (q & 1) ? loB1 : loB0, dst + q * 8 * kKC);
+        } else {
+            copy_block_edge(B, bytesB, off, (q & 1) ? loB1 : loB0, lds_addr(dst + q * 8 * kKC));
+        }
     };
     // the operand this wave streams inside the loop, selected once by value (group 0: A, group 1: B)
     const uint8_t *sX = g == 0 ? A : B;
@@ -345,6 +409,14 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
     const uint32_t sLd = g == 0 ? lda : ldb;
     const uint32_t sLo0 = g == 0 ? loA0 : loB0, sLo1 = g == 0 ? loA1 : loB1;
 
+    bool fullTile = false;  // the segment's tile lies wholly inside the matrix (set per segment)
+    // LDS byte address of the buffer k-tile I goes to: operand 0 = A (double-buffered), 1 = B (triple-buffered)
+    auto ldsOf = [&](auto ic, int operand) __attribute__((always_inline)) -> uint32_t {
+        constexpr int I = decltype(ic)::value;
+        const uint32_t la = lds_addr(I % 2 == 0 ? a0 : a1);
+        const uint32_t lb = lds_addr(I % 3 == 0 ? b0 : (I % 3 == 1 ? b1 : b2));
+        return operand == 0 ? la : lb;
+    };
     // fragment addressing: rows of a 32-row block start at multiples of 32, so the swizzle term depends on lrow only
     const int lrow = lane & 31, lh = lane >> 5;
     const int fsw = (lrow >> 1) & 7;
@@ -370,7 +442,7 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
 #pragma unroll
             for (int i = 0; i < 2; ++i) fa[s][i] = at[offA + i * 32 * kKC + sl];
         }
-        {
+        if constexpr (SK) {
             const int tt = t + 1 + g;  // group 0 copies A(t+1), group 1 copies B(t+2)
             uint4 *dst = g == 0 ? abuf(std::integral_constant<int, I + 1>{}) : bbuf(std::integral_constant<int, I + 2>{});
             if (tt < nk) {
@@ -380,6 +452,42 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
                     copy_block(sX, sBytes, static_cast<uint32_t>(sR0 + q * 8) * sLd + static_cast<uint32_t>((kb + tt) * kRowBytes),
                                (q & 1) ? sLo1 : sLo0, dst + q * 8 * kKC);
                 }
+            }
+        } else {
+            const int tt = t + 1 + g;  // group 0 copies A(t+1), group 1 copies B(t+2)
+            const uint32_t dl = __builtin_amdgcn_readfirstlane(g == 0 ? ldsOf(std::integral_constant<int, I + 1>{}, 0)
+                                                                      : ldsOf(std::integral_constant<int, I + 2>{}, 1));
+            if (tt < nk) {
+                const uint32_t kofs = static_cast<uint32_t>((kb + tt) * kRowBytes);
+                if (fullTile) {
+                    // one resource from the k-tile's first byte: the lane's row and chunk in the vector offset, the
+                    // 8-row block in the scalar offset; every word is scalar arithmetic
+                    const uint32_t tileOff = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(sR0)) * sLd + kofs;
+                    const i32x4_rs_t rs = make_rsrc(sX + tileOff, sBytes - tileOff);
+                    asm volatile("s_nop 4" ::: "memory");  // wait states after VALU writes of the SGPRs the copies read
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int q = p * 8 + j;
+                        copy_lds_fast(rs, (q & 1) ? sLo1 : sLo0, static_cast<uint32_t>(q * 8) * sLd,
+                                      dl + static_cast<uint32_t>(q * 8 * kKC * 16));
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int q = p * 8 + j;
+                        copy_block_edge(sX, sBytes, static_cast<uint32_t>(sR0 + q * 8) * sLd + kofs, (q & 1) ? sLo1 : sLo0,
+                                        dl + static_cast<uint32_t>(q * 8 * kKC * 16));
+                    }
+                }
+            }
+        }
+        // group 1 lets this phase's copies (B(t+2)) fly and waits for the previous phase's (B(t+1)), which group 0
+        // reads in the next phase
+        if (!SK && g == 1) {
+            if (t + 2 < nk) {
+                wait_vmcnt<8>();
+            } else {
+                wait_vmcnt<0>();
             }
         }
         readB(bt, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
@@ -414,14 +522,15 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
             }
             __builtin_amdgcn_sched_barrier(0);
         });
-        // copies that the next phase boundary needs: group 0's A(t+1) (its only copies in flight);
-        // group 1's B(t+1) (B(t+2) may stay in flight)
+        // group 0's A(t+1) (its only copies in flight), which it reads in the next phase; (SK) group 1's B(t+1)
         if (g == 0) {
             wait_vmcnt<0>();
-        } else if (t + 2 < nk) {
-            wait_vmcnt<8>();
-        } else {
-            wait_vmcnt<0>();
+        } else if (SK) {
+            if (t + 2 < nk) {
+                wait_vmcnt<8>();
+            } else {
+                wait_vmcnt<0>();
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();
@@ -439,6 +548,7 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
             }
         }
         const int sR0 = g == 0 ? m0 : n0;
+        fullTile = m0 + kBM <= M && n0 + kBN <= N;
         // prologue: A(0), B(0), B(1); wave w copies 8-row blocks 4w .. 4w+3 of each
 #pragma unroll
         for (int j = 0; j < 4; ++j) copyA(wave * 4 + j, 0, a0);
