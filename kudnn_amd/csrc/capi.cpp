@@ -357,6 +357,7 @@ struct GemmCore {
     OperandSpec A, B;
     TensorSpec C;
     bool hasBias = false;
+    bool bf16Scalars = false;  // cblas_bgemm's bf16 alpha / beta apply (a bf16 GEMM into bf16 without bias)
     TensorSpec Bias;
     int64_t kp = 0;  // packed row pitch (elements)
     int64_t Batches() const { return bdim[0] * bdim[1] * bdim[2]; }
@@ -382,6 +383,15 @@ void BatchStrides(const kudnn_tensor_desc &t, int64_t bs[3], int64_t dims[3])
 
 int ElemsPerChunk(int computeDt) { return 16 / DtSize(computeDt); }
 
+// The dtype ChooseImpl sees for a tensor: BatchedExtendedGemm (kudnn_gemm.cpp:722-765) first reorders every tensor of
+// more than two dims whose layout is not the standard ABC.. order into an f32 copy (and a reordered dst back from f32
+// afterwards, with the same saturating round-half-even conversion for integer types, vector_convert.hpp:153-179).
+int DispatchDt(const kudnn_tensor_desc &d, int nd)
+{
+    const int standard = nd == 3 ? KUDNN_LAYOUT_ABC : (nd == 4 ? KUDNN_LAYOUT_ABCD : KUDNN_LAYOUT_ABCDE);
+    return (nd > 2 && d.layout != standard) ? KUDNN_DT_F32 : d.dtype;
+}
+
 // Builds the core plan of C = A x B (+ bias) from validated descriptors. Returns a status.
 // `extra` lists further m-indexed epilogue tensors (linearRes, the binary operand) that must allow a batch
 // fold too; their batch strides are updated with the core's.
@@ -397,26 +407,31 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
 
     // dtype combination -> compute type (the registry of kudnn_gemm.cpp:590-601 and the widening / all-f32
     // fallback of ChooseImpl, :628-708):
+    //  - s8 / u8 x s8 / u8 -> s32 with an s32 or s8 bias or none: int8 MFMA into exact int32 (cblas_gemm_s8s8s32,
+    //    s8u8s32, u8s8s32, u8u8s32 with zero operand offsets, :243-324; an s8 bias is the wider-type match, widened
+    //    exactly, :655-671); a u8 operand is packed shifted by -128 and the epilogue adds back the shifted-out terms;
     //  - bf16 x bf16: bf16 MFMA (cblas_sbgemm / cblas_bgemm);
     //  - f16 x f16, f16 x s8, f16 x u8: f16 MFMA (cblas_hgemm / cblas_shgemm; an 8-bit weight is converted to f16
     //    exactly, as the reference's MatrixConverter does before hgemm, :341-372);
-    //  - s8 / u8 x s8 / u8 -> s32 (bias s32 or none): int8 MFMA into exact int32 (cblas_gemm_s8s8s32, s8u8s32, u8s8s32,
-    //    u8u8s32 with zero operand offsets, :243-324); a u8 operand is packed shifted by -128 and the epilogue adds
-    //    back the shifted-out terms;
-    //  - integer operands with a floating output: the all-f32 fallback (the operands are converted exactly);
-    //  - a floating GEMM into an integer output (ConvertFp32ToS32 / ToS8 / ToU8 of a rounded f32 sum) and integer
-    //    GEMMs into s8 / u8 are refused;
-    //  - everything else computes in f32.
-    const int biasDt = IsNone(bias) ? c.dtype : bias->dtype;
-    const bool intOut = !IsFp(c.dtype) || !IsFp(biasDt);
-    if (intOut) {
-        const bool int8a = a.dtype == KUDNN_DT_S8 || a.dtype == KUDNN_DT_U8;
-        const bool int8b = b.dtype == KUDNN_DT_S8 || b.dtype == KUDNN_DT_U8;
-        if (!(int8a && int8b && c.dtype == KUDNN_DT_S32 && biasDt == KUDNN_DT_S32)) {
-            return Fail(KUDNN_STATUS_UNSUPPORTED,
-                        std::string(op) + ": the integer outputs implemented on the MI355X path are s8 / u8 x s8 / u8 "
-                                          "-> s32 (with an s32 bias or none)");
-        }
+    //  - everything else computes in f32, with 8-bit integer operands converted exactly.
+    // Every combination but the first forms alpha * sum + beta * C + bias in f32, which is the all-f32 fallback's
+    // arithmetic (:673-679): the MFMA products of bf16 / f16 / 8-bit values are exact and accumulate in f32. Integer
+    // C and bias elements are read as f32 (s32 rounds to nearest even beyond 2^24, as MatrixConverter's cast does) and
+    // an integer output takes ConvertFp32ToS32 / ToS8 / ToU8 (saturate, then round half to even; :690-700,
+    // service.cpp:77-115). Summing in f32 in a different order than KML changes nothing while every partial sum is
+    // exact in f32 (integer-valued terms below 2^24), so integer outputs match bit for bit there; elsewhere they can
+    // differ where the f32 value lies within rounding of a .5 boundary.
+    // The choice between the exact integer GEMM and f32 arithmetic, and cblas_bgemm's bf16 scalars, follow the dtypes
+    // ChooseImpl sees (DispatchDt; without a bias it sees dst's dtype for the bias, :628-634 with the bias-less
+    // TensorInfo of kudnn_gemm.hpp). Among the float compute types the operands' own dtypes choose: bf16 / f16 products
+    // are exact in f32 either way.
+    const int ea = DispatchDt(a, nd), eb = DispatchDt(b, nd), ec = DispatchDt(c, nd);
+    const bool noBias = TotalSizeOpt(bias) == 0;
+    const int biasDt = noBias ? c.dtype : DispatchDt(*bias, nd);
+    const bool int8a = ea == KUDNN_DT_S8 || ea == KUDNN_DT_U8;
+    const bool int8b = eb == KUDNN_DT_S8 || eb == KUDNN_DT_U8;
+    core.bf16Scalars = noBias && ea == KUDNN_DT_BF16 && eb == KUDNN_DT_BF16 && ec == KUDNN_DT_BF16;
+    if (int8a && int8b && ec == KUDNN_DT_S32 && (biasDt == KUDNN_DT_S32 || biasDt == KUDNN_DT_S8)) {
         core.computeDt = KUDNN_DT_S8;
     } else if (a.dtype == KUDNN_DT_BF16 && b.dtype == KUDNN_DT_BF16) {
         core.computeDt = KUDNN_DT_BF16;
@@ -944,7 +959,11 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
         ep.src_sn = x.Src.sn;
         for (int s = 0; s < 3; ++s) ep.src_bs[s] = x.Src.bs[s];
     }
+    ep.acc_i32 = core.computeDt == KUDNN_DT_S8 ? 1 : 0;
     bool fast = beta == 0.0f && Vec4Ok(ep.y, Y.dt, Y, false);
+    if (!ep.acc_i32 && (!IsFp(Y.dt) || !IsFp(core.C.dt) || (core.hasBias && !IsFp(core.Bias.dt)))) {
+        fast = false;  // integer tensors around a float sum take the element-wise epilogue
+    }
     if (x.storeC) {
         fast = fast && Vec4Ok(c, core.C.dt, core.C, false);
     }
@@ -1402,7 +1421,7 @@ int kudnn_gemm_run(kudnn_gemm_t plan, const void *a, const void *b, void *c, con
         return Fail(KUDNN_STATUS_UNSUPPORTED, "GEMM: s8 x s8 -> s32 runs with alpha = 1 and beta = 0 only");
     }
     // cblas_bgemm takes bf16 alpha/beta when a bf16 C has no bias (kudnn_gemm.cpp:222-226).
-    if (!core.hasBias && core.C.dt == KUDNN_DT_BF16 && core.computeDt == KUDNN_DT_BF16) {
+    if (core.bf16Scalars) {
         alpha = RoundBf16(alpha);
         beta = RoundBf16(beta);
     }
@@ -1487,8 +1506,9 @@ int kudnn_linear_act_create(const kudnn_tensor_desc *a, const kudnn_tensor_desc 
     p->c = *c;
     CopyDesc(bias, p->bias);
     s = BuildCore(*a, *b, *c, &p->bias, p->core, "LinearActivationLayerFWD");
-    if (s == KUDNN_STATUS_SUCCESS && p->core.computeDt == KUDNN_DT_S8) {
-        s = Fail(KUDNN_STATUS_UNSUPPORTED, "LinearActivationLayerFWD: integer GEMMs run through Gemm only");
+    if (s == KUDNN_STATUS_SUCCESS && (p->core.computeDt == KUDNN_DT_S8 || !IsFp(c->dtype))) {
+        // the reference activates an integer C through ReorderLayer's f32 round trip (kudnn_eltwise.cpp:511-585)
+        s = Fail(KUDNN_STATUS_UNSUPPORTED, "LinearActivationLayerFWD: integer GEMMs and outputs run through Gemm only");
     }
     if (s != KUDNN_STATUS_SUCCESS) {
         delete p;
@@ -1595,14 +1615,13 @@ int kudnn_linear_res_create(const kudnn_tensor_desc *a, const kudnn_tensor_desc 
         p->x.Src = SpecOf(*linear_res);   // res is read in linearRes's memory order
         p->x.Src.dt = res->dtype;
         s = BuildCore(*a, *b, *c, &p->bias, p->core, "LinearResFWD", &p->x.Y, &p->x.Src);
-        if (s == KUDNN_STATUS_SUCCESS && p->core.computeDt == KUDNN_DT_S8) {
-            s = Fail(KUDNN_STATUS_UNSUPPORTED, "LinearResFWD: integer GEMMs run through Gemm only");
-        }
     } else {
         s = BuildCore(*a, *b, *c, &p->bias, p->core, "LinearResFWD");
-        if (s == KUDNN_STATUS_SUCCESS && p->core.computeDt == KUDNN_DT_S8) {
-            s = Fail(KUDNN_STATUS_UNSUPPORTED, "LinearResFWD: integer GEMMs run through Gemm only");
-        }
+    }
+    // AddOps reads C, res and linearRes as f16, bf16 or f32 (kudnn_linear_res.cpp:57-122, 192-200)
+    if (s == KUDNN_STATUS_SUCCESS &&
+        (p->core.computeDt == KUDNN_DT_S8 || !IsFp(c->dtype) || !IsFp(res->dtype) || !IsFp(linear_res->dtype))) {
+        s = Fail(KUDNN_STATUS_UNSUPPORTED, "LinearResFWD: integer GEMMs and outputs run through Gemm only");
     }
     if (s == KUDNN_STATUS_SUCCESS && kind == KUDNN_RES_MUL) {
         kudnn_tensor_desc none{};
@@ -1750,8 +1769,9 @@ int kudnn_linear_postops_create(const kudnn_tensor_desc *a, const kudnn_tensor_d
         p->x.Src = SpecOf(*src);
     }
     s = BuildCore(*a, *b, *y, &p->bias, p->core, "LinearPostOpsFWD", p->x.hasSrc ? &p->x.Src : nullptr);
-    if (s == KUDNN_STATUS_SUCCESS && p->core.computeDt == KUDNN_DT_S8 && (act_kind != KUDNN_ACT_UNIMPLEMENTED || p->x.hasSrc)) {
-        s = Fail(KUDNN_STATUS_UNSUPPORTED, "LinearPostOpsFWD: an s8 x s8 -> s32 Linear takes no activation or binary operand");
+    if (s == KUDNN_STATUS_SUCCESS && !IsFp(y->dtype) && (act_kind != KUDNN_ACT_UNIMPLEMENTED || p->x.hasSrc)) {
+        s = Fail(KUDNN_STATUS_UNSUPPORTED, "LinearPostOpsFWD: a Linear into an integer output takes no activation or "
+                                           "binary operand");
     }
     if (s != KUDNN_STATUS_SUCCESS) {
         delete p;

@@ -77,8 +77,29 @@ __device__ __forceinline__ float round_store(int dt, float f)
     return f;
 }
 
-// Element of dtype dt as f32 (8-bit integers are exact; int32 rounds beyond 2^24 and is read this way only where the
-// values are small, as in operand packing).
+// f32 -> integer output element, as ConvertFp32ToS32 / ToS8 / ToU8 (src/dnn/src/service.cpp:77-115): values below
+// the type's minimum or above its maximum saturate, the rest round half to even (nearbyintf in the default rounding
+// mode). The two inputs the reference hands to the hardware's own conversion take aarch64's saturating fcvtzs /
+// fcvtzu, the target the reference is built for: NaN -> 0 and, for s32, +2^31 (== (float)INT32_MAX, so not "above"
+// it) -> INT32_MAX.
+__device__ __forceinline__ int32_t f32_to_int_sat(float v, int dt)
+{
+    const float lo = dt == KUDNN_DT_S32 ? -2147483648.0f : (dt == KUDNN_DT_S8 ? -128.0f : 0.0f);
+    const float hi = dt == KUDNN_DT_S32 ? 2147483648.0f : (dt == KUDNN_DT_S8 ? 127.0f : 255.0f);
+    if (v != v) {
+        return 0;
+    }
+    if (v <= lo) {
+        return dt == KUDNN_DT_S32 ? INT32_MIN : static_cast<int32_t>(lo);
+    }
+    if (v >= hi) {
+        return dt == KUDNN_DT_S32 ? INT32_MAX : static_cast<int32_t>(hi);
+    }
+    return static_cast<int32_t>(__builtin_rintf(v));
+}
+
+// Element of dtype dt as f32 (8-bit integers are exact; int32 rounds to nearest even beyond 2^24, as
+// static_cast<float> does in the reference's MatrixConverter).
 __device__ __forceinline__ float load_elem(const void *p, int dt, int64_t idx)
 {
     switch (dt) {
@@ -92,16 +113,17 @@ __device__ __forceinline__ float load_elem(const void *p, int dt, int64_t idx)
     }
 }
 
-// Stores a value that is already rounded to dt (exact conversion), or rounds with RNE. Integer stores take values
-// that are already integers in range (operand packing of 8-bit data).
+// Stores a value that is already rounded to dt (exact conversion), or rounds with RNE; integer types saturate and
+// round half to even (f32_to_int_sat; exact for the integer values of operand packing).
 __device__ __forceinline__ void store_elem(void *p, int dt, int64_t idx, float v)
 {
     switch (dt) {
         case KUDNN_DT_F32: static_cast<float *>(p)[idx] = v; break;
         case KUDNN_DT_BF16: static_cast<uint16_t *>(p)[idx] = f32_to_bf16_rne(v); break;
         case KUDNN_DT_F16: static_cast<uint16_t *>(p)[idx] = f32_to_f16_rne(v); break;
-        case KUDNN_DT_S8: static_cast<int8_t *>(p)[idx] = static_cast<int8_t>(v); break;
-        case KUDNN_DT_U8: static_cast<uint8_t *>(p)[idx] = static_cast<uint8_t>(v); break;
+        case KUDNN_DT_S8: static_cast<int8_t *>(p)[idx] = static_cast<int8_t>(f32_to_int_sat(v, dt)); break;
+        case KUDNN_DT_U8: static_cast<uint8_t *>(p)[idx] = static_cast<uint8_t>(f32_to_int_sat(v, dt)); break;
+        case KUDNN_DT_S32: static_cast<int32_t *>(p)[idx] = f32_to_int_sat(v, dt); break;
         default: break;
     }
 }
@@ -262,13 +284,17 @@ constexpr int form_dt()
     return FORM == EPI_FORM_BF16 ? KUDNN_DT_BF16 : (FORM == EPI_FORM_F16 ? KUDNN_DT_F16 : KUDNN_DT_F32);
 }
 
-// Raw bits of one element of dtype dt (f32: 32 bits; bf16 / f16: 16 bits, zero-extended).
+// Raw bits of one element of dtype dt (f32 / s32: 32 bits; bf16 / f16: 16 bits, zero-extended; s8 sign-extended,
+// u8 zero-extended).
 __device__ __forceinline__ uint32_t load_raw1(const void *p, int dt, int64_t idx)
 {
     switch (dt) {
-        case KUDNN_DT_F32: return static_cast<const uint32_t *>(p)[idx];
+        case KUDNN_DT_F32:
+        case KUDNN_DT_S32: return static_cast<const uint32_t *>(p)[idx];
         case KUDNN_DT_BF16:
         case KUDNN_DT_F16: return static_cast<const uint16_t *>(p)[idx];
+        case KUDNN_DT_S8: return static_cast<uint32_t>(static_cast<int32_t>(static_cast<const int8_t *>(p)[idx]));
+        case KUDNN_DT_U8: return static_cast<const uint8_t *>(p)[idx];
         default: return 0u;
     }
 }
@@ -279,6 +305,9 @@ __device__ __forceinline__ float raw1_to_f32(uint32_t r, int dt)
         case KUDNN_DT_F32: return u2f(r);
         case KUDNN_DT_BF16: return u2f(r << 16);
         case KUDNN_DT_F16: return f16_to_f32(static_cast<uint16_t>(r));
+        case KUDNN_DT_S8:
+        case KUDNN_DT_S32: return static_cast<float>(static_cast<int32_t>(r));
+        case KUDNN_DT_U8: return static_cast<float>(r);
         default: return 0.0f;
     }
 }
@@ -595,8 +624,8 @@ __device__ __forceinline__ void epi_apply8(const EpiParams &e, const EpiBatch &o
 inline int epi_form(const EpiParams &e, bool need8 = true)
 {
     const int dt = e.y_dt;
-    if (dt == KUDNN_DT_S32) {
-        // the only epilogue of an integer output (the host admits no other options); it checks fast8 itself
+    if (e.acc_i32) {
+        // the only epilogue of int32 accumulators (the host admits no other options); it checks fast8 itself
         return EPI_FORM_I32;
     }
     if ((need8 && !e.fast8) || e.store_c || e.beta != 0.0f) {
@@ -834,10 +863,11 @@ __device__ __forceinline__ void epi_elem(const EpiParams &e, const EpiBatch &ob,
 // Integer epilogue: s8 x s8 -> s32 (cblas_gemm_s8s8s32, src/dnn/src/kudnn_gemm.cpp:243-264, with the bias passed as
 // the C offset for a row / column vector and added afterwards for a full [M, N] bias: the same sum either way).
 // y = acc + bias in int32 with two's-complement wrap; alpha 1, beta 0, no activation or binary operand (the host
-// rejects anything else). The accumulators arrive as the bit patterns of the MFMA's int32 results.
+// rejects anything else). The bias is s32, or s8 widened exactly (ChooseImpl's wider-type match, :655-671). The
+// accumulators arrive as the bit patterns of the MFMA's int32 results.
 __device__ __forceinline__ uint32_t i32_bias(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n)
 {
-    uint32_t v = e.bias == nullptr ? 0u : static_cast<const uint32_t *>(e.bias)[ob.bias + m * e.bias_sm + n * e.bias_sn];
+    uint32_t v = e.bias == nullptr ? 0u : load_raw1(e.bias, e.bias_dt, ob.bias + m * e.bias_sm + n * e.bias_sn);
     // u8 operands: the terms of the -128 shift (all in wrapping 32-bit arithmetic, like the accumulators)
     if (e.corr_m != nullptr) {
         v += static_cast<uint32_t>(e.corr_m[ob.corr_m + m]);

@@ -25,6 +25,7 @@ struct EpiParams {
     int store_c;  // also store the GEMM-stage value to c (LinearResFWD writes C and linearRes)
     int fast4;    // 4-wide vector epilogue allowed (host-checked contiguity and alignment)
     int fast8;    // 8-wide vector epilogue allowed
+    int acc_i32;  // the accumulators are int32 bit patterns (s8 MFMA): the exact integer epilogue
     void *c;              // C (read when beta != 0, written when store_c)
     const void *bias;     // nullptr = no bias
     const void *src;      // binary operand

@@ -20,6 +20,7 @@ _DIR = Path(__file__).resolve().parent
 LIB_PATH = _DIR / "liboracle.so"
 
 F32, F16, BF16, S32, S8, U8 = 1, 2, 3, 4, 5, 6
+DT_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", S32: "s32", S8: "s8", U8: "u8"}
 ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_SWISH, ACT_GELU_ERF = 0, 5, 20, 25, 27
 # the other forward kinds (KuDNN::ActivationFunction values)
 (ACT_ABS, ACT_EXP, ACT_LINEAR, ACT_LOG, ACT_ROUND, ACT_SQRT, ACT_SQUARE, ACT_TANH, ACT_SIGMOID, ACT_POW, ACT_CLIP,
@@ -43,6 +44,7 @@ class OGemm(ctypes.Structure):
         ("a", OTensor), ("b", OTensor), ("c", OTensor), ("bias", OTensor),
         ("pa", ctypes.c_void_p), ("pb", ctypes.c_void_p), ("pbias", ctypes.c_void_p), ("pc", ctypes.c_void_p),
         ("alpha", ctypes.c_float), ("beta", ctypes.c_float),
+        ("reordered", ctypes.c_int32),
     ]
 
 
@@ -70,6 +72,7 @@ def lib() -> ctypes.CDLL:
             "oracle_bf16_to_f32": ([ctypes.c_uint16], ctypes.c_float),
             "oracle_f16_to_f32": ([ctypes.c_uint16], ctypes.c_float),
             "oracle_f32_to_f16_rne": ([ctypes.c_float], ctypes.c_uint16),
+            "oracle_f32_to_int_sat": ([ctypes.c_float, ctypes.c_int], ctypes.c_int64),
             "oracle_act_f32": ([ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_float], ctypes.c_float),
             "oracle_activation": ([T, P, ctypes.c_int, ctypes.c_float, ctypes.c_float], ctypes.c_int),
             "oracle_gemm": ([G], ctypes.c_int),
@@ -195,9 +198,24 @@ def _gemm_struct(a: Tensor, b: Tensor, c: Tensor, bias: Optional[Tensor], alpha=
     return g
 
 
-def gemm(a, b, c, bias=None, alpha=1.0, beta=0.0) -> None:
-    """In place into c.buf: Gemm::Run semantics."""
+_STANDARD_LAYOUTS = {3: "ABC", 4: "ABCD", 5: "ABCDE"}
+REORDERED_A, REORDERED_B, REORDERED_C, REORDERED_BIAS = 1, 2, 4, 8  # O_REORDERED_* of oracle.h
+
+
+def reordered_mask(ndims: int, la=None, lb=None, lc=None, lbias=None) -> int:
+    """The tensors the reference's BatchedExtendedGemm copies to f32 before ChooseImpl (kudnn_gemm.cpp:722-765): those
+    of more than two dims whose layout (a name such as "ABCED"; None = the standard order) is not ABC.., ABCD..."""
+    mask = 0
+    for bit, lay in ((REORDERED_A, la), (REORDERED_B, lb), (REORDERED_C, lc), (REORDERED_BIAS, lbias)):
+        if ndims > 2 and lay is not None and lay != _STANDARD_LAYOUTS[ndims]:
+            mask |= bit
+    return mask
+
+
+def gemm(a, b, c, bias=None, alpha=1.0, beta=0.0, reordered=0) -> None:
+    """In place into c.buf: Gemm::Run semantics. reordered: reordered_mask() of the tensors' layouts."""
     g = _gemm_struct(a, b, c, bias, alpha, beta)
+    g.reordered = reordered
     assert lib().oracle_gemm(ctypes.byref(g)) == 0
 
 
@@ -233,6 +251,11 @@ def binary(y: Tensor, src: Tensor, kind: int, gamma: float = 1.0) -> None:
     """In place into y: the binary stage of the post-op chain against a same-shaped src."""
     yt, st = y.otensor(), src.otensor()
     assert lib().oracle_binary(ctypes.byref(yt), y.ptr(), ctypes.byref(st), src.ptr(), kind, gamma) == 0
+
+
+def f32_to_int_sat(x: float, dt: int) -> int:
+    """ConvertFp32ToS32 / ToS8 / ToU8 of one f32 value (saturate, then round half to even)."""
+    return lib().oracle_f32_to_int_sat(x, dt)
 
 
 def act_f32(kind: int, x: float, alpha: float = 0.0, beta: float = 0.0) -> float:

@@ -40,6 +40,8 @@
 #include <omp.h>
 #endif
 
+#include "oracle.h"
+
 #define O_F32 1
 #define O_F16 2
 #define O_BF16 3
@@ -80,12 +82,6 @@
 #define O_BIN_EXT 2
 #define O_BIN_MUL 3
 
-typedef struct {
-    int32_t ndims;
-    int32_t dtype;
-    int64_t dims[5];
-    int64_t strides[5]; /* logical order, 0 for size-1 dims */
-} otensor;
 
 /* ------------------------------------------------------------------------------------------------ */
 /* element conversions                                                                              */
@@ -201,13 +197,38 @@ static int64_t ld_int(const void *p, int dt, int64_t i)
     }
 }
 
-/* Stores with RNE (the conversion the reference applies when it writes a typed buffer). */
+/* ConvertFp32ToS32 / ToS8 / ToU8 (src/dnn/src/service.cpp:77-115): below the type's minimum -> minimum, above its
+ * maximum -> maximum, else static_cast of nearbyintf (round half to even in the default rounding mode). The reference
+ * leaves two inputs to the hardware's conversion, undefined in C++: NaN, and for s32 +2^31 (equal to
+ * (float)INT32_MAX, so not above it). They are restated as aarch64's saturating fcvtzs / fcvtzu give them, the target
+ * the reference is built for: NaN -> 0, +2^31 -> INT32_MAX. */
+int64_t oracle_f32_to_int_sat(float v, int dt)
+{
+    const double lo = dt == O_S32 ? -2147483648.0 : (dt == O_S8 ? -128.0 : 0.0);
+    const double hi = dt == O_S32 ? 2147483647.0 : (dt == O_S8 ? 127.0 : 255.0);
+    if (isnan(v)) {
+        return 0;
+    }
+    if ((double)v < lo) {
+        return (int64_t)lo;
+    }
+    if ((double)v > hi) {
+        return (int64_t)hi;
+    }
+    return (int64_t)nearbyintf(v);
+}
+
+/* Stores with RNE (the conversion the reference applies when it writes a typed buffer); integer types through
+ * oracle_f32_to_int_sat. */
 static void st(void *p, int dt, int64_t i, float v)
 {
     switch (dt) {
         case O_F32: ((float *)p)[i] = v; break;
         case O_BF16: ((uint16_t *)p)[i] = oracle_f32_to_bf16_rne(v); break;
         case O_F16: ((uint16_t *)p)[i] = oracle_f32_to_f16_rne(v); break;
+        case O_S32: ((int32_t *)p)[i] = (int32_t)oracle_f32_to_int_sat(v, dt); break;
+        case O_S8: ((int8_t *)p)[i] = (int8_t)oracle_f32_to_int_sat(v, dt); break;
+        case O_U8: ((uint8_t *)p)[i] = (uint8_t)oracle_f32_to_int_sat(v, dt); break;
         default: break;
     }
 }
@@ -352,12 +373,6 @@ int oracle_activation(const otensor *t, void *p, int kind, float alpha, float be
 /* ------------------------------------------------------------------------------------------------ */
 /* GEMM stage                                                                                      */
 
-typedef struct {
-    otensor a, b, c, bias; /* bias.ndims == 0: no bias */
-    const void *pa, *pb, *pbias;
-    void *pc;
-    float alpha, beta;
-} ogemm;
 
 static void batch_slots(const otensor *t, int64_t dims[3], int64_t bs[3])
 {
@@ -380,14 +395,29 @@ static float bf16_round_scalar(float f) { return oracle_bf16_to_f32(oracle_f32_t
  *  - bf16 C with bias: f32 temp = f32(C), temp = alpha*AB + beta*temp, temp += bias, RNE (:208-221);
  *  - bf16 C without bias: cblas_bgemm with bf16 alpha/beta, RNE (:222-226);
  *  - f32 / f16 C: value rounded once into C's type after bias (all-f32 fallback :672-705);
- *  - s8 x s8 -> s32 (cblas_gemm_s8s8s32, :243-264): exact integer sum plus the s32 bias (a row / column vector is
+ *  - s8 / u8 x s8 / u8 -> s32 with an s32 or s8 bias or none (cblas_gemm_s8s8s32 and its u8 forms, :243-324; an s8
+ *    bias is ChooseImpl's wider-type match, :655-671): exact integer sum plus the bias (a row / column vector is
  *    KML's C offset, a full [M, N] bias is added afterwards: the same sum), two's-complement wrap into int32; only
- *    alpha 1 and beta 0 are restated (the scaling of an int32 result by float alpha / beta is KML-internal). */
+ *    alpha 1 and beta 0 are restated (the scaling of an int32 result by float alpha / beta is KML-internal);
+ *  - any other integer output or bias: the all-f32 fallback (:673-705): operands, C and bias read as f32, the f32
+ *    value converted by ConvertFp32ToS32 / ToS8 / ToU8 (oracle_f32_to_int_sat). */
 static int oracle_gemm_s8(const ogemm *g);
+
+static int is_int8(int dt) { return dt == O_S8 || dt == O_U8; }
+
+/* The dtype ChooseImpl sees: f32 for a tensor that BatchedExtendedGemm reordered (:722-765). A reordered integer dst
+ * comes back from f32 through ReorderLayer's clamp and nearbyint (vector_convert.hpp:153-179), which gives the same
+ * values as ConvertFp32ToS32 / ToS8 / ToU8, so the final store is the same either way. */
+static int seen_dt(const ogemm *g, const otensor *t, int bit) { return (g->reordered & bit) ? O_F32 : t->dtype; }
 
 int oracle_gemm(const ogemm *g)
 {
-    if (g->c.dtype == O_S32) {
+    const int hasBias0 = g->bias.ndims != 0 && total(&g->bias) != 0;
+    const int ea = seen_dt(g, &g->a, O_REORDERED_A), eb = seen_dt(g, &g->b, O_REORDERED_B);
+    const int ec = seen_dt(g, &g->c, O_REORDERED_C);
+    /* without a bias ChooseImpl sees dst's own dtype for it (the bias-less TensorInfo of kudnn_gemm.hpp) */
+    const int biasDt = hasBias0 ? seen_dt(g, &g->bias, O_REORDERED_BIAS) : g->c.dtype;
+    if (is_int8(ea) && is_int8(eb) && ec == O_S32 && (biasDt == O_S32 || biasDt == O_S8)) {
         return oracle_gemm_s8(g);
     }
     const int nd = g->a.ndims;
@@ -397,7 +427,7 @@ int oracle_gemm(const ogemm *g)
     const int64_t M = g->a.dims[nd - 2], K = g->a.dims[nd - 1], N = g->b.dims[nd - 1];
     const int hasBias = g->bias.ndims != 0 && total(&g->bias) != 0;
     float alpha = g->alpha, beta = g->beta;
-    if (!hasBias && g->c.dtype == O_BF16 && g->a.dtype == O_BF16 && g->b.dtype == O_BF16) {
+    if (!hasBias && ec == O_BF16 && ea == O_BF16 && eb == O_BF16) {
         alpha = bf16_round_scalar(alpha);
         beta = bf16_round_scalar(beta);
     }
@@ -480,7 +510,7 @@ static int oracle_gemm_s8(const ogemm *g)
     }
     const int64_t M = g->a.dims[nd - 2], K = g->a.dims[nd - 1], N = g->b.dims[nd - 1];
     const int hasBias = g->bias.ndims != 0 && total(&g->bias) != 0;
-    if (hasBias && g->bias.dtype != O_S32) {
+    if (hasBias && g->bias.dtype != O_S32 && g->bias.dtype != O_S8) {
         return -3;
     }
     int64_t ad[3], as[3], bd[3], bs_[3], cd[3], cs[3], xd[3], xs[3] = {0, 0, 0};
@@ -514,7 +544,7 @@ static int oracle_gemm_s8(const ogemm *g)
                                    ld_int(g->pb, g->b.dtype, bo + k * b_sk + n * b_sn);
                         }
                         if (hasBias) {
-                            acc += ld_int(g->pbias, O_S32, xo + m * x_sm + n * x_sn);
+                            acc += ld_int(g->pbias, g->bias.dtype, xo + m * x_sm + n * x_sn);
                         }
                         ((int32_t *)g->pc)[co + m * c_sm + n * c_sn] = (int32_t)(uint32_t)(uint64_t)acc;
                     }

@@ -238,22 +238,7 @@ static void TestGemmNegative()
 // ---------------------------------------------------------------------------------------------------
 // numeric cases with host buffers (needs a GPU), checked against the CPU oracle
 
-extern "C" {
-typedef struct {
-    int32_t ndims, dtype;
-    int64_t dims[5], strides[5];
-} otensor;
-typedef struct {
-    otensor a, b, c, bias;
-    const void *pa, *pb, *pbias;
-    void *pc;
-    float alpha, beta;
-} ogemm;
-int oracle_linear_act(const ogemm *g, int kind, float act_alpha);
-int oracle_linear_res(const ogemm *g, const otensor *res, const void *pres, const otensor *lr, void *plr, int kind,
-                      float gamma);
-int oracle_fill(void *p, int dtype, int64_t n, uint64_t seed, int dist, double lo, double hi);
-}
+#include "oracle.h"
 
 static otensor OT(const TensorInfo &t)
 {

@@ -19,7 +19,7 @@ def binary(tmp_path_factory):
     for so in (LIB / "libkudnn.so", LIB / "libkudnn_hip.so", ORACLE / "liboracle.so"):
         assert so.exists(), f"{so} missing: run __graft_entry__.build()"
     out = tmp_path_factory.mktemp("cpp") / "test_kudnn_api"
-    cmd = ["g++", "-std=c++17", "-O1", "-Wall", "-Werror", "-I", str(ROOT / "include"), str(SRC),
+    cmd = ["g++", "-std=c++17", "-O1", "-Wall", "-Werror", "-I", str(ROOT / "include"), "-I", str(ORACLE), str(SRC),
            "-L", str(LIB), "-lkudnn", "-lkudnn_hip", "-L", str(ORACLE), "-loracle",
            f"-Wl,-rpath,{LIB}", f"-Wl,-rpath,{ORACLE}", "-o", str(out)]
     subprocess.run(cmd, check=True)

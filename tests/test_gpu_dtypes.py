@@ -1,7 +1,9 @@
 """GPU parity of the other dtype combinations of the primitive (the reference's GEMM registry,
 src/dnn/src/kudnn_gemm.cpp:590-601): f16 x f16 (cblas_hgemm / cblas_shgemm), f16 x s8 (W8A16: the weight converted
 to f16, :341-372) and s8 x s8 -> s32 (W8A8, cblas_gemm_s8s8s32, :243-264), each on its own MFMA kernels with the same
-epilogue. Integer results are compared bit for bit; f16 results within 2e-3 max-normalised.
+epilogue. ChooseImpl's all-f32 fallback into integer outputs (:673-705) and integer bias / C around a float sum run on the same
+kernels with an element-wise epilogue. Integer results are compared bit for bit (the fallback on integer-valued operands,
+whose f32 sums are exact in any order); f16 results within 2e-3 max-normalised.
 """
 import numpy as np
 import pytest
@@ -278,3 +280,148 @@ def test_s8_operands_float_output():
     ref = c.clone_empty()
     O.gemm(x.t, w.t, ref)
     compare(from_device(dc, O.F32), ref.buf, O.F32, plan.describe())
+
+
+# ---------------------------------------------------------------------------------------------------
+# ChooseImpl's all-f32 fallback into integer outputs (src/dnn/src/kudnn_gemm.cpp:673-705): f32 arithmetic, then
+# ConvertFp32ToS32 / ToS8 / ToU8 (saturate, round half to even; src/dnn/src/service.cpp:77-115); and integer bias or C
+# around a float sum
+
+
+def _int_valued(dims, dt, seed, lo, hi, layout=None):
+    """A Case of dtype dt holding uniform integers in [lo, hi] (exact in every dtype used here)."""
+    c = Case(dims, dt, layout, zero=True)
+    v = np.random.default_rng(seed).integers(lo, hi + 1, size=c.t.buf.size)
+    if dt in (O.S32, O.S8, O.U8):
+        c.t.buf[:] = v.astype(O.storage_dtype(dt))
+    else:
+        c.t.buf[:] = O.from_f32_rne(v.astype(np.float32), dt)
+    return c
+
+
+def run_fallback(M, N, Kd, adt, bdt, cdt, xdt, alpha=0.5, beta=0.5, seed=400, expect=None, span=8):
+    lo = lambda dt, v: 0 if dt == O.U8 else -v
+    x = _int_valued([M, Kd], adt, seed, lo(adt, span), span)
+    w = _int_valued([Kd, N], bdt, seed + 1, lo(bdt, span), span, "BA")
+    c = _int_valued([M, N], cdt, seed + 2, lo(cdt, 100), 100)
+    b = _int_valued([1, N], xdt, seed + 3, lo(xdt, 60), 60) if xdt is not None else None
+    plan = K.Gemm(x.desc, w.desc, c.desc, b.desc if b else None)
+    if expect:
+        assert expect in plan.describe(), plan.describe()
+    dc = c.device()
+    plan.run(x.device(), w.device(), dc, b.device() if b else None, alpha=alpha, beta=beta)
+    torch.cuda.synchronize()
+    ref = O.Tensor(c.t.dims, c.t.strides, cdt, c.t.buf.copy())
+    O.gemm(x.t, w.t, ref, b.t if b else None, alpha=alpha, beta=beta)
+    got = from_device(dc, cdt)
+    if cdt in (O.S32, O.S8, O.U8):
+        # integer-valued operands keep every f32 partial sum exact: bit-exact, whatever the summation order
+        compare(got, ref.buf, cdt, plan.describe())
+    else:
+        assert np.array_equal(got, ref.buf), plan.describe()
+    return plan, got
+
+
+FALLBACK_COMBOS = [
+    (O.F32, O.F32, O.S32, O.F32), (O.F32, O.F32, O.S8, None), (O.BF16, O.BF16, O.U8, O.F32),
+    (O.F16, O.F16, O.S8, O.F16), (O.S8, O.S8, O.S8, None), (O.U8, O.S8, O.U8, O.S32), (O.S8, O.U8, O.S32, O.F32),
+    (O.S8, O.S8, O.S32, O.U8), (O.F32, O.F32, O.F32, O.S32), (O.BF16, O.BF16, O.BF16, O.S8),
+    (O.U8, O.U8, O.S8, O.BF16), (O.F16, O.S8, O.U8, None),
+]
+
+
+@pytest.mark.parametrize("adt,bdt,cdt,xdt", FALLBACK_COMBOS)
+@pytest.mark.parametrize("mnk", [(200, 136, 96), (5, 70, 64), (33, 17, 300)])
+def test_fallback_integer_exact(adt, bdt, cdt, xdt, mnk):
+    # alpha = beta = 0.5 put exact .5 ties in front of the conversion; the value range saturates s8 and u8 outputs
+    M, N, Kd = mnk
+    plan, got = run_fallback(M, N, Kd, adt, bdt, cdt, xdt)
+    if cdt in (O.S8, O.U8):
+        lo, hi = (-128, 127) if cdt == O.S8 else (0, 255)
+        assert np.any(got == hi), "the case does not saturate"
+        if adt != O.U8 or bdt != O.U8:  # u8 x u8 sums are never negative
+            assert np.any(got == lo), "the case does not saturate"
+
+
+def test_fallback_pingpong_and_skinny(monkeypatch):
+    # the bf16 kernels' element-wise epilogue: the ping-pong kernel (forced) and the decode kernel (M <= 16)
+    monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "4")
+    run_fallback(300, 520, 384, O.BF16, O.BF16, O.S8, O.F32, expect="pingpong")
+    monkeypatch.delenv("KUDNN_HIP_FORCE_CFG")
+    run_fallback(4, 520, 384, O.BF16, O.BF16, O.U8, None, expect="skinny")
+    run_fallback(1, 300, 512, O.BF16, O.BF16, O.S32, O.S32, expect="skinny")
+
+
+def test_s8_bias_into_exact_int32():
+    # s8 x s8 -> s32 with an s8 bias: the integer GEMM (ChooseImpl's wider-type match), exact beyond 2^24
+    M, N, Kd = 64, 72, 4096
+    x = Case([M, Kd], O.S8, seed=410, lo=-128, hi=127)
+    w = Case([Kd, N], O.S8, "BA", seed=411, lo=-128, hi=127)
+    x.t.buf[: Kd * 4] = -128
+    w.t.buf[: Kd * 4] = -128
+    b = Case([1, N], O.S8, seed=412, lo=-128, hi=127)
+    c = Case([M, N], O.S32, zero=True)
+    plan = K.Gemm(x.desc, w.desc, c.desc, b.desc)
+    assert "mfma_s8" in plan.describe(), plan.describe()
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc, b.device())
+    torch.cuda.synchronize()
+    ref = c.clone_empty()
+    O.gemm(x.t, w.t, ref, b.t)
+    compare(from_device(dc, O.S32), ref.buf, O.S32, plan.describe())
+    assert np.abs(ref.buf.astype(np.int64)).max() > (1 << 24)
+
+
+@pytest.mark.parametrize("cdt", [O.S32, O.S8, O.U8])
+def test_fallback_random_floats(cdt):
+    # non-integer f32 operands: the GPU and the oracle sum in different orders, so an output may differ by one where
+    # the f32 value lies within rounding of a .5 boundary; every other element is bit-exact
+    M, N, Kd = 160, 200, 256
+    scale = {O.S32: 3e3, O.S8: 300.0, O.U8: 600.0}[cdt]  # sums of about scale / 3 (saturating s8 and u8)
+    x = Case([M, Kd], O.F32, seed=420, lo=-1.0, hi=1.0)
+    w = Case([Kd, N], O.F32, "BA", seed=421, lo=-scale / 16, hi=scale / 16)
+    c = Case([M, N], cdt, zero=True)
+    plan = K.Gemm(x.desc, w.desc, c.desc)
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc)
+    torch.cuda.synchronize()
+    ref = c.clone_empty()
+    O.gemm(x.t, w.t, ref)
+    f = O.empty(c.t.dims, c.t.strides, O.F32)
+    O.gemm(x.t, w.t, f)
+    got = from_device(dc, cdt).astype(np.int64)
+    want = ref.buf.astype(np.int64)
+    bad = np.nonzero(got != want)[0]
+    v = f.buf.astype(np.float64)[bad]
+    # f32 summation error grows with the terms, not with the result: allow 32 f32 ulps of sum |x_k w_k| (the
+    # worst-case bound is K = 256 of them)
+    mag = (np.abs(x.t.logical().astype(np.float64)) @ np.abs(w.t.logical().astype(np.float64))).reshape(-1)[bad]
+    near_tie = np.abs(np.abs(v - np.floor(v)) - 0.5) <= 32 * 2.0 ** -24 * mag
+    assert np.all(np.abs(got[bad] - want[bad]) == 1) and np.all(near_tie), (
+        f"{bad.size} differences, unexplained at {bad[~near_tie][:5]}: f32 {v[~near_tie][:5]}")
+    print(f"{cdt}: {bad.size} of {got.size} outputs one step apart at a .5 boundary")
+    lo, hi = {O.S32: (-2147483648, 2147483647), O.S8: (-128, 127), O.U8: (0, 255)}[cdt]
+    if cdt != O.S32:
+        assert np.any(want == lo) and np.any(want == hi)
+
+
+@pytest.mark.parametrize("cdt", [O.S32, O.S8, O.U8])
+def test_integer_conversion_special_values(cdt):
+    # [n, 1] x [1, 1] -> the conversion of each f32 value alone: the saturation bounds, .5 ties, +-2^31 and non-finite
+    # values, bit-exact against the oracle (whose conversion is pinned on the CPU)
+    vals = np.array([np.nan, np.inf, -np.inf, -0.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, 127.5, 128.5, 254.5, 255.5,
+                     256.5, -127.5, -128.5, -129.5, 8388607.5, 16777216.0, 2.0 ** 31, -(2.0 ** 31), 2147483520.0,
+                     -2147483520.0, 3e9, -3e9, 1e38, -1e38, 0.49999997, 1.0000001, 300.25, -300.75], dtype=np.float32)
+    n = vals.size
+    x = Case([n, 1], O.F32, zero=True)
+    x.t.buf[:] = vals
+    w = Case([1, 1], O.F32, zero=True)
+    w.t.buf[:] = 1.0
+    c = Case([n, 1], cdt, zero=True)
+    plan = K.Gemm(x.desc, w.desc, c.desc)
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc)
+    torch.cuda.synchronize()
+    ref = c.clone_empty()
+    O.gemm(x.t, w.t, ref)
+    compare(from_device(dc, cdt), ref.buf, cdt, plan.describe())
