@@ -29,6 +29,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import platform
 import sys
 import time
 from pathlib import Path
@@ -123,6 +124,30 @@ def time_launches(fn, steps, warmup, torch, stream, prewarm_ms=0.0):
     return start.elapsed_time(end) / steps, wall / steps * 1e3
 
 
+def time_graph(run_on, n, replays, torch):
+    """Milliseconds per step of n steps captured in one HIP graph and replayed `replays` times on a side stream (the
+    device's time per step without the host's launch cost). run_on(stream, i) issues step i on `stream`; it is warmed
+    on that stream first, so nothing is allocated during capture."""
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        for i in range(n):
+            run_on(s, i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for i in range(n):
+                run_on(s, i)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(replays):
+            g.replay()
+        e1.record(s)
+        torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (n * replays)
+
+
 def bench_c3(args, torch, K):
     M, Kd, N = 4096, 4096, 11008
     dev = "cuda"
@@ -177,10 +202,13 @@ def bench_decode(args, torch, K, N, M=1):
 
     steps = max(args.steps, 4 * copies)
     ms, ms_wall = time_launches(step, steps, max(args.warmup, copies), torch, stream, args.prewarm_ms)
+    ms_graph = time_graph(lambda s, i: plan.run(x, ws[i % copies], y, None, m2, stream=s), 4 * copies, 10, torch)
     alg_bytes = 2 * (N * Kd + M * Kd + 2 * M * N)
     gbs = alg_bytes / (ms * 1e-3) / 1e9
+    gbs_graph = alg_bytes / (ms_graph * 1e-3) / 1e9
     return {"N": N, "M": M, "K": Kd, "plan": plan.describe(), "us": ms * 1e3, "us_wall": ms_wall * 1e3,
-            "GB/s": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "weight_copies": copies, "alg_bytes": alg_bytes}
+            "GB/s": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "us_graph": ms_graph * 1e3, "frac_hbm_graph": gbs_graph / PEAK_HBM_GBS,
+            "weight_copies": copies, "alg_bytes": alg_bytes}
 
 
 def bench_config(args, torch, K, name):
@@ -220,8 +248,11 @@ def bench_config(args, torch, K, name):
     flops = 2.0 * M * N * Kd
     tflops = flops / (ms * 1e-3) / 1e12
     peak = PEAK_F32_TFLOPS if dt == torch.float32 else PEAK_BF16_TFLOPS
-    return {"config": name, "M": M, "K": Kd, "N": N, "plan": plan.describe(), "us": ms * 1e3, "TFLOP/s": tflops,
-            "frac_peak": tflops / peak, "input_copies": copies}
+    out = {"config": name, "M": M, "K": Kd, "N": N, "plan": plan.describe(), "us": ms * 1e3, "TFLOP/s": tflops,
+           "frac_peak": tflops / peak, "input_copies": copies}
+    if name == "C1":  # a latency-bound call: also its time per step with the launches captured in a graph
+        out["us_graph"] = time_graph(lambda s, i: plan.run(xs[0], ws[0], y, bias, stream=s), 50, 20, torch) * 1e3
+    return out
 
 
 def bench_c3_dtype(args, torch, K, name):
@@ -260,8 +291,50 @@ def bench_c3_dtype(args, torch, K, name):
             "frac_peak": rate / peak}
 
 
+def cpu_model():
+    """The host CPU's model name (as lscpu prints it), from /proc/cpuinfo."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_rate(np, O, dt, M, N, Kd, act, act_alpha, threads, seconds, resid=None, bias_scale=0.0, w_scale=0.02):
+    """TFLOP/s of the reference tests' naive Linear loop (f32 accumulation, OpenMP over rows) on a row sample of an
+    M x K x N problem, grown until it takes about `seconds`; resid "mul" multiplies a [rows, N] operand in (C4).
+    O is the oracle module (the timed CPU loop lives there). Returns (TFLOP/s, rows, seconds)."""
+    rng = np.random.default_rng(0)
+    f32 = dt == O.F32
+    conv = (lambda a: a.astype(np.float32)) if f32 else (lambda a: O.from_f32_rne(a.astype(np.float32), O.BF16))
+    w = conv(rng.standard_normal((N, Kd), dtype=np.float32) * w_scale)
+    bias = conv(rng.standard_normal(N, dtype=np.float32) * bias_scale)
+
+    def run(rows):
+        x = conv(rng.standard_normal((rows, Kd), dtype=np.float32))
+        r = conv(rng.uniform(0.5, 1.5, (rows, N)).astype(np.float32)) if resid else None
+        y = np.zeros(rows * N, dtype=np.float32 if f32 else np.uint16)
+        t0 = time.perf_counter()
+        O.cpu_baseline(dt, rows, N, Kd, x, w, bias, r, y, act, act_alpha, threads, r_mul=resid == "mul")
+        return time.perf_counter() - t0
+
+    rows = min(M, 8)
+    t = run(rows)
+    if t < seconds and rows < M:  # cost is linear in rows
+        rows = int(min(M, max(rows, rows * seconds / max(t, 1e-3))))
+        t = run(rows)
+    reps = 1
+    if t < seconds / 2:  # the whole problem is short: repeat it
+        reps = int(min(10000, seconds / max(t, 1e-4)))
+        t = sum(run(rows) for _ in range(reps)) / reps
+    return 2.0 * rows * N * Kd / t / 1e12, rows, t, reps
+
+
 def cpu_baseline(args, np):
-    """The reference tests' naive Linear loop (f32 accumulation, OpenMP over rows) on a row sample of C3."""
+    """The reference tests' naive Linear loop (f32 accumulation, OpenMP over rows) on a row sample of C3, and the same
+    loop on every other configuration (C1 also on one thread)."""
     import oracle as O
 
     M, Kd, N = 4096, 4096, 11008
@@ -284,11 +357,30 @@ def cpu_baseline(args, np):
         rows = int(min(M, max(rows, rows * args.cpu_seconds / max(dt, 1e-3))))
         dt = run(rows)
     tflops = 2.0 * rows * N * Kd / dt / 1e12
-    return {"value": tflops, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+
+    # the other configurations, each on a sample of about a quarter of cpu_seconds
+    share = args.cpu_seconds / 4
+    per = []
+    for name, dtp, m, n, k, act, alpha, resid, bs, ws, thr in (
+            ("C1", O.F32, 128, 1024, 1024, O.ACT_RELU, 0.0, None, 0.1, 1.0, threads),
+            ("C1 (1 thread)", O.F32, 128, 1024, 1024, O.ACT_RELU, 0.0, None, 0.1, 1.0, 1),
+            ("C2", O.F32, 2048, 4096, 4096, O.ACT_SWISH, 1.0, None, 0.02, 1.0 / 64, threads),
+            ("C4 M=1 N=4096", O.BF16, 1, 4096, 4096, O.ACT_NONE, 0.0, "mul", 0.0, 0.02, threads),
+            ("C4 M=16 N=14336", O.BF16, 16, 14336, 4096, O.ACT_NONE, 0.0, "mul", 0.0, 0.02, threads),
+            ("C5 (one batch of 8)", O.BF16, 2048, 13824, 5120, O.ACT_SWISH, 1.0, None, 0.02, 0.014, threads)):
+        rate, r, t, reps = cpu_rate(np, O, dtp, m, n, k, act, alpha, thr, share, resid, bs, ws)
+        e = {"config": name, "TFLOP/s": round(rate, 6), "threads": thr, "rows": r, "of_rows": m,
+             "seconds_per_run": round(t, 4), "runs": reps}
+        if resid == "mul":  # decode: the bandwidth metric (bf16 weight, X, M2 and Y bytes of the sampled rows)
+            e["GB/s"] = round(2.0 * (n * k + r * k + 2 * r * n) / t / 1e9, 3)
+        per.append(e)
+    return {"value": tflops, "unit": "TFLOP/s", "cores": threads, "kind": "port", "cpu_model": cpu_model(),
             "sample": f"{rows} of {M} rows of C3 (bf16 Linear+GELU_tanh+residual, K={Kd}, N={N}); naive f32-accumulate "
                       f"loop of the reference gtest oracle, OpenMP over rows, {dt:.1f} s; the aarch64 SVE/KML path "
                       f"cannot build on this x86 host",
-            "seconds": dt}
+            "seconds": dt, "per_config": per,
+            "per_config_note": "the same loop on a row sample of each configuration (C4: whole problem, times the "
+                               "multiplier M2; C5: one batch, weight read as [N][K])"}
 
 
 def bench_dispatch(args, torch, K):

@@ -84,8 +84,8 @@ def lib() -> ctypes.CDLL:
                                       ctypes.c_int),
             "oracle_fill": ([P, ctypes.c_int, ctypes.c_int64, ctypes.c_uint64, ctypes.c_int, ctypes.c_double,
                              ctypes.c_double], ctypes.c_int),
-            "oracle_cpu_baseline": ([ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, P, P, P, P, P,
-                                     ctypes.c_int, ctypes.c_float, ctypes.c_int], ctypes.c_int),
+            "oracle_cpu_baseline": ([ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, P, P, P, P,
+                                     ctypes.c_int, P, ctypes.c_int, ctypes.c_float, ctypes.c_int], ctypes.c_int),
             "oracle_max_threads": ([], ctypes.c_int),
         }
         for name, (args, res) in sig.items():
@@ -262,11 +262,12 @@ def act_f32(kind: int, x: float, alpha: float = 0.0, beta: float = 0.0) -> float
     return lib().oracle_act_f32(kind, x, alpha, beta)
 
 
-def cpu_baseline(dt, M, N, K, X, W, bias, R, Y, act, act_alpha, threads) -> None:
-    """The reference tests' naive loop (f32 accumulation), OpenMP over rows; X[M][K], W[N][K], Y[M][N]."""
+def cpu_baseline(dt, M, N, K, X, W, bias, R, Y, act, act_alpha, threads, r_mul=False) -> None:
+    """The reference tests' naive loop (f32 accumulation), OpenMP over rows; X[M][K], W[N][K], Y[M][N]; R (optional)
+    added to, or with r_mul multiplied into, the activated result."""
     ptr = lambda t: None if t is None else t.ctypes.data
-    assert lib().oracle_cpu_baseline(dt, M, N, K, ptr(X), ptr(W), ptr(bias), ptr(R), ptr(Y), act, act_alpha,
-                                     threads) == 0
+    assert lib().oracle_cpu_baseline(dt, M, N, K, ptr(X), ptr(W), ptr(bias), ptr(R), int(r_mul), ptr(Y), act,
+                                     act_alpha, threads) == 0
 
 
 def max_threads() -> int:

@@ -701,7 +701,7 @@ int oracle_fill(void *p, int dtype, int64_t n, uint64_t seed, int dist, double l
  * optional residual add, parallelised over output rows as MatmulRef does (matmul_gtest.cpp:112). Used only
  * as the reported CPU baseline. */
 int oracle_cpu_baseline(int dtype, int64_t M, int64_t N, int64_t K, const void *X, const void *W, const void *bias,
-                        const void *R, void *Y, int act, float act_alpha, int threads)
+                        const void *R, int r_mul, void *Y, int act, float act_alpha, int threads)
 {
 #ifdef _OPENMP
     if (threads > 0) {
@@ -733,12 +733,14 @@ int oracle_cpu_baseline(int dtype, int64_t M, int64_t N, int64_t K, const void *
             if (dtype == O_BF16) {
                 v = oracle_bf16_to_f32(oracle_f32_to_bf16_rne(v));
             }
-            v = oracle_act_f32(act, v, act_alpha, 0.0f);
-            if (dtype == O_BF16) {
-                v = oracle_bf16_to_f32(oracle_f32_to_bf16_trunc(v));
+            if (act != O_ACT_NONE) {
+                v = oracle_act_f32(act, v, act_alpha, 0.0f);
+                if (dtype == O_BF16) {
+                    v = oracle_bf16_to_f32(oracle_f32_to_bf16_trunc(v));
+                }
             }
             if (R) {
-                v = v + ld(R, dtype, i * N + j);
+                v = r_mul ? v * ld(R, dtype, i * N + j) : v + ld(R, dtype, i * N + j);
             }
             st(Y, dtype, i * N + j, v);
         }

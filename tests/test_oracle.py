@@ -439,3 +439,20 @@ def test_cpu_baseline_matches_oracle():
                      O.Tensor((M, N), (N, 1), BF16, R))
     d = np.abs(O.to_f32(Y, BF16) - O.to_f32(y.buf, BF16))
     assert np.mean(d == 0) > 0.95 and d.max() <= 0.02
+
+
+def test_cpu_baseline_residual_mul_matches_oracle():
+    """The timed loop's multiplier form (C4: Y = (X W^T) * M2) against the oracle's BIN_MUL post-op."""
+    rng = np.random.default_rng(12)
+    M, K, N = 3, 96, 40
+    X = O.from_f32_rne(rng.standard_normal((M, K)).astype(np.float32), BF16)
+    W = O.from_f32_rne((rng.standard_normal((N, K)) * 0.05).astype(np.float32), BF16)
+    R = O.from_f32_rne(rng.uniform(0.5, 1.5, (M, N)).astype(np.float32), BF16)
+    Y = np.zeros(M * N, np.uint16)
+    O.cpu_baseline(BF16, M, N, K, X, W, None, R, Y, O.ACT_NONE, 0.0, 1, r_mul=True)
+    a = O.Tensor((M, K), (K, 1), BF16, X)
+    b = O.Tensor((K, N), (1, K), BF16, W)
+    y = O.empty((M, N), (N, 1), BF16)
+    O.linear_postops(a, b, y, None, O.ACT_NONE, 0.0, O.BIN_MUL, O.Tensor((M, N), (N, 1), BF16, R))
+    g, r = O.to_f32(Y, BF16), O.to_f32(y.buf, BF16)
+    assert np.max(np.abs(g - r) / np.maximum(np.abs(r), 1e-3)) <= 2 ** -7  # one bf16 ulp of summation-order slack
