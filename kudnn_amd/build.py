@@ -25,7 +25,7 @@ BUILD = PKG / "_build"
 INCLUDE = ROOT / "include"
 
 ARCH = os.environ.get("KUDNN_OFFLOAD_ARCH", "gfx950")
-HIP_SOURCES = ["gemm_mfma.hip", "gemm_pingpong.hip", "skinny_bf16.hip", "pack.hip", "capi.cpp"]
+HIP_SOURCES = ["gemm_mfma.hip", "gemm_pingpong.hip", "gemm_kslice.hip", "skinny_bf16.hip", "pack.hip", "capi.cpp"]
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",

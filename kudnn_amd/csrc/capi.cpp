@@ -563,6 +563,16 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
         core.engine = ENGINE_MFMA_F32;
         int64_t t128 = (core.M + 127) / 128 * ((core.N + 127) / 128) * batches;
         core.cfg = t128 >= 256 ? KUDNN_CFG_F32_128x128 : KUDNN_CFG_F32_64x64;
+        // A grid of fewer than 128 tiles of 64 x 64 (which the 64 x 64 kernel would split along K across workgroups)
+        // that still makes at least 128 tiles of 16 x 32: one tile per workgroup, K split over its waves. Measured on
+        // MI355X it wins up to K = 4096 (C1, 128 x 1024 x 1024: 8.5 against 12.5 us) and for M <= 16 at any K; beyond,
+        // its 16 x 32 tiles read more operand bytes per FLOP than the split 64 x 64 tiles (128 x 1024 x 16384: 86
+        // against 68 us).
+        const int64_t t64 = (core.M + 63) / 64 * ((core.N + 63) / 64) * batches;
+        const int64_t tks = (core.M + 15) / 16 * ((core.N + 31) / 32) * batches;
+        if (t64 < KUDNN_SPLIT_MAX_TILES && tks >= 128 && (core.kp <= 4096 || core.M <= 16)) {
+            core.cfg = KUDNN_CFG_F32_KSLICE_16x32;
+        }
     }
     if (const char *force = std::getenv("KUDNN_HIP_FORCE_CFG")) {
         int f = std::atoi(force);
@@ -573,7 +583,8 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
                       (((f == KUDNN_CFG_BF16_256x256 || f == KUDNN_CFG_BF16_256x128 || f == KUDNN_CFG_BF16_128x128 ||
                          f == KUDNN_CFG_BF16_PINGPONG_256x256) && mfmaOk) ||
                        (f == KUDNN_CFG_SKINNY_BF16 && core.M <= 16 && lowp16));
-        bool okF32 = core.computeDt == KUDNN_DT_F32 && (f == KUDNN_CFG_F32_128x128 || f == KUDNN_CFG_F32_64x64);
+        bool okF32 = core.computeDt == KUDNN_DT_F32 &&
+                     (f == KUDNN_CFG_F32_128x128 || f == KUDNN_CFG_F32_64x64 || f == KUDNN_CFG_F32_KSLICE_16x32);
         if (okBf16 || okF32) {
             core.cfg = f;
             core.engine = f == KUDNN_CFG_SKINNY_BF16 ? ENGINE_SKINNY_BF16
@@ -592,6 +603,7 @@ const char *CfgName(int cfg)
         case KUDNN_CFG_BF16_PINGPONG_256x256: return "mfma_bf16_pingpong_256x256";
         case KUDNN_CFG_F32_128x128: return "mfma_f32_128x128";
         case KUDNN_CFG_F32_64x64: return "mfma_f32_64x64";
+        case KUDNN_CFG_F32_KSLICE_16x32: return "mfma_f32_kslice_16x32";
         case KUDNN_CFG_SKINNY_BF16: return "skinny_bf16_16xK";
         case KUDNN_CFG_GEMV_BF16: return "skinny_bf16_gemv_row";
         default: return "unknown";
@@ -1004,8 +1016,13 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
             const int cfg = core.cfg == KUDNN_CFG_BF16_PINGPONG_256x256 ? KUDNN_CFG_BF16_256x256 : core.cfg;
             lrc = kudnn_launch_gemm_mfma(op, ep, batches, cfg, core.computeDt, splitWs, counters, stream);
         }
+    } else if (core.cfg == KUDNN_CFG_F32_KSLICE_16x32 && kudnn_kslice_eligible(op)) {
+        lrc = kudnn_launch_gemm_f32_kslice(op, ep, batches, stream);
     } else {
-        lrc = kudnn_launch_gemm_f32(op, ep, batches, core.cfg, splitWs, counters, stream);
+        // (an operand the k-slice kernel cannot address runs on the 64 x 64 kernel, unsplit: no workspace was reserved)
+        const int cfg = core.cfg == KUDNN_CFG_F32_KSLICE_16x32 ? KUDNN_CFG_F32_64x64 : core.cfg;
+        lrc = kudnn_launch_gemm_f32(op, ep, batches, cfg, cfg == core.cfg ? splitWs : nullptr,
+                                    cfg == core.cfg ? counters : nullptr, stream);
     }
     hipError_t le = hipGetLastError();
     if (lrc != 0 || le != hipSuccess) {

@@ -14,6 +14,7 @@ enum {
     KUDNN_CFG_BF16_PINGPONG_256x256 = 4,
     KUDNN_CFG_F32_128x128 = 10,
     KUDNN_CFG_F32_64x64 = 11,
+    KUDNN_CFG_F32_KSLICE_16x32 = 12,  // small f32 grids: 16 x 32 tiles, K split over the waves of the workgroup
     KUDNN_CFG_SKINNY_BF16 = 20,
     KUDNN_CFG_GEMV_BF16 = 21,  // M == 1: one wave per weight row (skinny engine)
 };
@@ -42,6 +43,10 @@ int kudnn_launch_gemm_pingpong(const GemmOperands &op, const EpiParams &ep, int6
                                hipStream_t stream);
 int kudnn_launch_gemm_f32(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, void *ws,
                           uint32_t *counters, hipStream_t stream);
+// f32, one 16 x 32 tile per workgroup with K split over its waves (gemm_kslice.hip): no workspace. Needs K a multiple
+// of 16, 16-byte aligned operands and row strides; kudnn_kslice_eligible says whether `op` qualifies.
+bool kudnn_kslice_eligible(const GemmOperands &op);
+int kudnn_launch_gemm_f32_kslice(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream);
 // M <= 16, bf16 or f16 operands (`ct`), B contiguous along K (M == 1: row-per-wave GEMV, otherwise 16-row MFMA tiles).
 int kudnn_launch_skinny(const GemmOperands &op, const EpiParams &ep, int64_t batches, int ct, hipStream_t stream);
 

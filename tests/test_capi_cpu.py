@@ -185,7 +185,8 @@ def test_dispatcher_choices():
             assert plan_of(M, 4096, N).describe().startswith("skinny_bf16")
     assert plan_of(17, 4096, 4096).describe().startswith("mfma_bf16")
     assert plan_of(2048, 4096, 4096, K.F32).describe().startswith("mfma_f32_128x128")
-    assert plan_of(128, 1024, 1024, K.F32).describe().startswith("mfma_f32_64x64")
+    assert plan_of(128, 1024, 1024, K.F32).describe().startswith("mfma_f32_kslice_16x32")
+    assert plan_of(100, 2048, 200, K.F32).describe().startswith("mfma_f32_64x64")  # 49 tiles of 16 x 32: split-K
     # C5: 3-D input with a batch-broadcast K-major weight folds into one M=16384 GEMM
     p = K.LinearActivation(K.desc([8, 2048, 5120], K.BF16, "ABC"), K.desc([1, 5120, 13824], K.BF16, "ABC"),
                            K.desc([8, 2048, 13824], K.BF16, "ABC"), K.desc([1, 1, 13824], K.BF16, "ABC"), 1.0, 0.0,

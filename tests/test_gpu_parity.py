@@ -161,7 +161,49 @@ def test_c1_fp32_relu_full():
     torch.cuda.synchronize()
     ref = c.clone_empty()
     O.linear_act(x.t, w.t, ref, b.t, O.ACT_RELU, 0.0)
+    assert "kslice" in plan.describe(), plan.describe()
     compare(from_device(dc, O.F32), ref.buf, O.F32, "C1")
+
+
+@pytest.mark.parametrize("dims", [(128, 1024, 1024), (100, 1000, 520), (1, 4096, 256), (37, 3000, 96), (16, 6000, 48),
+                                  (250, 260, 2048)])
+@pytest.mark.parametrize("bias", [None, "1N", "MN"])
+def test_f32_kslice_shapes(dims, bias):
+    # the k-slice kernel (one 16 x 32 tile per workgroup, K over its waves): ragged M and N, K tails the pack pads,
+    # every bias kind, beta != 0
+    M, N, Kd = dims
+    x = Case([M, Kd], O.F32, seed=60)
+    w = Case([Kd, N], O.F32, "BA", seed=61)
+    bd = {"1N": [1, N], "MN": [M, N]}.get(bias)
+    b = Case(bd, O.F32, seed=62) if bd else None
+    c = Case([M, N], O.F32, seed=63)
+    plan = K.Gemm(x.desc, w.desc, c.desc, b.desc if b else None)
+    assert "kslice" in plan.describe(), plan.describe()
+    dc = c.device()
+    plan.run(x.device(), w.device(), dc, b.device() if b else None, alpha=0.75, beta=0.5)
+    torch.cuda.synchronize()
+    ref = O.Tensor(c.t.dims, c.t.strides, O.F32, c.t.buf.copy())
+    O.gemm(x.t, w.t, ref, b.t if b else None, alpha=0.75, beta=0.5)
+    compare(from_device(dc, O.F32), ref.buf, O.F32, plan.describe())
+
+
+def test_f32_kslice_batched_and_repeatable():
+    # batches in grid.y (a weight per batch); two runs give the same bits
+    x = Case([3, 2, 40, 264], O.F32, seed=64)
+    w = Case([3, 2, 264, 700], O.F32, seed=65)
+    c = Case([3, 2, 40, 700], O.F32, zero=True)
+    plan = K.LinearActivation(x.desc, w.desc, c.desc, None, 1.0, 0.0, K.ACT_SWISH)
+    assert "kslice" in plan.describe(), plan.describe()
+    outs = []
+    for _ in range(2):
+        dc = zeros_device(c)
+        plan.run(x.device(), w.device(), dc)
+        torch.cuda.synchronize()
+        outs.append(from_device(dc, O.F32))
+    assert np.array_equal(outs[0], outs[1])
+    ref = c.clone_empty()
+    O.linear_act(x.t, w.t, ref, None, O.ACT_SWISH, 1.0)
+    compare(outs[0], ref.buf, O.F32, plan.describe())
 
 
 def test_c2_fp32_silu_rows():
@@ -362,9 +404,12 @@ def test_m1_row_gemv_batched_broadcast_weight():
 @pytest.mark.parametrize("dt", [O.F32, O.BF16])
 @pytest.mark.parametrize("mnk", [(128, 1024, 1024), (100, 200, 2048), (64, 70, 512)])
 @pytest.mark.parametrize("post", ["gelu_add", "swish_mul", "gemm_beta"])
-def test_split_k_small_grids(dt, mnk, post):
+def test_split_k_small_grids(monkeypatch, dt, mnk, post):
     # grids of fewer than 128 tiles with at least 8 k-tiles run split along K: raw f32 partials in the plan's
-    # workspace, then one pass that sums them in split order and applies the whole epilogue
+    # workspace, then one pass that sums them in split order and applies the whole epilogue (f32 forced onto the
+    # 64 x 64 kernel, which the planner gives to the k-slice kernel where that one makes 128 tiles or more)
+    if dt == O.F32:
+        monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "11")
     M, N, Kd = mnk
     x = Case([M, Kd], dt, seed=220, dist="normal", lo=0.0, hi=1.0)
     w = Case([Kd, N], dt, "BA", seed=221, dist="normal", lo=0.0, hi=1.0 / 32)
@@ -388,8 +433,9 @@ def test_split_k_small_grids(dt, mnk, post):
     compare(from_device(dy, dt), ref.buf, dt, f"split-K {post} {plan.describe()}", explain=why)
 
 
-def test_plan_workspace_across_streams():
+def test_plan_workspace_across_streams(monkeypatch):
     # one plan with a workspace (split-K) run alternately on two streams: the workspace is ordered between them
+    monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "11")  # the 64 x 64 kernel, split along K
     M, N, Kd = 128, 1024, 1024
     dt = O.F32
     xs = [Case([M, Kd], dt, seed=230 + i, dist="normal", lo=0.0, hi=1.0) for i in range(4)]
