@@ -338,6 +338,7 @@ struct OperandSpec {
     int64_t s_k = 0;       // stride along k
     int64_t bs[3] = {0, 0, 0};
     bool staticPack = false;  // must be packed whatever the pointer alignment
+    bool kmajor = false;      // B read in place as [K][N] (N contiguous) by the ping-pong kernel
 };
 
 struct TensorSpec {
@@ -591,6 +592,17 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
                                                      : (okF32 ? ENGINE_MFMA_F32 : ENGINE_MFMA_BF16);
         }
     }
+    // A K-major weight (B stored [K][N], N contiguous: C5's W{1,K,N} ABC) is read in place by the ping-pong kernel,
+    // through transposing LDS reads, instead of being packed on every run; it needs whole 256-column tiles and
+    // 64-deep k-tiles, 16-byte aligned k-rows and batches, and 32-bit offsets.
+    const bool bBatchAligned = core.B.bs[0] % 8 == 0 && core.B.bs[1] % 8 == 0 && core.B.bs[2] % 8 == 0;
+    if (core.engine == ENGINE_MFMA_BF16 && core.cfg == KUDNN_CFG_BF16_PINGPONG_256x256 &&
+        (core.computeDt == KUDNN_DT_BF16 || core.computeDt == KUDNN_DT_F16) && core.B.dt == core.computeDt &&
+        core.B.s_r == 1 && core.B.s_k >= core.N && core.B.s_k % 8 == 0 && bBatchAligned && core.K % 64 == 0 &&
+        core.N % 256 == 0 && core.K * core.B.s_k * 2 < (int64_t(1) << 31) && !std::getenv("KUDNN_HIP_PACK_KMAJOR")) {
+        core.B.kmajor = true;
+        core.B.staticPack = false;
+    }
     return KUDNN_STATUS_SUCCESS;
 }
 
@@ -635,7 +647,8 @@ std::string DescribeCore(const GemmCore &c)
     char buf[320];
     std::snprintf(buf, sizeof(buf), "%s M=%lld N=%lld K=%lld batches=%lld%s%s%s%s", cfg.c_str(),
                   static_cast<long long>(c.M), static_cast<long long>(c.N), static_cast<long long>(c.K),
-                  static_cast<long long>(c.Batches()), c.A.staticPack ? " packA" : "", c.B.staticPack ? " packB" : "",
+                  static_cast<long long>(c.Batches()), c.A.staticPack ? " packA" : "",
+                  c.B.staticPack ? " packB" : (c.B.kmajor ? " kmajorB" : ""),
                   c.serial ? " serial" : "", split);
     return buf;
 }
@@ -831,7 +844,7 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
                             int64_t &ld, int64_t outBs[3]) -> int {
         if (!pack) {
             outPtr = ptr;
-            ld = o.s_r;
+            ld = o.kmajor ? o.s_k : o.s_r;  // a K-major B is addressed by its k-row pitch
             for (int s = 0; s < 3; ++s) outBs[s] = o.bs[s];
             return 0;
         }
@@ -912,6 +925,7 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
     int rc = setupOperand(core.A, a, packA, ws, op.a, op.lda, op.a_bs);
     if (rc == 0) {
         rc = setupOperand(core.B, b, packB, static_cast<char *>(ws) + wsA, op.b, op.ldb, op.b_bs);
+        op.b_kmajor = core.B.kmajor && !packB ? 1 : 0;
     }
     if (rc != 0) {
         return HipFail(hipGetLastError(), "pack launch");
@@ -1010,6 +1024,9 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
     } else if (core.engine == ENGINE_MFMA_BF16) {
         if (core.cfg == KUDNN_CFG_BF16_PINGPONG_256x256 && kudnn_pingpong_eligible(op, core.computeDt)) {
             lrc = kudnn_launch_gemm_pingpong(op, ep, batches, core.computeDt, tailWs, stream);
+        } else if (op.b_kmajor) {
+            // only the ping-pong kernel reads a K-major B (the plan's conditions make it eligible)
+            return Fail(KUDNN_STATUS_UNSUPPORTED, "GEMM: a K-major weight the ping-pong kernel cannot address");
         } else {
             // operands the ping-pong kernel cannot address (e.g. offsets beyond 2 GiB) use the 4-wave kernel
             // (no split-K workspace was reserved for the ping-pong configuration: runs unsplit)

@@ -339,12 +339,23 @@ struct SkArgs {
 
 constexpr int kSlotFloats = kBM * kBN;  // one 256 x 256 accumulator tile
 
+// K-major B (BKM). A weight stored [K][N] (N contiguous, the K-major W{K,N} of a transposed nn.Linear) is read in
+// place instead of packed: a k-tile of B is 64 k-rows of 512 bytes (256 n), copied two rows per 1 KB copy, and held
+// in LDS as [64 k][32 chunks of 16 bytes] with chunk c of row k in slot c ^ (4 * (k % 4)). The MFMA wants 8
+// consecutive k of one n per lane, which ds_read_b64_tr_b16 delivers: within each 16-lane group, address lane
+// a = 4 jj + q reads 4 consecutive n (n0 + 4q .. +3) of row k0 + jj, and output lane i receives element i % 4 of
+// address lane 4 jj + i / 4 for jj = 0..3, that is n0 + i at k0 .. k0 + 3 (measured on gfx950). Two such reads give
+// a lane its 8 k. In a half-wave the four rows sit at four distinct 64-byte offsets modulo 256 bytes, so the reads are
+// free of bank conflicts. Needs N a multiple of 256 and K of 64 (no edge along n or k).
+//
 // CT: operand type, KUDNN_DT_BF16 / F16 / S8. SK: false for the data-parallel launch (block -> one whole tile),
-// true for the tail launch (block -> a range of k-iterations over one or more tiles).
-template <int CT, int ACT, int FORM, bool SK>
+// true for the tail launch (block -> a range of k-iterations over one or more tiles). BKM: B is K-major (bf16 / f16,
+// data-parallel launch only).
+template <int CT, int ACT, int FORM, bool SK, bool BKM = false>
 __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, EpiParams ep, int tilesM, int tilesN,
                                                                int group, SkArgs sk)
 {
+    static_assert(!BKM || (!SK && CT != KUDNN_DT_S8), "K-major B: 16-bit operands, data-parallel launch");
     constexpr uint32_t ES = CT == KUDNN_DT_S8 ? 1u : 2u;  // element size in bytes
     __shared__ uint4 a0[kTile], a1[kTile], b0[kTile], b1[kTile], b2[kTile];
     auto abuf = [&](auto ic) __attribute__((always_inline)) -> uint4 * {
@@ -367,7 +378,9 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
     const uint8_t *A = static_cast<const uint8_t *>(op.a) + (i0 * op.a_bs[0] + i1 * op.a_bs[1] + i2 * op.a_bs[2]) * ES;
     const uint8_t *B = static_cast<const uint8_t *>(op.b) + (i0 * op.b_bs[0] + i1 * op.b_bs[1] + i2 * op.b_bs[2]) * ES;
     const uint32_t lda = static_cast<uint32_t>(op.lda) * ES, ldb = static_cast<uint32_t>(op.ldb) * ES;  // row pitch, bytes
-    const uint32_t bytesA = static_cast<uint32_t>(op.M) * lda, bytesB = static_cast<uint32_t>(op.N) * ldb;
+    // bytes of each operand after its base (K-major B: K rows of ldb bytes)
+    const uint32_t bytesA = static_cast<uint32_t>(op.M) * lda,
+                   bytesB = static_cast<uint32_t>(BKM ? op.K : op.N) * ldb;
     const int KT = static_cast<int>(static_cast<uint32_t>(K) * ES / kRowBytes);
 
     // the data-parallel launch clears the tail launch's arrival counters (the tail runs after it on the stream)
@@ -385,8 +398,13 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
     const int lr = lane >> 3, ls = lane & 7;
     const uint32_t loA0 = lr * lda + static_cast<uint32_t>((ls ^ (lr >> 1)) * 16);
     const uint32_t loA1 = lr * lda + static_cast<uint32_t>((ls ^ (4 + (lr >> 1))) * 16);
-    const uint32_t loB0 = lr * ldb + static_cast<uint32_t>((ls ^ (lr >> 1)) * 16);
-    const uint32_t loB1 = lr * ldb + static_cast<uint32_t>((ls ^ (4 + (lr >> 1))) * 16);
+    // K-major B: a 1 KB copy covers rows 2q, 2q+1 of the k-tile; lane -> row 2q + lane / 32, LDS slot lane % 32,
+    // source chunk slot ^ (4 * (row % 4)), where row % 4 = 2 (q & 1) + lane / 32
+    const uint32_t kmRow = static_cast<uint32_t>(lane >> 5), kmSlot = static_cast<uint32_t>(lane & 31);
+    const uint32_t loB0 = BKM ? kmRow * ldb + ((kmSlot ^ (4u * kmRow)) * 16u)
+                              : lr * ldb + static_cast<uint32_t>((ls ^ (lr >> 1)) * 16);
+    const uint32_t loB1 = BKM ? kmRow * ldb + ((kmSlot ^ (4u * (2u + kmRow))) * 16u)
+                              : lr * ldb + static_cast<uint32_t>((ls ^ (4 + (lr >> 1))) * 16);
     auto copyA = [&](int q, int t, uint4 *dst) __attribute__((always_inline)) {
         const uint32_t off = static_cast<uint32_t>(m0 + q * 8) * lda + static_cast<uint32_t>((kb + t) * kRowBytes);
         if constexpr (SK) {
@@ -396,7 +414,8 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
         }
     };
     auto copyB = [&](int q, int t, uint4 *dst) __attribute__((always_inline)) {
-        const uint32_t off = static_cast<uint32_t>(n0 + q * 8) * ldb + static_cast<uint32_t>((kb + t) * kRowBytes);
+        const uint32_t off = BKM ? static_cast<uint32_t>((kb + t) * 64 + 2 * q) * ldb + static_cast<uint32_t>(n0) * ES
+                                 : static_cast<uint32_t>(n0 + q * 8) * ldb + static_cast<uint32_t>((kb + t) * kRowBytes);
         if constexpr (SK) {
             copy_block(B, bytesB, off, (q & 1) ? loB1 : loB0, dst + q * 8 * kKC);
         } else {
@@ -425,11 +444,33 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
     f32x16_t acc[4][2];
     uint4 fa[4][2], fb[2][4];
 
+    // K-major B: this lane's byte offset in a B tile for its transposed reads of strip j = 0 (strip j: XOR 64 j):
+    // row 8 (lane / 32) + jj, column bytes g * 256 + 64 jj + 16 (2 ((lane / 16) & 1) + (lane & 3) / 2) + 8 (lane & 1)
+    // with jj = (lane & 15) / 4; step s and half h add (16 s + 4 h) rows
+    const uint32_t kmJJ = static_cast<uint32_t>((lane & 15) >> 2);
+    const uint32_t trOff = (8u * static_cast<uint32_t>(lane >> 5) + kmJJ) * 512u + static_cast<uint32_t>(g) * 256u +
+                           64u * kmJJ + 16u * (2u * static_cast<uint32_t>((lane >> 4) & 1) + static_cast<uint32_t>((lane & 3) >> 1)) +
+                           8u * static_cast<uint32_t>(lane & 1);
     auto readB = [&](const uint4 *bt, auto slotc, auto stepc) __attribute__((always_inline)) {
         constexpr int slot = decltype(slotc)::value, s = decltype(stepc)::value;
-        const int sl = (2 * s + lh) ^ fsw;
+        if constexpr (BKM) {
+            typedef short v4i16_t __attribute__((ext_vector_type(4)));
+            typedef __attribute__((address_space(3))) v4i16_t lds_v4i16;
+            typedef __attribute__((address_space(3))) char lds_char;
+            lds_char *base = (lds_char *)(const_cast<uint4 *>(bt));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) fb[slot][j] = bt[offB + j * 32 * kKC + sl];
+            for (int j = 0; j < 4; ++j) {
+                lds_char *pj = base + (trOff ^ static_cast<uint32_t>(64 * j));
+                const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)(pj + (16 * s) * 512));
+                const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)(pj + (16 * s + 4) * 512));
+                const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+                fb[slot][j] = make_uint4(l2.x, l2.y, h2.x, h2.y);
+            }
+        } else {
+            const int sl = (2 * s + lh) ^ fsw;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) fb[slot][j] = bt[offB + j * 32 * kKC + sl];
+        }
     };
     auto step = [&](auto ic, int t, int sR0) __attribute__((always_inline)) {
         constexpr int I = decltype(ic)::value;
@@ -459,7 +500,20 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
                                                                       : ldsOf(std::integral_constant<int, I + 2>{}, 1));
             if (tt < nk) {
                 const uint32_t kofs = static_cast<uint32_t>((kb + tt) * kRowBytes);
-                if (fullTile) {
+                if (BKM && g == 1) {
+                    // K-major B (never at an edge): the k-tile's 64 rows from its first byte at column n0, two rows
+                    // per copy
+                    const uint32_t tileOff = static_cast<uint32_t>((kb + tt) * 64) * sLd +
+                                             static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(n0)) * ES;
+                    const i32x4_rs_t rs = make_rsrc(sX + tileOff, sBytes - tileOff);
+                    asm volatile("s_nop 4" ::: "memory");  // wait states after VALU writes of the SGPRs the copies read
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int q = p * 8 + j;
+                        copy_lds_fast(rs, (q & 1) ? sLo1 : sLo0, static_cast<uint32_t>(q * 2) * sLd,
+                                      dl + static_cast<uint32_t>(q * 8 * kKC * 16));
+                    }
+                } else if (fullTile) {
                     // one resource from the k-tile's first byte: the lane's row and chunk in the vector offset, the
                     // 8-row block in the scalar offset; every word is scalar arithmetic
                     const uint32_t tileOff = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(sR0)) * sLd + kofs;
@@ -711,8 +765,14 @@ __global__ void sk_zero_kernel(uint32_t *cnt, int n)
 
 bool kudnn_pingpong_eligible(const GemmOperands &op, int ct)
 {
-    // whole k-tiles, 16-byte aligned rows, 32-bit buffer offsets
+    // whole k-tiles, 16-byte aligned rows, 32-bit buffer offsets; a K-major B also whole 256-column tiles
     const int64_t es = ct == KUDNN_DT_S8 ? 1 : 2;
+    if (op.b_kmajor) {
+        return (ct == KUDNN_DT_BF16 || ct == KUDNN_DT_F16) && op.K > 0 && op.K % 64 == 0 && op.N % kBN == 0 &&
+               (op.lda * es) % 16 == 0 && (op.ldb * es) % 16 == 0 && op.ldb >= op.N &&
+               op.M * op.lda * es < (int64_t(1) << 31) && op.K * op.ldb * es < (int64_t(1) << 31) &&
+               reinterpret_cast<uintptr_t>(op.b) % 16 == 0;
+    }
     return (ct == KUDNN_DT_BF16 || ct == KUDNN_DT_F16 || ct == KUDNN_DT_S8) && (op.K * es) % kRowBytes == 0 &&
            (op.lda * es) % 16 == 0 && (op.ldb * es) % 16 == 0 && op.M * op.lda * es < (int64_t(1) << 31) &&
            op.N * op.ldb * es < (int64_t(1) << 31) && op.K > 0;
@@ -757,7 +817,7 @@ SkPlan sk_plan(const GemmOperands &op, int64_t batches, int ct)
 {
     SkPlan s;
     const int64_t es = ct == KUDNN_DT_S8 ? 1 : 2;
-    if (batches != 1 || op.K <= 0 || (op.K * es) % kRowBytes != 0) {
+    if (batches != 1 || op.K <= 0 || (op.K * es) % kRowBytes != 0 || op.b_kmajor) {
         return s;
     }
     const char *f = std::getenv("KUDNN_HIP_FORCE_STREAMK");
@@ -797,7 +857,7 @@ SkPlan sk_plan(const GemmOperands &op, int64_t batches, int ct)
 using PingpongKernel = decltype(&gemm_pingpong_kernel<KUDNN_DT_BF16, 0, EPI_FORM_GENERIC, false>);
 
 // The activation and the tensor types of the epilogue select one of the compiled variants.
-template <int CT, bool SK>
+template <int CT, bool SK, bool BKM = false>
 PingpongKernel select_pingpong(const EpiParams &ep)
 {
     PingpongKernel kernel = nullptr;
@@ -810,11 +870,11 @@ PingpongKernel select_pingpong(const EpiParams &ep)
         auto pick = [&](auto formc) {
             constexpr int F = decltype(formc)::value;
             switch (ep.act) {
-                case KUDNN_ACT_UNIMPLEMENTED: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_UNIMPLEMENTED, F, SK>; break;
-                case KUDNN_ACT_RELU: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_RELU, F, SK>; break;
-                case KUDNN_ACT_SWISH: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_SWISH, F, SK>; break;
-                case KUDNN_ACT_GELU_TANH: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_GELU_TANH, F, SK>; break;
-                case KUDNN_ACT_GELU_ERF: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_GELU_ERF, F, SK>; break;
+                case KUDNN_ACT_UNIMPLEMENTED: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_UNIMPLEMENTED, F, SK, BKM>; break;
+                case KUDNN_ACT_RELU: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_RELU, F, SK, BKM>; break;
+                case KUDNN_ACT_SWISH: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_SWISH, F, SK, BKM>; break;
+                case KUDNN_ACT_GELU_TANH: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_GELU_TANH, F, SK, BKM>; break;
+                case KUDNN_ACT_GELU_ERF: kernel = gemm_pingpong_kernel<CT, KUDNN_ACT_GELU_ERF, F, SK, BKM>; break;
                 default: break;
             }
         };
@@ -832,7 +892,7 @@ PingpongKernel select_pingpong(const EpiParams &ep)
         }
         if (kernel == nullptr && form != EPI_FORM_I32) {
             // the other activation kinds, and the other tensor types, read everything at run time
-            kernel = gemm_pingpong_kernel<CT, 0, EPI_FORM_GENERIC, SK>;
+            kernel = gemm_pingpong_kernel<CT, 0, EPI_FORM_GENERIC, SK, BKM>;
         }
     }
     return kernel;
@@ -853,7 +913,12 @@ int launch_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches
         args.L = s.L;
         args.maxc = s.maxc;
     }
-    PingpongKernel dp = select_pingpong<CT, false>(ep);
+    PingpongKernel dp = nullptr;
+    if constexpr (CT != KUDNN_DT_S8) {
+        dp = op.b_kmajor ? select_pingpong<CT, false, true>(ep) : select_pingpong<CT, false>(ep);
+    } else {
+        dp = select_pingpong<CT, false>(ep);
+    }
     PingpongKernel tail = s.nTail > 0 ? select_pingpong<CT, true>(ep) : nullptr;
     if (dp == nullptr || (s.nTail > 0 && tail == nullptr)) {
         return -1;

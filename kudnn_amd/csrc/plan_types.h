@@ -43,13 +43,14 @@ struct EpiParams {
 };
 
 // Operands of the MFMA / skinny kernels: A is [M][K] with row stride lda, B is [N][K] with row stride ldb,
-// both contiguous along K ("K-major"), element type = the kernel's compute type.
+// both contiguous along K, element type = the kernel's compute type (or, with b_kmajor, B is [K][N]).
 struct GemmOperands {
     const void *a;
     const void *b;
     int64_t M, N, K;
     int64_t lda, ldb;
     int64_t a_bs[3], b_bs[3];  // batch strides (elements), same batch dims as EpiParams::bdim
+    int b_kmajor;  // 1: B is stored [K][N] (N contiguous, row pitch ldb along k); only the ping-pong kernel reads it
 };
 
 #endif  // KUDNN_PLAN_TYPES_H

@@ -473,6 +473,46 @@ def test_c5_bf16_3d_silu_kmajor_rows():
     O.linear_act(dense_rows(x.t, rows), as2d(w.t), ref, as2d(b.t), O.ACT_SWISH, 1.0)
     compare(got[rows].reshape(-1), ref.buf, O.BF16, "C5 " + plan.describe())
     assert len(rows) >= B * S // 256
+    # the K-major weight is read in place (transposing LDS reads), not packed
+    assert "kmajorB" in plan.describe() and "packB" not in plan.describe(), plan.describe()
+
+
+def _kmajor_case(dt, lead, M, Kd, N, wlead, act, bias, seed):
+    x = Case(lead + [M, Kd], dt, seed=seed, dist="normal", lo=0.0, hi=1.0)
+    w = Case(wlead + [Kd, N], dt, seed=seed + 1, dist="normal", lo=0.0, hi=0.05)  # standard layout: [K][N]
+    b = Case([1] * len(lead) + [1, N], dt, seed=seed + 2, lo=-0.2, hi=0.2) if bias else None
+    y = Case(lead + [M, N], dt, zero=True)
+    return x, w, b, y
+
+
+@pytest.mark.parametrize("dt", [O.BF16, O.F16])
+@pytest.mark.parametrize("shape", [([], 256, 64, 256, []), ([], 300, 640, 768, []), ([], 1000, 256, 1536, []),
+                                   ([2], 260, 192, 512, [2]), ([3], 128, 128, 256, [1])])
+@pytest.mark.parametrize("act", [K.ACT_UNIMPLEMENTED, K.ACT_SWISH, K.ACT_GELU_TANH])
+def test_kmajor_weight_in_place(monkeypatch, dt, shape, act):
+    # a [K][N] weight read in place by the ping-pong kernel (M edges, batched and broadcast weights, every fixed
+    # epilogue form) against the oracle, and bit for bit against the same plan with the weight packed to [N][K]:
+    # both feed the MFMAs the same k groups in the same order
+    monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "4")
+    lead, M, Kd, N, wlead = shape
+    x, w, b, y = _kmajor_case(dt, lead, M, Kd, N, wlead, act, act != K.ACT_UNIMPLEMENTED, 700)
+    outs = []
+    for packed in (False, True):
+        if packed:
+            monkeypatch.setenv("KUDNN_HIP_PACK_KMAJOR", "1")
+        plan = K.LinearPostOps(x.desc, w.desc, y.desc, b.desc if b else None, act=act, act_alpha=1.0)
+        assert ("packB" in plan.describe()) == packed and ("kmajorB" in plan.describe()) != packed, plan.describe()
+        dy = zeros_device(y)
+        plan.run(x.device(), w.device(), dy, b.device() if b else None)
+        torch.cuda.synchronize()
+        outs.append(from_device(dy, dt))
+    monkeypatch.delenv("KUDNN_HIP_PACK_KMAJOR")
+    assert np.array_equal(outs[0], outs[1]), "in-place and packed K-major weights differ"
+    ref = y.clone_empty()
+    O.linear_postops(x.t, w.t, ref, b.t if b else None, act, 1.0, O.BIN_NONE, None)
+    compare(outs[0], ref.buf, dt, "kmajor " + plan.describe(),
+            explain=explainer(dt, x.t, w.t, b.t if b else None, tuple(y.t.dims[-2:]), act=act, act_alpha=1.0)
+            if not lead and dt == O.BF16 else None)
 
 
 # ---------------------------------------------------------------------------------------------------
