@@ -743,25 +743,21 @@ __device__ __forceinline__ void store16_stream(void *p, uint32_t w0, uint32_t w1
     __builtin_nontemporal_store(v, static_cast<u32x4_t *>(p));
 }
 
-// Epilogue of the 8-column group (m, n .. n+7), all in bounds, operands from epi_prefetch8.
+// Epilogue of 8 consecutive columns of one row, all in bounds: acc are the accumulators, bv the bias values (read
+// only when e.bias is set), src the binary operand's raw bits (epi_prefetch8_src), yp the output's first element.
 template <int ACT, int FORM>
-__device__ __forceinline__ void epi_fast8(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, const float acc[8],
-                                          const Pre8 &pre)
+__device__ __forceinline__ void epi_fast8_core(const EpiParams &e, void *yp, const float acc[8], const Raw8 &src,
+                                               const float bv[8])
 {
     constexpr int DT = form_dt<FORM>();
     float v[8];
-    float bv[8];
-    if (e.bias == nullptr) {
+    if (e.bias != nullptr) {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) bv[q] = 0.0f;
-    } else if (e.bias_sn == 0) {
-#pragma unroll
-        for (int q = 0; q < 8; ++q) bv[q] = u2f(pre.bias.lo.x);
+        for (int q = 0; q < 8; ++q) v[q] = fmaf(acc[q], e.alpha, bv[q]);
     } else {
-        unpack_raw8<FORM>(pre.bias, bv);
-    }
 #pragma unroll
-    for (int q = 0; q < 8; ++q) v[q] = acc[q] * e.alpha + bv[q];
+        for (int q = 0; q < 8; ++q) v[q] = acc[q] * e.alpha;
+    }
     if constexpr (DT == KUDNN_DT_BF16) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) round_bf16_pair(v[2 * q], v[2 * q + 1]);
@@ -775,7 +771,7 @@ __device__ __forceinline__ void epi_fast8(const EpiParams &e, const EpiBatch &ob
     }
     if (e.bin != KUDNN_BINARY_NONE) {
         float sv[8];
-        unpack_raw8<FORM>(pre.src, sv);
+        unpack_raw8<FORM>(src, sv);
         if (e.bin == KUDNN_BINARY_ADD) {
 #pragma unroll
             for (int q = 0; q < 8; ++q) v[q] = v[q] + sv[q];
@@ -787,24 +783,47 @@ __device__ __forceinline__ void epi_fast8(const EpiParams &e, const EpiBatch &ob
             for (int q = 0; q < 8; ++q) v[q] = v[q] * sv[q];
         }
     }
-    const int64_t yi = ob.y + m * e.y_sm + n;
-    if constexpr (FORM == EPI_FORM_BF16) {
-        uint32_t w[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) w[q] = pack_bf16x2_rne(v[2 * q], v[2 * q + 1]);
-        store16_stream(static_cast<uint16_t *>(e.y) + yi, w[0], w[1], w[2], w[3]);
-    } else if constexpr (FORM == EPI_FORM_F16) {
+    if constexpr (FORM == EPI_FORM_BF16 || FORM == EPI_FORM_F16) {
         uint32_t w[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            w[q] = static_cast<uint32_t>(f32_to_f16_rne(v[2 * q])) | (static_cast<uint32_t>(f32_to_f16_rne(v[2 * q + 1])) << 16);
+            if constexpr (FORM == EPI_FORM_BF16) {
+                w[q] = pack_bf16x2_rne(v[2 * q], v[2 * q + 1]);
+            } else {
+                w[q] = static_cast<uint32_t>(f32_to_f16_rne(v[2 * q])) |
+                       (static_cast<uint32_t>(f32_to_f16_rne(v[2 * q + 1])) << 16);
+            }
         }
-        store16_stream(static_cast<uint16_t *>(e.y) + yi, w[0], w[1], w[2], w[3]);
+        store16_stream(yp, w[0], w[1], w[2], w[3]);
     } else {
-        float *yp = static_cast<float *>(e.y) + yi;
-        store16_stream(yp, f2u(v[0]), f2u(v[1]), f2u(v[2]), f2u(v[3]));
-        store16_stream(yp + 4, f2u(v[4]), f2u(v[5]), f2u(v[6]), f2u(v[7]));
+        float *fp = static_cast<float *>(yp);
+        store16_stream(fp, f2u(v[0]), f2u(v[1]), f2u(v[2]), f2u(v[3]));
+        store16_stream(fp + 4, f2u(v[4]), f2u(v[5]), f2u(v[6]), f2u(v[7]));
     }
+}
+
+// The bias values of an 8-column group from epi_prefetch8_bias's raw bits (one value broadcast when the bias has one
+// column).
+template <int FORM>
+__device__ __forceinline__ void epi_bias8(const EpiParams &e, const Raw8 &raw, float bv[8])
+{
+    if (e.bias != nullptr && e.bias_sn == 0) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) bv[q] = u2f(raw.lo.x);
+    } else {
+        unpack_raw8<FORM>(raw, bv);
+    }
+}
+
+// Epilogue of the 8-column group (m, n .. n+7), all in bounds, operands from epi_prefetch8.
+template <int ACT, int FORM>
+__device__ __forceinline__ void epi_fast8(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, const float acc[8],
+                                          const Pre8 &pre)
+{
+    constexpr int ES = form_dt<FORM>() == KUDNN_DT_F32 ? 4 : 2;
+    float bv[8];
+    epi_bias8<FORM>(e, pre.bias, bv);
+    epi_fast8_core<ACT, FORM>(e, static_cast<char *>(e.y) + (ob.y + m * e.y_sm + n) * ES, acc, pre.src, bv);
 }
 
 // Epilogue of one element (m, n) in a fixed form, its bias and binary operand from epi_prefetch1.
@@ -859,6 +878,63 @@ __device__ __forceinline__ void epi_elem(const EpiParams &e, const EpiBatch &ob,
     }
     store_elem(e.y, DT, ob.y + m * e.y_sm + n, v);
 }
+
+// Epilogue for four consecutive columns n..n+3 of row m in a fixed form (EPI_FORM_BF16 or EPI_FORM_F32), with the bias
+// and binary operand of epi_prefetch4; the arithmetic and rounding of epi_apply4_pre. Columns at or past N are skipped.
+template <int ACT, int FORM>
+__device__ __forceinline__ void epi_fixed4(const EpiParams &e, const EpiBatch &ob, int64_t m, int64_t n, int64_t N,
+                                           const float acc[4], const EpiPre4 &pre)
+{
+    static_assert(FORM == EPI_FORM_BF16 || FORM == EPI_FORM_F32, "the prefetched operands are bf16 or f32");
+    constexpr int DT = form_dt<FORM>();
+    if (n + 3 < N && e.fast4) {
+        float v[4];
+        float bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (e.bias != nullptr) {
+            if (e.bias_sn == 0) {
+                const float b0 = load_elem(e.bias, DT, ob.bias + m * e.bias_sm);
+                bv[0] = bv[1] = bv[2] = bv[3] = b0;
+            } else {
+                unpack_pre4(pre.bias16, pre.bias32, DT, bv);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = round_store(DT, acc[q] * e.alpha + bv[q]);
+        if constexpr (ACT != KUDNN_ACT_UNIMPLEMENTED) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = act_round(DT, ACT, act_fixed<ACT>(v[q], e.act_alpha));
+        }
+        if (e.bin != KUDNN_BINARY_NONE) {
+            float sv[4];
+            unpack_pre4(pre.src16, pre.src32, DT, sv);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (e.bin == KUDNN_BINARY_ADD) {
+                    v[q] = v[q] + sv[q];
+                } else if (e.bin == KUDNN_BINARY_EXT) {
+                    v[q] = fmaf(sv[q], e.gamma, v[q]);
+                } else {
+                    v[q] = v[q] * sv[q];
+                }
+            }
+        }
+        const int64_t yi = ob.y + m * e.y_sm + n;
+        if constexpr (FORM == EPI_FORM_BF16) {
+            *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(e.y) + yi) =
+                make_uint2(pack_bf16x2_rne(v[0], v[1]), pack_bf16x2_rne(v[2], v[3]));
+        } else {
+            *reinterpret_cast<float4 *>(static_cast<float *>(e.y) + yi) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+        return;
+    }
+#pragma unroll 1
+    for (int q = 0; q < 4; ++q) {
+        if (n + q < N) {
+            epi_elem<ACT, FORM>(e, ob, m, n + q, acc[q]);
+        }
+    }
+}
+
 
 // Integer epilogue: s8 x s8 -> s32 (cblas_gemm_s8s8s32, src/dnn/src/kudnn_gemm.cpp:243-264, with the bias passed as
 // the C offset for a row / column vector and added afterwards for a full [M, N] bias: the same sum either way).

@@ -194,11 +194,18 @@ __device__ __forceinline__ void epilogue_full(const EpiParams &ep, const EpiBatc
         });
     };
     sfor<AHEAD>([&](auto jc) __attribute__((always_inline)) { fetch(jc); });
+    // the output address of this lane's first group (row mW + rl, column nW + col8); pass ps adds 16 ps rows, strip j
+    // 32 j columns
+    constexpr int64_t ES = FORM == EPI_FORM_F32 ? 4 : 2;
+    char *yLane = static_cast<char *>(ep.y) + (ob.y + (mW + rl) * ep.y_sm + nW + col8) * ES;
+    const int64_t yPass = 16 * ep.y_sm * ES;
     __syncthreads();  // every wave is done with the tile buffers that the staging area reuses
     sfor<4>([&](auto jc) __attribute__((always_inline)) {
         constexpr int j = decltype(jc)::value;
-        const int64_t n = nW + j * 32 + col8;
         stage_strip(acc[j], stage, lrow, lh);
+        // the strip's bias values (one row of them: the same for the four passes)
+        float bv[8];
+        epi_bias8<FORM>(ep, bias[j % AHEAD], bv);
         wave_sync();
         sfor<4>([&](auto pc) __attribute__((always_inline)) {
             constexpr int ps = decltype(pc)::value;
@@ -207,7 +214,7 @@ __device__ __forceinline__ void epilogue_full(const EpiParams &ep, const EpiBatc
             const float4 lo = *reinterpret_cast<const float4 *>(sp);
             const float4 hi = *reinterpret_cast<const float4 *>(sp + 4);
             const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-            epi_fast8<ACT, FORM>(ep, ob, mW + r, n, v, Pre8{src[j % AHEAD][ps], bias[j % AHEAD]});
+            epi_fast8_core<ACT, FORM>(ep, yLane + ps * yPass + j * 32 * ES, v, src[j % AHEAD][ps], bv);
         });
         if constexpr (j + AHEAD < 4) {
             fetch(std::integral_constant<int, j + AHEAD>{});
