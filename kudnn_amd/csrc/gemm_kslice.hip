@@ -32,7 +32,7 @@ constexpr int kAhead = 2;          // chunks per batch of loads (two batches in 
 // epilogue is a long chain of run-time branches whose first pass on each CU misses the instruction cache: for a
 // kernel this short that is a large part of its time, so the common forms are compiled out.
 template <int NW, int ACT, int FORM>
-__global__ __launch_bounds__(NW * 64) void gemm_f32_kslice_kernel(GemmOperands op, EpiParams ep, int tilesN)
+__device__ __forceinline__ void kslice_body(const GemmOperands &op, const EpiParams &ep, int tilesN)
 {
     constexpr int kPer = kTM * kTN / (NW * 64);  // output elements per thread in the epilogue
     static_assert(kPer * NW * 64 == kTM * kTN, "the tile must divide over the threads");
@@ -151,6 +151,56 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32_kslice_kernel(GemmOperands o
     }
 }
 
+// Any call: the whole GemmOperands and EpiParams as arguments.
+template <int NW, int ACT, int FORM>
+__global__ __launch_bounds__(NW * 64) void gemm_f32_kslice_kernel(GemmOperands op, EpiParams ep, int tilesN)
+{
+    kslice_body<NW, ACT, FORM>(op, ep, tilesN);
+}
+
+// A single-batch call in the f32 form: the fields it uses (120 bytes instead of 380). A smaller argument block
+// shortens every launch of this latency-bound kernel.
+struct KsArgs {
+    const void *a, *b, *bias, *src;
+    void *y;
+    int64_t M, N, K, lda, ldb;
+    int64_t bias_sm, bias_sn, src_sm, y_sm;
+    float alpha, gamma, act_alpha;
+    int bin, tilesN;
+};
+
+template <int NW, int ACT>
+__global__ __launch_bounds__(NW * 64) void gemm_f32_kslice_compact_kernel(KsArgs r)
+{
+    GemmOperands op{};
+    op.a = r.a;
+    op.b = r.b;
+    op.M = r.M;
+    op.N = r.N;
+    op.K = r.K;
+    op.lda = r.lda;
+    op.ldb = r.ldb;
+    // the epilogue helpers read an EpiParams: the fields the f32 form uses, the rest zero
+    EpiParams ep{};
+    ep.alpha = r.alpha;
+    ep.gamma = r.gamma;
+    ep.act_alpha = r.act_alpha;
+    ep.act = ACT;
+    ep.bin = r.bin;
+    ep.c_dt = ep.bias_dt = ep.src_dt = ep.y_dt = KUDNN_DT_F32;
+    ep.bias = r.bias;
+    ep.src = r.src;
+    ep.y = r.y;
+    ep.bias_sm = r.bias_sm;
+    ep.bias_sn = r.bias_sn;
+    ep.src_sm = r.src_sm;
+    ep.src_sn = 1;
+    ep.y_sm = r.y_sm;
+    ep.y_sn = 1;
+    ep.bdim[0] = ep.bdim[1] = ep.bdim[2] = 1;
+    kslice_body<NW, ACT, EPI_FORM_F32>(op, ep, r.tilesN);
+}
+
 }  // namespace
 
 bool kudnn_kslice_eligible(const GemmOperands &op)
@@ -170,8 +220,27 @@ int kudnn_launch_gemm_f32_kslice(const GemmOperands &op, const EpiParams &ep, in
     }
     const dim3 grid(static_cast<unsigned>(tilesM * tilesN), static_cast<unsigned>(batches));
     constexpr int NW = 4;
+    const bool f32Form = epi_form(ep, false) == EPI_FORM_F32;
+    if (f32Form && batches == 1 && (ep.bin == KUDNN_BINARY_NONE || ep.src_sn == 1) && ep.y_sn == 1) {
+        decltype(&gemm_f32_kslice_compact_kernel<NW, 0>) ck = nullptr;
+        switch (ep.act) {
+            case KUDNN_ACT_UNIMPLEMENTED: ck = gemm_f32_kslice_compact_kernel<NW, KUDNN_ACT_UNIMPLEMENTED>; break;
+            case KUDNN_ACT_RELU: ck = gemm_f32_kslice_compact_kernel<NW, KUDNN_ACT_RELU>; break;
+            case KUDNN_ACT_SWISH: ck = gemm_f32_kslice_compact_kernel<NW, KUDNN_ACT_SWISH>; break;
+            case KUDNN_ACT_GELU_TANH: ck = gemm_f32_kslice_compact_kernel<NW, KUDNN_ACT_GELU_TANH>; break;
+            case KUDNN_ACT_GELU_ERF: ck = gemm_f32_kslice_compact_kernel<NW, KUDNN_ACT_GELU_ERF>; break;
+            default: break;
+        }
+        if (ck != nullptr) {
+            const KsArgs r{op.a,   op.b,       ep.bias,    ep.src,    ep.y,    op.M,     op.N,     op.K,
+                           op.lda, op.ldb,     ep.bias_sm, ep.bias_sn, ep.src_sm, ep.y_sm, ep.alpha, ep.gamma,
+                           ep.act_alpha, ep.bin, static_cast<int>(tilesN)};
+            hipLaunchKernelGGL(ck, grid, dim3(NW * 64), 0, stream, r);
+            return hipGetLastError() == hipSuccess ? 0 : -1;
+        }
+    }
     decltype(&gemm_f32_kslice_kernel<NW, 0, EPI_FORM_GENERIC>) kernel = gemm_f32_kslice_kernel<NW, 0, EPI_FORM_GENERIC>;
-    if (epi_form(ep, false) == EPI_FORM_F32) {
+    if (f32Form) {
         switch (ep.act) {
             case KUDNN_ACT_UNIMPLEMENTED:
                 kernel = gemm_f32_kslice_kernel<NW, KUDNN_ACT_UNIMPLEMENTED, EPI_FORM_F32>;
