@@ -599,7 +599,8 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
     if (core.engine == ENGINE_MFMA_BF16 && core.cfg == KUDNN_CFG_BF16_PINGPONG_256x256 &&
         (core.computeDt == KUDNN_DT_BF16 || core.computeDt == KUDNN_DT_F16) && core.B.dt == core.computeDt &&
         core.B.s_r == 1 && core.B.s_k >= core.N && core.B.s_k % 8 == 0 && bBatchAligned && core.K % 64 == 0 &&
-        core.N % 256 == 0 && core.K * core.B.s_k * 2 < (int64_t(1) << 31) && !std::getenv("KUDNN_HIP_PACK_KMAJOR")) {
+        core.N % 256 == 0 && core.K * core.B.s_k * 2 < (int64_t(1) << 31) &&
+        core.M * std::max<int64_t>(core.A.s_r, core.kp) * 2 < (int64_t(1) << 31) && !std::getenv("KUDNN_HIP_PACK_KMAJOR")) {
         core.B.kmajor = true;
         core.B.staticPack = false;
     }
