@@ -385,9 +385,11 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
     const uint8_t *A = static_cast<const uint8_t *>(op.a) + (i0 * op.a_bs[0] + i1 * op.a_bs[1] + i2 * op.a_bs[2]) * ES;
     const uint8_t *B = static_cast<const uint8_t *>(op.b) + (i0 * op.b_bs[0] + i1 * op.b_bs[1] + i2 * op.b_bs[2]) * ES;
     const uint32_t lda = static_cast<uint32_t>(op.lda) * ES, ldb = static_cast<uint32_t>(op.ldb) * ES;  // row pitch, bytes
-    // bytes of each operand after its base (K-major B: K rows of ldb bytes)
-    const uint32_t bytesA = static_cast<uint32_t>(op.M) * lda,
-                   bytesB = static_cast<uint32_t>(BKM ? op.K : op.N) * ldb;
+    // bytes of each operand after its base, through the end of its last row (K-major B: K rows of N elements); a row
+    // count of one has a pitch of 0 in the descriptors, so the count times the pitch is not the extent
+    const uint32_t bytesA = static_cast<uint32_t>(op.M - 1) * lda + static_cast<uint32_t>(op.K) * ES,
+                   bytesB = BKM ? static_cast<uint32_t>(op.K - 1) * ldb + static_cast<uint32_t>(op.N) * ES
+                                : static_cast<uint32_t>(op.N - 1) * ldb + static_cast<uint32_t>(op.K) * ES;
     const int KT = static_cast<int>(static_cast<uint32_t>(K) * ES / kRowBytes);
 
     // the data-parallel launch clears the tail launch's arrival counters (the tail runs after it on the stream)
@@ -772,17 +774,20 @@ __global__ void sk_zero_kernel(uint32_t *cnt, int n)
 
 bool kudnn_pingpong_eligible(const GemmOperands &op, int ct)
 {
-    // whole k-tiles, 16-byte aligned rows, 32-bit buffer offsets; a K-major B also whole 256-column tiles
+    // whole k-tiles, 16-byte aligned rows, 32-bit buffer offsets (the offset of the first byte past each operand's
+    // last row, and that of the row after it, which an edge tile's copies compute); a K-major B also whole 256-column
+    // tiles
     const int64_t es = ct == KUDNN_DT_S8 ? 1 : 2;
+    const int64_t lim = int64_t(1) << 31;
+    const bool aFits = op.M * op.lda * es < lim && ((op.M - 1) * op.lda + op.K) * es < lim;
     if (op.b_kmajor) {
         return (ct == KUDNN_DT_BF16 || ct == KUDNN_DT_F16) && op.K > 0 && op.K % 64 == 0 && op.N % kBN == 0 &&
-               (op.lda * es) % 16 == 0 && (op.ldb * es) % 16 == 0 && op.ldb >= op.N &&
-               op.M * op.lda * es < (int64_t(1) << 31) && op.K * op.ldb * es < (int64_t(1) << 31) &&
-               reinterpret_cast<uintptr_t>(op.b) % 16 == 0;
+               (op.lda * es) % 16 == 0 && (op.ldb * es) % 16 == 0 && op.ldb >= op.N && aFits &&
+               op.K * op.ldb * es < lim && reinterpret_cast<uintptr_t>(op.b) % 16 == 0;
     }
     return (ct == KUDNN_DT_BF16 || ct == KUDNN_DT_F16 || ct == KUDNN_DT_S8) && (op.K * es) % kRowBytes == 0 &&
-           (op.lda * es) % 16 == 0 && (op.ldb * es) % 16 == 0 && op.M * op.lda * es < (int64_t(1) << 31) &&
-           op.N * op.ldb * es < (int64_t(1) << 31) && op.K > 0;
+           (op.lda * es) % 16 == 0 && (op.ldb * es) % 16 == 0 && aFits && op.N * op.ldb * es < lim &&
+           ((op.N - 1) * op.ldb + op.K) * es < lim && op.K > 0;
 }
 
 namespace {

@@ -340,6 +340,14 @@ int launch_gemv(const GemmOperands &op, const EpiParams &ep, int64_t batches, hi
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+// Bytes a kernel reads from an operand of `rows` rows of `chunks` 16-byte chunks at a pitch of `ld` 16-bit elements:
+// through the last row's last chunk. A row count of one has a pitch of 0 in the descriptors (and a strided descriptor
+// may repeat a row with pitch 0), so the count times the pitch is not the extent.
+__host__ __device__ inline int64_t operand_extent(int64_t rows, int64_t ld, int64_t chunks)
+{
+    return (rows - 1) * ld * 2 + chunks * 16;
+}
+
 // 2 <= M <= 16: 16 weight rows per workgroup, KW waves splitting K into blocks of 256 (block b goes to wave b % KW).
 // A wave loads a block of all 16 rows two rows per instruction (lanes 0-31 one row, 32-63 the next: 512 contiguous
 // bytes per row, whole cache lines; the MFMA operand layout would read 16 rows x 64 bytes per instruction, which the
@@ -349,6 +357,8 @@ int launch_gemv(const GemmOperands &op, const EpiParams &ep, int64_t batches, hi
 // it back in the operand layout of v_mfma_f32_16x16x32_bf16, weight rows first, X (rows m < M, cache-resident) second.
 // Loads go through buffer resources and are issued by every lane: a lane with nothing to load (a chunk past K, an X
 // row m >= M) gets an offset past the resource's range, which reads zero, so no branch separates the loads of a block.
+// The weight loads are non-temporal: measured on MI355X, a plain stream of 8 KB weight rows from HBM reads at 6.2 TB/s
+// without the hint and 6.6 TB/s with it (the row kernel's M = 4 and 16 steps at N = 14336 went 5-6 % faster).
 // With PIPE, a wave issues the weight loads of its next block before the current block goes through LDS and the MFMAs,
 // into a second set of registers (the two sets alternate). The KW partial 16 x 16 tiles are summed through LDS and
 // wave 0 runs the epilogue on runs of 4 consecutive columns.
@@ -380,14 +390,14 @@ __device__ __forceinline__ void skinny_rows_body(const GemmOperands &op, const E
     const int q = lane >> 4;
     const int half = lane >> 5, c32 = lane & 31;
     // rows are 16-byte aligned with a zero-padded or exact multiple-of-8 length (the planner packs otherwise), so whole
-    // chunks up to ceil(K / 8) are in bounds; the launcher guarantees N * ldb * 2 < 2^31 and M * lda * 2 < 2^31
+    // chunks up to ceil(K / 8) are in bounds; the launcher guarantees both operands' extents are below 2^31 bytes
     const int chunks = static_cast<int>((op.K + 7) / 8);
     const int blocks = (chunks + 31) / 32;
     constexpr uint32_t kOut = 0xFFFFFFF0u;  // past any range below
     const __amdgpu_buffer_rsrc_t wrs =
-        __builtin_amdgcn_make_buffer_rsrc((void *)W, (short)0, static_cast<int>(N * op.ldb * 2), 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc((void *)W, (short)0, static_cast<int>(operand_extent(N, op.ldb, chunks)), 0x00020000);
     const __amdgpu_buffer_rsrc_t xrs =
-        __builtin_amdgcn_make_buffer_rsrc((void *)X, (short)0, static_cast<int>(M * op.lda * 2), 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc((void *)X, (short)0, static_cast<int>(operand_extent(M, op.lda, chunks)), 0x00020000);
     const uint32_t rowBytes = static_cast<uint32_t>(op.ldb) * 2u;
     const uint32_t xrow = static_cast<uint32_t>(r16) * static_cast<uint32_t>(op.lda) * 2u;
     // byte offset of this lane's row within instruction i (rows 2i, 2i+1; rows past N load row N-1, never stored)
@@ -412,7 +422,7 @@ __device__ __forceinline__ void skinny_rows_body(const GemmOperands &op, const E
         const bool win = b < blocks && c0 + c32 < chunks;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            wv[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, win ? wrow[i] + static_cast<uint32_t>(c0 + c32) * 16u : kOut, 0, 0);
+            wv[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, win ? wrow[i] + static_cast<uint32_t>(c0 + c32) * 16u : kOut, 0, 2);
         }
     };
     // one block: X's loads of block b, then the weight loads of the wave's next block into wn (so they stay in flight
@@ -513,10 +523,11 @@ struct RowsArgs {
     int bin, fast4;
 };
 
-template <int CT, int KW, bool PIPE, int ACT, int FORM>
-__global__ __launch_bounds__(KW * 64) void skinny_rows_compact_kernel(RowsArgs r)
+// The GemmOperands and EpiParams of a compact call: the fields a fixed-form epilogue reads, the rest zero.
+template <int ACT, int FORM>
+__device__ __forceinline__ void unpack_rows_args(const RowsArgs &r, GemmOperands &op, EpiParams &ep)
 {
-    GemmOperands op{};
+    op = GemmOperands{};
     op.a = r.a;
     op.b = r.b;
     op.M = r.M;
@@ -524,9 +535,8 @@ __global__ __launch_bounds__(KW * 64) void skinny_rows_compact_kernel(RowsArgs r
     op.K = r.K;
     op.lda = r.lda;
     op.ldb = r.ldb;
-    // the epilogue helpers read an EpiParams: the fields a fixed form uses, the rest zero
     constexpr int DT = FORM == EPI_FORM_BF16 ? KUDNN_DT_BF16 : KUDNN_DT_F32;
-    EpiParams ep{};
+    ep = EpiParams{};
     ep.alpha = r.alpha;
     ep.gamma = r.gamma;
     ep.act_alpha = r.act_alpha;
@@ -544,40 +554,72 @@ __global__ __launch_bounds__(KW * 64) void skinny_rows_compact_kernel(RowsArgs r
     ep.y_sm = r.y_sm;
     ep.y_sn = 1;
     ep.bdim[0] = ep.bdim[1] = ep.bdim[2] = 1;
+}
+
+template <int CT, int KW, bool PIPE, int ACT, int FORM>
+__global__ __launch_bounds__(KW * 64) void skinny_rows_compact_kernel(RowsArgs r)
+{
+    GemmOperands op;
+    EpiParams ep;
+    unpack_rows_args<ACT, FORM>(r, op, ep);
     skinny_rows_body<CT, KW, PIPE, ACT, FORM>(op, ep);
+}
+
+// The compact instance kernelOf(activation, form) for a single-batch call in a fixed epilogue form (bf16 or f32
+// tensors) with one of the compiled activations; nullptr otherwise, for the generic kernel.
+template <typename KernelOf>
+auto pick_compact(const EpiParams &ep, bool single, KernelOf kernelOf)
+    -> decltype(kernelOf(std::integral_constant<int, KUDNN_ACT_UNIMPLEMENTED>{}, std::integral_constant<int, EPI_FORM_BF16>{}))
+{
+    decltype(kernelOf(std::integral_constant<int, KUDNN_ACT_UNIMPLEMENTED>{}, std::integral_constant<int, EPI_FORM_BF16>{})) ck =
+        nullptr;
+    auto pick = [&](auto formc) {
+        switch (ep.act) {
+            case KUDNN_ACT_UNIMPLEMENTED: ck = kernelOf(std::integral_constant<int, KUDNN_ACT_UNIMPLEMENTED>{}, formc); break;
+            case KUDNN_ACT_RELU: ck = kernelOf(std::integral_constant<int, KUDNN_ACT_RELU>{}, formc); break;
+            case KUDNN_ACT_SWISH: ck = kernelOf(std::integral_constant<int, KUDNN_ACT_SWISH>{}, formc); break;
+            case KUDNN_ACT_GELU_TANH: ck = kernelOf(std::integral_constant<int, KUDNN_ACT_GELU_TANH>{}, formc); break;
+            case KUDNN_ACT_GELU_ERF: ck = kernelOf(std::integral_constant<int, KUDNN_ACT_GELU_ERF>{}, formc); break;
+            default: break;
+        }
+    };
+    const int form = epi_form(ep, false);
+    if (single && form == EPI_FORM_BF16) {
+        pick(std::integral_constant<int, EPI_FORM_BF16>{});
+    } else if (single && form == EPI_FORM_F32) {
+        pick(std::integral_constant<int, EPI_FORM_F32>{});
+    }
+    return ck;
+}
+
+// The fields of a compact call.
+inline RowsArgs rows_args(const GemmOperands &op, const EpiParams &ep)
+{
+    return RowsArgs{op.a,    op.b,   ep.bias,    ep.src,     ep.y,      op.M,    op.N,     op.K,
+                    op.lda,  op.ldb, ep.bias_sm, ep.bias_sn, ep.src_sm, ep.y_sm, ep.alpha, ep.gamma,
+                    ep.act_alpha, ep.bin, ep.fast4};
+}
+
+// A call that can take a compact kernel: one batch, contiguous 4-element runs, a binary operand contiguous along n.
+inline bool compact_call(const EpiParams &ep, dim3 grid)
+{
+    return grid.y == 1 && ep.fast4 && (ep.bin == KUDNN_BINARY_NONE || ep.src_sn == 1);
 }
 
 // Launches the row kernel of form (KW, PIPE): the compact kernel when the call is single-batch in a fixed form with one
 // of the compiled activations, the generic kernel otherwise.
 template <int CT, int KW, bool PIPE>
-void launch_rows(const GemmOperands &op, const EpiParams &ep, dim3 grid, hipStream_t stream)
+void launch_rows(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream)
 {
+    const dim3 grid(static_cast<unsigned>((op.N + 15) / 16), static_cast<unsigned>(batches));
     decltype(&skinny_rows_compact_kernel<CT, KW, PIPE, 0, EPI_FORM_BF16>) ck = nullptr;
-    const int form = epi_form(ep, false);
-    const bool single = grid.y == 1 && ep.fast4 && (ep.bin == KUDNN_BINARY_NONE || ep.src_sn == 1);
     if constexpr (CT == KUDNN_DT_BF16) {
-        auto pick = [&](auto formc) {
-            constexpr int F = decltype(formc)::value;
-            switch (ep.act) {
-                case KUDNN_ACT_UNIMPLEMENTED: ck = skinny_rows_compact_kernel<CT, KW, PIPE, KUDNN_ACT_UNIMPLEMENTED, F>; break;
-                case KUDNN_ACT_RELU: ck = skinny_rows_compact_kernel<CT, KW, PIPE, KUDNN_ACT_RELU, F>; break;
-                case KUDNN_ACT_SWISH: ck = skinny_rows_compact_kernel<CT, KW, PIPE, KUDNN_ACT_SWISH, F>; break;
-                case KUDNN_ACT_GELU_TANH: ck = skinny_rows_compact_kernel<CT, KW, PIPE, KUDNN_ACT_GELU_TANH, F>; break;
-                case KUDNN_ACT_GELU_ERF: ck = skinny_rows_compact_kernel<CT, KW, PIPE, KUDNN_ACT_GELU_ERF, F>; break;
-                default: break;
-            }
-        };
-        if (single && form == EPI_FORM_BF16) {
-            pick(std::integral_constant<int, EPI_FORM_BF16>{});
-        } else if (single && form == EPI_FORM_F32) {
-            pick(std::integral_constant<int, EPI_FORM_F32>{});
-        }
+        ck = pick_compact(ep, compact_call(ep, grid), [](auto actc, auto formc) {
+            return skinny_rows_compact_kernel<CT, KW, PIPE, decltype(actc)::value, decltype(formc)::value>;
+        });
     }
     if (ck != nullptr) {
-        const RowsArgs r{op.a,    op.b,  ep.bias,    ep.src,     ep.y,       op.M,   op.N,     op.K,
-                         op.lda,  op.ldb, ep.bias_sm, ep.bias_sn, ep.src_sm,  ep.y_sm, ep.alpha, ep.gamma,
-                         ep.act_alpha, ep.bin, ep.fast4};
-        hipLaunchKernelGGL(ck, grid, dim3(KW * 64), 0, stream, r);
+        hipLaunchKernelGGL(ck, grid, dim3(KW * 64), 0, stream, rows_args(op, ep));
     } else {
         hipLaunchKernelGGL((skinny_rows_kernel<CT, KW, PIPE>), grid, dim3(KW * 64), 0, stream, op, ep);
     }
@@ -605,19 +647,19 @@ int launch_skinny(const GemmOperands &op, const EpiParams &ep, int64_t batches, 
     if (gemv_eligible(op)) {
         return launch_gemv<CT>(op, ep, batches, stream);
     }
-    if (op.N * op.ldb * 2 < (int64_t(1) << 31) && op.M * op.lda * 2 < (int64_t(1) << 31)) {
+    const int64_t chunks = (op.K + 7) / 8;
+    if (operand_extent(op.N, op.ldb, chunks) < (int64_t(1) << 31) && operand_extent(op.M, op.lda, chunks) < (int64_t(1) << 31)) {
         // fewer than 2 row groups per CU: split K over 16 waves (one workgroup per CU); otherwise 8 (two per CU)
         const int64_t groups = (op.N + 15) / 16 * batches;
-        dim3 grid(static_cast<unsigned>((op.N + 15) / 16), static_cast<unsigned>(batches));
         // measured at M = 4 and 16, N = 4096 and 14336, K = 4096: with more than 8 rows of X, 2-wave workgroups with
         // the next block's weights in flight (145 VGPRs, 12 waves and 6 workgroups per CU, one round of workgroups)
         // beat the 8- and 16-wave forms by 8-9 %; at M = 4 they lose 1-4 %, and with few row groups they leave CUs idle
         if (op.M > 8 && groups >= 256) {
-            launch_rows<CT, 2, true>(op, ep, grid, stream);
+            launch_rows<CT, 2, true>(op, ep, batches, stream);
         } else if (groups < 512) {
-            launch_rows<CT, 16, false>(op, ep, grid, stream);
+            launch_rows<CT, 16, false>(op, ep, batches, stream);
         } else {
-            launch_rows<CT, 8, false>(op, ep, grid, stream);
+            launch_rows<CT, 8, false>(op, ep, batches, stream);
         }
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }

@@ -757,3 +757,25 @@ def test_operands_of_2_gib(case):
         O.linear_act(xs, ws, ref, None, O.ACT_SWISH, 1.0)
         got = _bits(y[:, torch.as_tensor(cols, device="cuda")]).reshape(-1)
     compare(got, ref.buf, dt, f"{case} {plan.describe()}")
+
+
+@pytest.mark.parametrize("M,Kd,expect", [(20480, 128, "mfma_bf16_pingpong"), (16, 4096, "skinny_bf16_16xK"),
+                                         (9, 256, "skinny_bf16_16xK"), (3, 64, "skinny_bf16_16xK"),
+                                         (1, 520, "skinny_bf16_gemv")])
+def test_single_weight_row(M, Kd, expect):
+    # N = 1: the weight descriptor's row pitch is 0 (a dimension of size one), so the kernels that bound their reads by
+    # a buffer range take the operand's extent from its last row, not from rows x pitch (which is 0)
+    N = 1
+    x = Case([M, Kd], O.BF16, seed=270, dist="normal", lo=0.0, hi=1.0)
+    w = Case([Kd, N], O.BF16, "BA", seed=271, dist="normal", lo=0.0, hi=0.05)
+    b = Case([1, N], O.BF16, seed=272, lo=-0.1, hi=0.1)
+    c = Case([M, N], O.BF16, zero=True)
+    assert w.desc.stride()[1] == 0
+    plan = K.LinearActivation(x.desc, w.desc, c.desc, b.desc, 0.0, 0.0, K.ACT_RELU)
+    assert plan.describe().startswith(expect), plan.describe()
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc, b.device())
+    torch.cuda.synchronize()
+    ref = c.clone_empty()
+    O.linear_act(x.t, w.t, ref, b.t, O.ACT_RELU, 0.0)
+    compare(from_device(dc, O.BF16), ref.buf, O.BF16, plan.describe())
