@@ -3,14 +3,16 @@
 // conversion of the VALU dot product changes, nothing else.
 //
 // The reference reaches cblas_sgemv for m == 1 (src/dnn/src/kudnn_gemm.cpp:164-173) and cblas_sbgemm /
-// cblas_bgemm otherwise (:208-241). On MI355X this shape is bound by streaming W from HBM once, so the
-// kernel is organised around the weight stream, not around compute:
-//  - a workgroup owns 16 weight rows (n) and all of K; its KW waves split K into KW contiguous ranges;
-//  - each lane loads 16-byte chunks of W straight from global memory into the register layout of
-//    v_mfma_f32_16x16x32_bf16 (lane l: row l%16, k-chunk l/16; a wave instruction reads 16 rows x 64
-//    contiguous bytes), UNR k-steps are issued back to back to keep enough bytes in flight;
-//  - X rows (m < M, tiny and cache-resident) form the second MFMA operand; lanes with m >= M feed zeros;
-//  - the KW partial 16x16 tiles are summed through LDS and wave 0 runs the fused epilogue.
+// cblas_bgemm otherwise (:208-241). On MI355X this shape is bound by streaming W from HBM once, so the kernels are
+// organised around the weight stream, not around compute:
+//  - M = 1, gemv_bf16_(compact_)kernel: one wave per weight row, 1 KB of the row per load instruction, a VALU dot
+//    product reduced across the wave;
+//  - 2 <= M <= 16, skinny_rows_(compact_)kernel: 16 weight rows per workgroup, K split over its waves in blocks of
+//    256; whole-row loads go through a per-wave LDS tile into the operand layout of v_mfma_f32_16x16x32_bf16, X (rows
+//    m < M, cache-resident) is the second operand, and the waves' partial 16 x 16 tiles are summed through LDS;
+//  - operands of 2^31 bytes or more, skinny_bf16_kernel: loads straight into the MFMA operand layout (16 rows x 64
+//    bytes per instruction) with 64-bit addressing, UNR k-steps in flight.
+// Wave 0 (lane 0 for M = 1) runs the fused epilogue.
 #include <utility>
 
 #include "device_common.h"
