@@ -1049,20 +1049,27 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
     return KUDNN_STATUS_SUCCESS;
 }
 
-// Runs a core, batch by batch in order when C is broadcast over a looped batch dim (the reference's
-// sequential batch loop, kudnn_gemm.cpp:783-807, then leaves the last batch's result).
-int RunCore(const GemmCore &core, const EpiExtras &x, const void *a, const void *b, void *c, const void *bias,
-            const void *src, void *y, float alpha, float beta, float gamma, Workspace &wsp, hipStream_t stream)
+// Launches `core` over its batch dims in order: one launch per index of the outer `split` dims, each covering the
+// inner dims; with split 3, each launch covers `chunk` consecutive indices of the last dim (the reference's batch loop,
+// kudnn_gemm.cpp:783-807).
+int RunSplit(const GemmCore &core, int split, int64_t chunk, const EpiExtras &x, const void *a, const void *b, void *c,
+             const void *bias, const void *src, void *y, float alpha, float beta, float gamma, Workspace &wsp,
+             hipStream_t stream)
 {
-    if (!core.serial) {
-        return LaunchCore(core, x, a, b, c, bias, src, y, alpha, beta, gamma, wsp, stream);
-    }
     GemmCore one = core;
     one.serial = false;
-    one.bdim[0] = one.bdim[1] = one.bdim[2] = 1;
-    for (int64_t i0 = 0; i0 < core.bdim[0]; ++i0) {
-        for (int64_t i1 = 0; i1 < core.bdim[1]; ++i1) {
-            for (int64_t i2 = 0; i2 < core.bdim[2]; ++i2) {
+    int64_t outer[3] = {1, 1, 1};
+    for (int s = 0; s < split; ++s) {
+        outer[s] = core.bdim[s];
+        one.bdim[s] = 1;
+    }
+    const int64_t step2 = split == 3 ? chunk : 1;
+    for (int64_t i0 = 0; i0 < outer[0]; ++i0) {
+        for (int64_t i1 = 0; i1 < outer[1]; ++i1) {
+            for (int64_t i2 = 0; i2 < outer[2]; i2 += step2) {
+                if (split == 3) {
+                    one.bdim[2] = std::min(chunk, outer[2] - i2);
+                }
                 auto off = [&](const int64_t bs[3], int dt) {
                     return (i0 * bs[0] + i1 * bs[1] + i2 * bs[2]) * DtSize(dt);
                 };
@@ -1080,6 +1087,23 @@ int RunCore(const GemmCore &core, const EpiExtras &x, const void *a, const void 
         }
     }
     return KUDNN_STATUS_SUCCESS;
+}
+
+// Runs a core: batch by batch in order when C is broadcast over a looped batch dim (the reference's sequential batch
+// loop, kudnn_gemm.cpp:783-807, then leaves the last batch's result); in several launches over the batch dims when the
+// batches exceed what one launch's grid carries (65535 rows of workgroups); otherwise in one launch.
+int RunCore(const GemmCore &core, const EpiExtras &x, const void *a, const void *b, void *c, const void *bias,
+            const void *src, void *y, float alpha, float beta, float gamma, Workspace &wsp, hipStream_t stream)
+{
+    constexpr int64_t kMaxGridBatches = 65535;
+    if (core.serial) {
+        return RunSplit(core, 3, 1, x, a, b, c, bias, src, y, alpha, beta, gamma, wsp, stream);
+    }
+    if (core.Batches() > kMaxGridBatches) {
+        const int split = core.bdim[1] * core.bdim[2] <= kMaxGridBatches ? 1 : (core.bdim[2] <= kMaxGridBatches ? 2 : 3);
+        return RunSplit(core, split, kMaxGridBatches, x, a, b, c, bias, src, y, alpha, beta, gamma, wsp, stream);
+    }
+    return LaunchCore(core, x, a, b, c, bias, src, y, alpha, beta, gamma, wsp, stream);
 }
 
 // ---------------------------------------------------------------------------------------------------

@@ -203,3 +203,26 @@ def test_mtest_float(caller, dims, mnk, mode):
 @pytest.mark.parametrize("caller", OTHER_CALLERS, ids=lambda c: "_".join(O.DT_NAMES[t] for t in c))
 def test_mtest_other_dtypes(caller, dims, mnk, mode):
     _mtest(caller, dims, mnk, mode, seed=610)
+
+
+@pytest.mark.parametrize("case", ["bf16_one_dim", "f32_two_dims"])
+def test_batches_beyond_one_grid(case):
+    # more batches than one launch's grid carries (65535 rows of workgroups): the run is split over the batch dims,
+    # in order, as the reference loops over them (kudnn_gemm.cpp:783-807). 70000 batches of one dim are launched in
+    # chunks of that dim; 3 x 30000 loops over the outer dim
+    if case == "bf16_one_dim":
+        dt, xd, wd, bd, cd, lay = O.BF16, [70000, 2, 16], [70000, 16, 8], [1, 1, 8], [70000, 2, 8], "ABC"
+    else:
+        dt, xd, wd, bd, cd, lay = O.F32, [3, 30000, 4, 32], [3, 30000, 32, 8], [1, 1, 1, 8], [3, 30000, 4, 8], "ABCD"
+    x = _case(xd, dt, lay, seed=500)
+    w = _case(wd, dt, lay, seed=501)
+    b = _case(bd, dt, lay, seed=502)
+    c = _case(cd, dt, lay, zero=True)
+    plan = K.LinearActivation(x.desc, w.desc, c.desc, b.desc, 0.0, 0.0, K.ACT_RELU)
+    assert "batches=70000" in plan.describe() or "batches=90000" in plan.describe(), plan.describe()
+    dc = torch.zeros(c.t.buf.size, dtype=torch.float32 if dt == O.F32 else torch.int16, device="cuda")
+    plan.run(x.device(), w.device(), dc, b.device())
+    torch.cuda.synchronize()
+    ref = c.clone_empty()
+    O.linear_act(x.t, w.t, ref, b.t, O.ACT_RELU, 0.0)
+    compare(from_device(dc, dt), ref.buf, dt, plan.describe())
