@@ -20,8 +20,9 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs p)
 {
     __shared__ float tile[kTile][kTile + 1];
     const int tid = threadIdx.x;
-    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kTile;
-    const int64_t k0 = static_cast<int64_t>(blockIdx.x) * kTile;
+    // rows on x (up to 2^31 - 1 workgroups: a folded batch makes M large), K on y
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kTile;
+    const int64_t k0 = static_cast<int64_t>(blockIdx.y) * kTile;
     const int64_t b = blockIdx.z;
     const int64_t i2 = b % p.bdim[2];
     const int64_t i1 = (b / p.bdim[2]) % p.bdim[1];
@@ -99,7 +100,7 @@ int kudnn_launch_rowsum_s8(const int8_t *p, int64_t rows, int64_t kp, int64_t co
 
 int kudnn_launch_pack(const PackArgs &p, int64_t batches, hipStream_t stream)
 {
-    dim3 grid(static_cast<unsigned>((p.kp + kTile - 1) / kTile), static_cast<unsigned>((p.rows + kTile - 1) / kTile),
+    dim3 grid(static_cast<unsigned>((p.rows + kTile - 1) / kTile), static_cast<unsigned>((p.kp + kTile - 1) / kTile),
               static_cast<unsigned>(batches));
     hipLaunchKernelGGL(pack_kernel, grid, dim3(256), 0, stream, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
