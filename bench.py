@@ -20,9 +20,11 @@ elementwise copy-like kernel (y = -x, 512 MiB bf16 in, 512 MiB out) whose known 
 FETCH_SIZE / WRITE_SIZE counters against which the C3 kernel's HBM traffic is read. --only dispatch times a bf16
 Linear + GELU(tanh) over prefill-like shapes under every kernel configuration (forced through KUDNN_HIP_FORCE_CFG and
 KUDNN_HIP_FORCE_STREAMK) and under the planner's own choice, one JSON line per shape: the measurement the
-dispatcher's rule is drawn from.
+dispatcher's rule is drawn from. --only refperf times KuDNN::Gemm on the reference's own perf shape sets (the
+matmul gtest's freParas and freParasMulti) in f32 and bf16, one JSON line per shape and type.
 
-Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--prewarm-ms 300] [--only c3|copy|decode|dispatch]
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--prewarm-ms 300]
+                       [--only c3|copy|decode|dispatch|refperf]
 """
 from __future__ import annotations
 
@@ -51,7 +53,7 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--prewarm-ms", type=float, default=300.0, help="untimed run time before warmup (clock ramp)")
-    p.add_argument("--only", choices=["c3", "copy", "decode", "dispatch"], default=None,
+    p.add_argument("--only", choices=["c3", "copy", "decode", "dispatch", "refperf"], default=None,
                    help="profiling modes (see module docstring)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-decode", action="store_true")
@@ -430,6 +432,43 @@ def bench_dispatch(args, torch, K):
             os.environ[key] = val
 
 
+# The reference's perf shape sets: freParas and freParasMulti of test/dnn/llt/gtest/src/matmul_gtest.cpp:550 and :697-705,
+# as (M, N, K), run in its Matmul mode (src [M, K], wei [K, N] in layout AB, bias [1, N]).
+REF_PERF_SHAPES = [(4096, 3072, 5120), (4096, 32768, 512), (4096, 1536, 5120), (4096, 5120, 1536), (4096, 5120, 3072),
+                   (4096, 4096, 1152), (4096, 4608, 1152), (4096, 1152, 3256), (4096, 1152, 4608)]
+
+
+def bench_refperf(args, torch, K):
+    """KuDNN::Gemm on the reference's perf shapes, f32 and bf16, with the weight [K][N] as the reference's Matmul mode
+    stores it (microseconds per call; CUDA events around `--steps` back-to-back calls after `--warmup`)."""
+    g = torch.Generator(device="cuda").manual_seed(0)
+    out = []
+    for M, N, Kd in REF_PERF_SHAPES:
+        for name, kdt, tdt, peak in (("f32", K.F32, torch.float32, PEAK_F32_TFLOPS), ("bf16", K.BF16, torch.bfloat16,
+                                                                                      PEAK_BF16_TFLOPS)):
+            x = torch.randn(M, Kd, device="cuda", generator=g).to(tdt)
+            w = (torch.randn(Kd, N, device="cuda", generator=g) * 0.02).to(tdt)
+            b = (torch.randn(1, N, device="cuda", generator=g) * 0.02).to(tdt)
+            y = torch.empty(M, N, device="cuda", dtype=tdt)
+            plan = K.Gemm(K.desc([M, Kd], kdt), K.desc([Kd, N], kdt), K.desc([M, N], kdt), K.desc([1, N], kdt))
+            for _ in range(args.warmup):
+                plan.run(x, w, y, b)
+            torch.cuda.synchronize()
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record()
+            for _ in range(args.steps):
+                plan.run(x, w, y, b)
+            t1.record()
+            torch.cuda.synchronize()
+            us = t0.elapsed_time(t1) / args.steps * 1e3
+            tf = 2.0 * M * N * Kd / (us * 1e-6) / 1e12
+            out.append({"M": M, "N": N, "K": Kd, "dtype": name, "us": round(us, 1), "TFLOP/s": round(tf, 1),
+                        "frac_peak": round(tf / peak, 3), "plan": plan.describe()})
+            print(json.dumps(out[-1]), flush=True)
+            del x, w, b, y, plan
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -458,6 +497,10 @@ def main():
 
     if args.only == "dispatch":
         bench_dispatch(args, torch, K)
+        return
+
+    if args.only == "refperf":
+        bench_refperf(args, torch, K)
         return
 
     if args.only == "decode":

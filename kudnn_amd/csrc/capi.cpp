@@ -562,8 +562,13 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
         }
     } else {
         core.engine = ENGINE_MFMA_F32;
-        int64_t t128 = (core.M + 127) / 128 * ((core.N + 127) / 128) * batches;
-        core.cfg = t128 >= 256 ? KUDNN_CFG_F32_128x128 : KUDNN_CFG_F32_64x64;
+        // 128 x 128 tiles from one full round of the 256 CUs on, except below 1024 tiles when the last round is at
+        // most half full: measured on MI355X over 256..640 tiles at K = 1024..5120, 64 x 64 tiles were 8-17 % faster
+        // at 288-384 tiles, within 3 % at 576 and 640, and slower at 256, 400-512
+        const int64_t t128 = (core.M + 127) / 128 * ((core.N + 127) / 128) * batches;
+        const int64_t lastRound = t128 % 256;
+        const bool halfRound = t128 > 256 && t128 < 1024 && lastRound != 0 && lastRound <= 128;
+        core.cfg = t128 >= 256 && !halfRound ? KUDNN_CFG_F32_128x128 : KUDNN_CFG_F32_64x64;
         // A grid of fewer than 128 tiles of 64 x 64 (which the 64 x 64 kernel would split along K across workgroups)
         // that still makes at least 128 tiles of 16 x 32: one tile per workgroup, K split over its waves. Measured on
         // MI355X it wins up to K = 4096 (C1, 128 x 1024 x 1024: 8.5 against 12.5 us) and for M <= 16 at any K; beyond,
