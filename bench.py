@@ -19,9 +19,11 @@ decode lines, and --only copy runs an
 elementwise copy-like kernel (y = -x, 512 MiB bf16 in, 512 MiB out) whose known traffic calibrates the
 FETCH_SIZE / WRITE_SIZE counters against which the C3 kernel's HBM traffic is read. --only dispatch times a bf16
 Linear + GELU(tanh) over prefill-like shapes under every kernel configuration (forced through KUDNN_HIP_FORCE_CFG and
-KUDNN_HIP_FORCE_STREAMK) and under the planner's own choice, one JSON line per shape: the measurement the
-dispatcher's rule is drawn from. --only refperf times KuDNN::Gemm on the reference's own perf shape sets (the
-matmul gtest's freParas and freParasMulti) in f32 and bf16, one JSON line per shape and type.
+KUDNN_HIP_FORCE_STREAMK) and under the planner's own choice, one JSON line per shape, then an f32 Gemm over grids of
+256-640 tiles of 128 x 128 under the 128 x 128 and 64 x 64 configurations: the measurements the dispatcher's rules are
+drawn from. --only refperf times KuDNN::Gemm on the reference's own perf shape sets (the matmul gtest's freParas and
+freParasMulti) in f32 and bf16, under the planner and under every forced configuration, one JSON line per shape and
+type.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--prewarm-ms 300]
                        [--only c3|copy|decode|dispatch|refperf]
@@ -389,12 +391,43 @@ def cpu_baseline(args, np):
                                "multiplier M2; C5: one batch, weight read as [N][K])"}
 
 
+def _time_calls(fn, steps, warmup, torch, prewarm_ms=30.0):
+    """Microseconds per call of fn() over `steps` back-to-back calls, after `prewarm_ms` of wall time and `warmup`
+    calls untimed (the first configuration of a shape otherwise pays for the clock ramp and first touches)."""
+    t_end = time.perf_counter() + prewarm_ms * 1e-3
+    while time.perf_counter() < t_end:
+        for _ in range(4):
+            fn()
+        torch.cuda.synchronize()
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        fn()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps * 1e3
+
+
+def _with_env(settings):
+    """Sets (name, value) pairs in the environment (value None: unset) and returns the previous values."""
+    saved = {}
+    for key, val in settings:
+        saved[key] = os.environ.get(key)
+        if val is None:
+            os.environ.pop(key, None)
+        else:
+            os.environ[key] = val
+    return saved
+
+
 def bench_dispatch(args, torch, K):
     """Every bf16 kernel configuration against the planner's choice over prefill-like shapes (microseconds per call;
-    CUDA events around `--steps` back-to-back calls after `--warmup`)."""
+    CUDA events around `--steps` back-to-back calls after 30 ms and `--warmup` calls untimed)."""
     configs = [("pingpong", "4", "0"), ("pingpong_split", "4", "1"), ("4wave_256x128", "2", "0"),
                ("4wave_128x128", "3", "0"), ("4wave_256x256", "1", "0"), ("planner", None, None)]
-    saved = {k: os.environ.get(k) for k in ("KUDNN_HIP_FORCE_CFG", "KUDNN_HIP_FORCE_STREAMK")}
     g = torch.Generator(device="cuda").manual_seed(0)
     for M in (256, 512, 1024, 2048, 3072):
         for N, Kd in ((4096, 4096), (11008, 4096), (4096, 11008), (14336, 4096), (4096, 14336), (2048, 2048),
@@ -404,32 +437,16 @@ def bench_dispatch(args, torch, K):
             y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
             line = {"M": M, "N": N, "K": Kd}
             for name, cfg, split in configs:
-                for key, val in (("KUDNN_HIP_FORCE_CFG", cfg), ("KUDNN_HIP_FORCE_STREAMK", split)):
-                    if val is None:
-                        os.environ.pop(key, None)
-                    else:
-                        os.environ[key] = val
+                saved = _with_env((("KUDNN_HIP_FORCE_CFG", cfg), ("KUDNN_HIP_FORCE_STREAMK", split)))
                 plan = K.LinearPostOps(K.desc([M, Kd], K.BF16), K.desc([Kd, N], K.BF16, "BA"), K.desc([M, N], K.BF16),
                                        None, act=K.ACT_GELU_TANH)
-                for _ in range(args.warmup):
-                    plan.run(x, w, y)
-                torch.cuda.synchronize()
-                t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                t0.record()
-                for _ in range(args.steps):
-                    plan.run(x, w, y)
-                t1.record()
-                torch.cuda.synchronize()
-                line[name] = round(t0.elapsed_time(t1) / args.steps * 1e3, 1)
+                line[name] = round(_time_calls(lambda: plan.run(x, w, y), args.steps, args.warmup, torch), 1)
+                _with_env(saved.items())
                 if cfg is None:
                     line["planner_plan"] = plan.describe()
+                del plan
             print(json.dumps(line), flush=True)
             del x, w, y
-    for key, val in saved.items():
-        if val is None:
-            os.environ.pop(key, None)
-        else:
-            os.environ[key] = val
 
 
 # The reference's perf shape sets: freParas and freParasMulti of test/dnn/llt/gtest/src/matmul_gtest.cpp:550 and :697-705,
@@ -440,33 +457,66 @@ REF_PERF_SHAPES = [(4096, 3072, 5120), (4096, 32768, 512), (4096, 1536, 5120), (
 
 def bench_refperf(args, torch, K):
     """KuDNN::Gemm on the reference's perf shapes, f32 and bf16, with the weight [K][N] as the reference's Matmul mode
-    stores it (microseconds per call; CUDA events around `--steps` back-to-back calls after `--warmup`)."""
+    stores it: the planner's choice and every forced configuration (microseconds per call; CUDA events around
+    `--steps` back-to-back calls after 30 ms and `--warmup` calls untimed)."""
+    bf16_cfgs = [("ping-pong", "4", "0"), ("ping-pong + K-split", "4", "1"), ("4-wave 256x128", "2", "0"),
+                 ("4-wave 128x128", "3", "0"), ("4-wave 256x256", "1", "0")]
+    f32_cfgs = [("128x128", "10", None), ("64x64", "11", None)]
     g = torch.Generator(device="cuda").manual_seed(0)
     out = []
     for M, N, Kd in REF_PERF_SHAPES:
-        for name, kdt, tdt, peak in (("f32", K.F32, torch.float32, PEAK_F32_TFLOPS), ("bf16", K.BF16, torch.bfloat16,
-                                                                                      PEAK_BF16_TFLOPS)):
+        for name, kdt, tdt, peak, cfgs in (("f32", K.F32, torch.float32, PEAK_F32_TFLOPS, f32_cfgs),
+                                            ("bf16", K.BF16, torch.bfloat16, PEAK_BF16_TFLOPS, bf16_cfgs)):
             x = torch.randn(M, Kd, device="cuda", generator=g).to(tdt)
             w = (torch.randn(Kd, N, device="cuda", generator=g) * 0.02).to(tdt)
             b = (torch.randn(1, N, device="cuda", generator=g) * 0.02).to(tdt)
             y = torch.empty(M, N, device="cuda", dtype=tdt)
-            plan = K.Gemm(K.desc([M, Kd], kdt), K.desc([Kd, N], kdt), K.desc([M, N], kdt), K.desc([1, N], kdt))
-            for _ in range(args.warmup):
-                plan.run(x, w, y, b)
-            torch.cuda.synchronize()
-            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            t0.record()
-            for _ in range(args.steps):
-                plan.run(x, w, y, b)
-            t1.record()
-            torch.cuda.synchronize()
-            us = t0.elapsed_time(t1) / args.steps * 1e3
-            tf = 2.0 * M * N * Kd / (us * 1e-6) / 1e12
-            out.append({"M": M, "N": N, "K": Kd, "dtype": name, "us": round(us, 1), "TFLOP/s": round(tf, 1),
-                        "frac_peak": round(tf / peak, 3), "plan": plan.describe()})
-            print(json.dumps(out[-1]), flush=True)
-            del x, w, b, y, plan
+            line = {"M": M, "N": N, "K": Kd, "dtype": name}
+            for cname, cfg, split in [("planner", None, None)] + cfgs:
+                saved = _with_env((("KUDNN_HIP_FORCE_CFG", cfg), ("KUDNN_HIP_FORCE_STREAMK", split)))
+                plan = K.Gemm(K.desc([M, Kd], kdt), K.desc([Kd, N], kdt), K.desc([M, N], kdt), K.desc([1, N], kdt))
+                us = _time_calls(lambda: plan.run(x, w, y, b), args.steps, args.warmup, torch)
+                _with_env(saved.items())
+                if cname == "planner":
+                    tf = 2.0 * M * N * Kd / (us * 1e-6) / 1e12
+                    line.update({"us": round(us, 1), "TFLOP/s": round(tf, 1), "frac_peak": round(tf / peak, 3),
+                                 "plan": plan.describe()})
+                else:
+                    line[cname] = round(us, 1)
+                del plan
+            out.append(line)
+            print(json.dumps(line), flush=True)
+            del x, w, b, y
     return out
+
+
+# f32 grids of 256 to 640 tiles of 128 x 128 (and two larger), weight [N][K]: where the 128 x 128 and 64 x 64 kernels
+# trade places (the planner's f32 rule)
+F32_TILE_SHAPES = [(2048, 2048, 4096), (2304, 2048, 2048), (2048, 2560, 2048), (2048, 3072, 4096), (1536, 4096, 2048),
+                   (2560, 2560, 2048), (2048, 3584, 2048), (3072, 2560, 1024), (4096, 2304, 2048), (3072, 3072, 2048),
+                   (2560, 4096, 2048), (4096, 1152, 4096), (4096, 1536, 5120), (2048, 4096, 4096)]
+
+
+def bench_dispatch_f32(args, torch, K):
+    """f32 Gemm under the 128 x 128 and 64 x 64 configurations and the planner's choice (microseconds per call)."""
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for M, N, Kd in F32_TILE_SHAPES:
+        x = torch.randn(M, Kd, device="cuda", generator=g)
+        w = torch.randn(N, Kd, device="cuda", generator=g) * 0.02
+        b = torch.randn(1, N, device="cuda", generator=g) * 0.02
+        y = torch.empty(M, N, device="cuda")
+        line = {"M": M, "N": N, "K": Kd, "tiles_128x128": ((M + 127) // 128) * ((N + 127) // 128)}
+        for cname, cfg in (("128x128", "10"), ("64x64", "11"), ("planner", None)):
+            saved = _with_env((("KUDNN_HIP_FORCE_CFG", cfg),))
+            plan = K.Gemm(K.desc([M, Kd], K.F32), K.desc([Kd, N], K.F32, "BA"), K.desc([M, N], K.F32),
+                          K.desc([1, N], K.F32))
+            line[cname] = round(_time_calls(lambda: plan.run(x, w, y, b), args.steps, args.warmup, torch), 1)
+            _with_env(saved.items())
+            if cfg is None:
+                line["planner_plan"] = plan.describe()
+            del plan
+        print(json.dumps(line), flush=True)
+        del x, w, b, y
 
 
 def main():
@@ -497,6 +547,7 @@ def main():
 
     if args.only == "dispatch":
         bench_dispatch(args, torch, K)
+        bench_dispatch_f32(args, torch, K)
         return
 
     if args.only == "refperf":
