@@ -547,7 +547,9 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
     if (core.computeDt != KUDNN_DT_F32) {
         if (core.M <= 16 && lowp16) {
             core.engine = ENGINE_SKINNY_BF16;
-            core.cfg = core.M == 1 ? KUDNN_CFG_GEMV_BF16 : KUDNN_CFG_SKINNY_BF16;
+            // M = 1: the GEMV; 2 <= M <= 5: the GEMV with X staged in LDS (measured on MI355X at K = 4096, N = 4096 and
+            // 14336, it beats the 16-row MFMA kernel by 1-11 % up to M = 5 and loses from M = 6 on); above, 16-row tiles
+            core.cfg = core.M == 1 ? KUDNN_CFG_GEMV_BF16 : (core.M <= 5 ? KUDNN_CFG_GEMV_MULTI_BF16 : KUDNN_CFG_SKINNY_BF16);
         } else {
             core.engine = ENGINE_MFMA_BF16;
             // Measured on MI355X over prefill-like shapes (M 256..3072, N and K 2048..14336): the ping-pong kernel
@@ -588,12 +590,13 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
         bool okBf16 = core.computeDt != KUDNN_DT_F32 &&
                       (((f == KUDNN_CFG_BF16_256x256 || f == KUDNN_CFG_BF16_256x128 || f == KUDNN_CFG_BF16_128x128 ||
                          f == KUDNN_CFG_BF16_PINGPONG_256x256) && mfmaOk) ||
-                       (f == KUDNN_CFG_SKINNY_BF16 && core.M <= 16 && lowp16));
+                       (f == KUDNN_CFG_SKINNY_BF16 && core.M <= 16 && lowp16) ||
+                       (f == KUDNN_CFG_GEMV_MULTI_BF16 && core.M >= 2 && core.M <= 8 && lowp16));
         bool okF32 = core.computeDt == KUDNN_DT_F32 &&
                      (f == KUDNN_CFG_F32_128x128 || f == KUDNN_CFG_F32_64x64 || f == KUDNN_CFG_F32_KSLICE_16x32);
         if (okBf16 || okF32) {
             core.cfg = f;
-            core.engine = f == KUDNN_CFG_SKINNY_BF16 ? ENGINE_SKINNY_BF16
+            core.engine = f == KUDNN_CFG_SKINNY_BF16 || f == KUDNN_CFG_GEMV_MULTI_BF16 ? ENGINE_SKINNY_BF16
                                                      : (okF32 ? ENGINE_MFMA_F32 : ENGINE_MFMA_BF16);
         }
     }
@@ -624,6 +627,7 @@ const char *CfgName(int cfg)
         case KUDNN_CFG_F32_KSLICE_16x32: return "mfma_f32_kslice_16x32";
         case KUDNN_CFG_SKINNY_BF16: return "skinny_bf16_16xK";
         case KUDNN_CFG_GEMV_BF16: return "skinny_bf16_gemv_row";
+        case KUDNN_CFG_GEMV_MULTI_BF16: return "skinny_bf16_gemv_rows_xlds";
         default: return "unknown";
     }
 }
@@ -1026,7 +1030,7 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
 
     int lrc = 0;
     if (core.engine == ENGINE_SKINNY_BF16) {
-        lrc = kudnn_launch_skinny(op, ep, batches, core.computeDt, stream);
+        lrc = kudnn_launch_skinny(op, ep, batches, core.computeDt, core.cfg, stream);
     } else if (core.engine == ENGINE_MFMA_BF16) {
         if (core.cfg == KUDNN_CFG_BF16_PINGPONG_256x256 && kudnn_pingpong_eligible(op, core.computeDt)) {
             lrc = kudnn_launch_gemm_pingpong(op, ep, batches, core.computeDt, tailWs, stream);

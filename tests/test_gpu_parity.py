@@ -760,8 +760,9 @@ def test_operands_of_2_gib(case):
 
 
 @pytest.mark.parametrize("M,Kd,expect", [(20480, 128, "mfma_bf16_pingpong"), (16, 4096, "skinny_bf16_16xK"),
-                                         (9, 256, "skinny_bf16_16xK"), (3, 64, "skinny_bf16_16xK"),
-                                         (1, 520, "skinny_bf16_gemv")])
+                                         (9, 256, "skinny_bf16_16xK"), (6, 64, "skinny_bf16_16xK"),
+                                         (3, 64, "skinny_bf16_gemv_rows_xlds"), (5, 4104, "skinny_bf16_gemv_rows_xlds"),
+                                         (1, 520, "skinny_bf16_gemv_row")])
 def test_single_weight_row(M, Kd, expect):
     # N = 1: the weight descriptor's row pitch is 0 (a dimension of size one), so the kernels that bound their reads by
     # a buffer range take the operand's extent from its last row, not from rows x pitch (which is 0)
