@@ -547,8 +547,8 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
     if (core.computeDt != KUDNN_DT_F32) {
         if (core.M <= 16 && lowp16) {
             core.engine = ENGINE_SKINNY_BF16;
-            // M = 1: the GEMV; 2 <= M <= 5: the GEMV with X staged in LDS (measured on MI355X at K = 4096, N = 4096 and
-            // 14336, it beats the 16-row MFMA kernel by 1-11 % up to M = 5 and loses from M = 6 on); above, 16-row tiles
+            // M <= 5: the GEMV with X staged in LDS (measured on MI355X at K = 4096, N = 4096 and 14336, it beats the
+            // 16-row MFMA kernel by 1-11 % up to M = 5 and loses from M = 6 on); above, 16-row MFMA tiles
             core.cfg = core.M == 1 ? KUDNN_CFG_GEMV_BF16 : (core.M <= 5 ? KUDNN_CFG_GEMV_MULTI_BF16 : KUDNN_CFG_SKINNY_BF16);
         } else {
             core.engine = ENGINE_MFMA_BF16;
@@ -590,7 +590,7 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
         bool okBf16 = core.computeDt != KUDNN_DT_F32 &&
                       (((f == KUDNN_CFG_BF16_256x256 || f == KUDNN_CFG_BF16_256x128 || f == KUDNN_CFG_BF16_128x128 ||
                          f == KUDNN_CFG_BF16_PINGPONG_256x256) && mfmaOk) ||
-                       (f == KUDNN_CFG_SKINNY_BF16 && core.M <= 16 && lowp16) ||
+                       (f == KUDNN_CFG_SKINNY_BF16 && core.M >= 2 && core.M <= 16 && lowp16) ||
                        (f == KUDNN_CFG_GEMV_MULTI_BF16 && core.M >= 2 && core.M <= 8 && lowp16));
         bool okF32 = core.computeDt == KUDNN_DT_F32 &&
                      (f == KUDNN_CFG_F32_128x128 || f == KUDNN_CFG_F32_64x64 || f == KUDNN_CFG_F32_KSLICE_16x32);

@@ -16,7 +16,7 @@ enum {
     KUDNN_CFG_F32_64x64 = 11,
     KUDNN_CFG_F32_KSLICE_16x32 = 12,  // small f32 grids: 16 x 32 tiles, K split over the waves of the workgroup
     KUDNN_CFG_SKINNY_BF16 = 20,
-    KUDNN_CFG_GEMV_BF16 = 21,  // M == 1: one wave per weight row (skinny engine)
+    KUDNN_CFG_GEMV_BF16 = 21,  // M == 1: one wave per weight row, X staged in LDS (skinny engine)
     KUDNN_CFG_GEMV_MULTI_BF16 = 22,  // 2 <= M <= 5 (M <= 8 forced): one wave per weight row, X staged in LDS
 };
 
@@ -48,8 +48,9 @@ int kudnn_launch_gemm_f32(const GemmOperands &op, const EpiParams &ep, int64_t b
 // of 16, 16-byte aligned operands and row strides; kudnn_kslice_eligible says whether `op` qualifies.
 bool kudnn_kslice_eligible(const GemmOperands &op);
 int kudnn_launch_gemm_f32_kslice(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream);
-// M <= 16, bf16 or f16 operands (`ct`), B contiguous along K (M == 1: row-per-wave GEMV; cfg KUDNN_CFG_GEMV_MULTI_BF16
-// and M <= 8: row-per-wave GEMV with X staged in LDS; otherwise 16-row MFMA tiles).
+// M <= 16, bf16 or f16 operands (`ct`), B contiguous along K (M == 1, and M <= 8 under cfg KUDNN_CFG_GEMV_MULTI_BF16:
+// row-per-wave GEMV with X staged in LDS; otherwise 16-row MFMA tiles; 64-bit addressed forms for operands of 2 GiB or
+// more).
 int kudnn_launch_skinny(const GemmOperands &op, const EpiParams &ep, int64_t batches, int ct, int cfg, hipStream_t stream);
 
 // Pack: dst[b][r][k] (row pitch kp, zero for k >= cols) = convert(src element (b, r, k)) where the source

@@ -5,10 +5,11 @@
 // The reference reaches cblas_sgemv for m == 1 (src/dnn/src/kudnn_gemm.cpp:164-173) and cblas_sbgemm /
 // cblas_bgemm otherwise (:208-241). On MI355X this shape is bound by streaming W from HBM once, so the kernels are
 // organised around the weight stream, not around compute:
-//  - M = 1, gemv_bf16_(compact_)kernel: one wave per weight row, 1 KB of the row per load instruction, a VALU dot
-//    product reduced across the wave;
-//  - 2 <= M <= 5, gemv_multi_(compact_)kernel: one wave per weight row as at M = 1, X's M rows staged once per
-//    8-row workgroup in LDS, M accumulators per lane fed by v_dot2_f32_bf16;
+//  - 1 <= M <= 5, gemv_multi_(compact_)kernel: one wave per weight row, 1 KB of the row per load instruction, X's M
+//    rows staged once per 4- or 8-row workgroup in LDS, M accumulators per lane fed by v_dot2_f32_bf16, reduced across
+//    the wave;
+//  - M = 1 with an operand of 2^31 bytes or more, gemv_bf16_(compact_)kernel: the same row stream with 64-bit
+//    addressing, X loaded by every wave;
 //  - 6 <= M <= 16, skinny_rows_(compact_)kernel: 16 weight rows per workgroup, K split over its waves in blocks of
 //    256; whole-row loads go through a per-wave LDS tile into the operand layout of v_mfma_f32_16x16x32_bf16, X (rows
 //    m < M, cache-resident) is the second operand, and the waves' partial 16 x 16 tiles are summed through LDS;
@@ -121,8 +122,9 @@ __global__ __launch_bounds__(KW * 64) void skinny_bf16_kernel(GemmOperands op, E
     epi_apply4(ep, ob, r16, n, N, v);
 }
 
-// M = 1: one wave per weight row. Lane l reads 16-byte chunks l, l + 64, ... of the row, so every load instruction of
-// a wave reads 1 KB of one row contiguously. (The MFMA operand layout of the kernel above reads 16 rows x 64 bytes per
+// M = 1 with an operand of 2^31 bytes or more (the staged GEMV further below takes the others): one wave per weight row,
+// 64-bit addresses. Lane l reads 16-byte chunks l, l + 64, ... of the row, so every load instruction of a wave reads
+// 1 KB of one row contiguously. (The MFMA operand layout of the kernel above reads 16 rows x 64 bytes per
 // instruction; at M = 1, where the multiply is negligible, the memory system serves that pattern at about 4.9 TB/s
 // against 6.4 TB/s for whole rows, measured on MI355X with the weight streamed from HBM.) K is walked in blocks of
 // 4096 (512 chunks, 8 per lane): X's chunks of the block are loaded first, then the row's, all in flight together;
@@ -611,15 +613,16 @@ inline bool compact_call(const EpiParams &ep, dim3 grid)
     return grid.y == 1 && ep.fast4 && (ep.bin == KUDNN_BINARY_NONE || ep.src_sn == 1);
 }
 
-// 2 <= M <= 5: one wave per weight row as in the M = 1 GEMV (lane l reads 16-byte chunks l, l + 64, ... of its row, 1 KB
-// of the row per load instruction), with M accumulators per lane. The 8 waves of a workgroup stage X's rows into LDS
-// together, in blocks of 512 chunks (4096 elements of K, M x 8 KB), so X is read from L2 once per 8 weight rows instead
-// of once per row; each wave then reads the chunks it needs from LDS (16 contiguous bytes per lane: no bank conflicts).
-// Products are summed with v_dot2_f32_bf16 / _f16 (two products and the accumulator per instruction, no conversions),
-// then across the wave; lane m runs the epilogue of output (m, n), its operands loaded before the K loop.
-// Measured on MI355X (K = 4096, weight streamed from HBM, per step): M = 4, N = 14336 19.9 us against 22.3 us for the
-// row kernel, N = 4096 8.0 against 8.6 us. From M = 6 on the X reads from LDS (M x 8 KB per row) make it slower than
-// the row kernel; two rows per wave sharing each X read, or 4 or 16 waves per workgroup, were slower at every M.
+// 1 <= M <= 5 (up to 8 forced): one wave per weight row (lane l reads 16-byte chunks l, l + 64, ... of its row, 1 KB of
+// the row per load instruction), with M accumulators per lane. The waves of a workgroup stage X's rows into LDS
+// together, in blocks of 512 chunks (4096 elements of K, M x 8 KB), so X is read from L2 once per workgroup instead of
+// once per weight row; each wave then reads the chunks it needs from LDS (16 contiguous bytes per lane: no bank
+// conflicts). Products are summed with v_dot2_f32_bf16 / _f16 (two products and the accumulator per instruction, no
+// conversions), then across the wave; lane m runs the epilogue of output (m, n), its operands loaded before the K loop.
+// Measured on MI355X (K = 4096, weight streamed from HBM, per step): M = 4, N = 14336 19.9 us against 22.2 us for the
+// 16-row MFMA kernel, N = 4096 8.0 against 8.6 us; M = 1, N = 14336 18.4 against 18.9 us for the GEMV that loads X
+// in every wave. From M = 6 on the X reads from LDS (M x 8 KB per row) make it slower than the MFMA kernel; two rows per
+// wave sharing each X read, and 16 waves per workgroup, were slower at every M.
 constexpr int kMgChunks = 512;  // 16-byte chunks of K per staged X block
 constexpr int kMgWaves = 8;     // waves (weight rows) per workgroup
 
@@ -646,10 +649,10 @@ __device__ __forceinline__ float dot_chunk(u32x4_t w, u32x4_t x, float acc)
 
 // The body: MR = M rows of X; FORM = EPI_FORM_GENERIC reads the epilogue's types and activation at run time and takes
 // batches on grid y.
-template <int CT, int MR, int ACT, int FORM>
+template <int CT, int MR, int WV, int ACT, int FORM>
 __device__ __forceinline__ void gemv_multi_body(const GemmOperands &op, const EpiParams &ep)
 {
-    constexpr int kLanes = kMgWaves * 64;
+    constexpr int kLanes = WV * 64;
     constexpr int kXPer = MR * kMgChunks / kLanes;  // staged X chunks per lane and block
     static_assert(kXPer * kLanes == MR * kMgChunks, "the staging covers a block exactly");
     __shared__ u32x4_t xs[MR * kMgChunks];
@@ -658,7 +661,7 @@ __device__ __forceinline__ void gemv_multi_body(const GemmOperands &op, const Ep
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t N = op.N;
-    const int64_t n = static_cast<int64_t>(blockIdx.x) * kMgWaves + wave;
+    const int64_t n = static_cast<int64_t>(blockIdx.x) * WV + wave;
     int64_t aoff = 0, boff = 0;
     EpiBatch ob{0, 0, 0, 0, 0, 0};
     if (FORM == EPI_FORM_GENERIC && gridDim.y > 1) {
@@ -750,37 +753,54 @@ __device__ __forceinline__ void gemv_multi_body(const GemmOperands &op, const Ep
 }
 
 // A single-batch bf16 call in a fixed form: the 128-byte RowsArgs and a compiled-in epilogue.
-template <int CT, int MR, int ACT, int FORM>
-__global__ __launch_bounds__(kMgWaves * 64) void gemv_multi_compact_kernel(RowsArgs r)
+template <int CT, int MR, int WV, int ACT, int FORM>
+__global__ __launch_bounds__(WV * 64) void gemv_multi_compact_kernel(RowsArgs r)
 {
     GemmOperands op;
     EpiParams ep;
     unpack_rows_args<ACT, FORM>(r, op, ep);
-    gemv_multi_body<CT, MR, ACT, FORM>(op, ep);
+    gemv_multi_body<CT, MR, WV, ACT, FORM>(op, ep);
 }
 
 // Any other call: the whole GemmOperands and EpiParams, batches on grid y.
-template <int CT, int MR>
-__global__ __launch_bounds__(kMgWaves * 64) void gemv_multi_kernel(GemmOperands op, EpiParams ep)
+template <int CT, int MR, int WV>
+__global__ __launch_bounds__(WV * 64) void gemv_multi_kernel(GemmOperands op, EpiParams ep)
 {
-    gemv_multi_body<CT, MR, 0, EPI_FORM_GENERIC>(op, ep);
+    gemv_multi_body<CT, MR, WV, 0, EPI_FORM_GENERIC>(op, ep);
 }
 
-template <int CT, int MR>
-void launch_gemv_multi(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream)
+template <int CT, int MR, int WV>
+void launch_gemv_multi_wv(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream)
 {
-    const dim3 grid(static_cast<unsigned>((op.N + kMgWaves - 1) / kMgWaves), static_cast<unsigned>(batches));
-    decltype(&gemv_multi_compact_kernel<CT, MR, 0, EPI_FORM_BF16>) ck = nullptr;
+    const dim3 grid(static_cast<unsigned>((op.N + WV - 1) / WV), static_cast<unsigned>(batches));
+    decltype(&gemv_multi_compact_kernel<CT, MR, WV, 0, EPI_FORM_BF16>) ck = nullptr;
     if constexpr (CT == KUDNN_DT_BF16) {
         ck = pick_compact(ep, compact_call(ep, grid), [](auto actc, auto formc) {
-            return gemv_multi_compact_kernel<CT, MR, decltype(actc)::value, decltype(formc)::value>;
+            return gemv_multi_compact_kernel<CT, MR, WV, decltype(actc)::value, decltype(formc)::value>;
         });
     }
     if (ck != nullptr) {
-        hipLaunchKernelGGL(ck, grid, dim3(kMgWaves * 64), 0, stream, rows_args(op, ep));
+        hipLaunchKernelGGL(ck, grid, dim3(WV * 64), 0, stream, rows_args(op, ep));
     } else {
-        hipLaunchKernelGGL((gemv_multi_kernel<CT, MR>), grid, dim3(kMgWaves * 64), 0, stream, op, ep);
+        hipLaunchKernelGGL((gemv_multi_kernel<CT, MR, WV>), grid, dim3(WV * 64), 0, stream, op, ep);
     }
+}
+
+// Workgroups of 8 waves, or of 4 for M = 1 and for M = 2 from 10240 rows on. Measured on MI355X at K = 4096 over
+// N = 4096 .. 28672: M = 1 with 4 waves 7.2 / 11.7 / 14.8 / 18.4 / 34.7 us at N = 4096 / 8192 / 11008 / 14336 / 28672
+// (8 waves 7.2 / 11.8 / 15.4 / 19.2 / 37.4); M = 2 with 8 waves ahead below 10240 rows (7.3 against 7.5 us at 4096),
+// with 4 from 11008 on (34.2 against 37.2 us at 28672); M = 4 with 8 waves ahead at every N (19.99 against 21.6 us at
+// 14336), as X's share of the workgroup's reads grows with M.
+template <int CT, int MR>
+void launch_gemv_multi(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream)
+{
+    if constexpr (MR <= 2) {
+        if (MR == 1 || op.N * batches >= 10240) {
+            launch_gemv_multi_wv<CT, MR, 4>(op, ep, batches, stream);
+            return;
+        }
+    }
+    launch_gemv_multi_wv<CT, MR, kMgWaves>(op, ep, batches, stream);
 }
 
 // Launches the row kernel of form (KW, PIPE): the compact kernel when the call is single-batch in a fixed form with one
@@ -821,23 +841,28 @@ int launch_skinny(const GemmOperands &op, const EpiParams &ep, int64_t batches, 
     if (op.M > 16) {
         return -1;
     }
+    const int64_t chunks = (op.K + 7) / 8;
+    const bool fits = operand_extent(op.N, op.ldb, chunks) < (int64_t(1) << 31) &&
+                      operand_extent(op.M, op.lda, chunks) < (int64_t(1) << 31);
+    // M = 1 (any configuration) and the staged configuration up to M = 8: the GEMV with X staged in LDS; an M = 1
+    // operand of 2^31 bytes or more takes the GEMV with 64-bit addressing
+    if (fits && (op.M == 1 || (cfg == KUDNN_CFG_GEMV_MULTI_BF16 && op.M <= 8)) && op.N <= (int64_t(1) << 31) - kMgWaves) {
+        switch (op.M) {
+            case 1: launch_gemv_multi<CT, 1>(op, ep, batches, stream); break;
+            case 2: launch_gemv_multi<CT, 2>(op, ep, batches, stream); break;
+            case 3: launch_gemv_multi<CT, 3>(op, ep, batches, stream); break;
+            case 4: launch_gemv_multi<CT, 4>(op, ep, batches, stream); break;
+            case 5: launch_gemv_multi<CT, 5>(op, ep, batches, stream); break;
+            case 6: launch_gemv_multi<CT, 6>(op, ep, batches, stream); break;
+            case 7: launch_gemv_multi<CT, 7>(op, ep, batches, stream); break;
+            default: launch_gemv_multi<CT, 8>(op, ep, batches, stream); break;
+        }
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
     if (gemv_eligible(op)) {
         return launch_gemv<CT>(op, ep, batches, stream);
     }
-    const int64_t chunks = (op.K + 7) / 8;
-    if (operand_extent(op.N, op.ldb, chunks) < (int64_t(1) << 31) && operand_extent(op.M, op.lda, chunks) < (int64_t(1) << 31)) {
-        if (cfg == KUDNN_CFG_GEMV_MULTI_BF16 && op.M <= 8 && op.N <= (int64_t(1) << 31) - kMgWaves) {
-            switch (op.M) {
-                case 2: launch_gemv_multi<CT, 2>(op, ep, batches, stream); break;
-                case 3: launch_gemv_multi<CT, 3>(op, ep, batches, stream); break;
-                case 4: launch_gemv_multi<CT, 4>(op, ep, batches, stream); break;
-                case 5: launch_gemv_multi<CT, 5>(op, ep, batches, stream); break;
-                case 6: launch_gemv_multi<CT, 6>(op, ep, batches, stream); break;
-                case 7: launch_gemv_multi<CT, 7>(op, ep, batches, stream); break;
-                default: launch_gemv_multi<CT, 8>(op, ep, batches, stream); break;
-            }
-            return hipGetLastError() == hipSuccess ? 0 : -1;
-        }
+    if (fits) {
         // fewer than 2 row groups per CU: split K over 16 waves (one workgroup per CU); otherwise 8 (two per CU)
         const int64_t groups = (op.N + 15) / 16 * batches;
         // measured at M = 4 and 16, N = 4096 and 14336, K = 4096: with more than 8 rows of X, 2-wave workgroups with

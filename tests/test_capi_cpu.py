@@ -155,16 +155,17 @@ def test_batch_dim_of_output_must_match_operands():
 
 
 def test_decode_kernel_rule(monkeypatch):
-    # M = 1: the GEMV; 2 <= M <= 5: the GEMV with X staged in LDS; 6 <= M <= 16: 16-row MFMA tiles (bf16 and f16)
+    # M <= 5: the GEMV with X staged in LDS (M = 1 named apart); 6 <= M <= 16: 16-row MFMA tiles (bf16 and f16)
     assert plan_of(1, 4096, 4096).describe().startswith("skinny_bf16_gemv_row ")
     for M in (2, 3, 4, 5):
         assert plan_of(M, 4096, 14336).describe().startswith("skinny_bf16_gemv_rows_xlds"), M
         assert plan_of(M, 1000, 300, K.F16).describe().startswith("skinny_f16_gemv_rows_xlds"), M
     for M in (6, 8, 16):
         assert plan_of(M, 4096, 14336).describe().startswith("skinny_bf16_16xK"), M
-    # the overrides: the 16-row kernel at any M <= 16, the staged GEMV for 2 <= M <= 8 only
+    # the overrides: the 16-row kernel for 2 <= M <= 16, the staged GEMV for 2 <= M <= 8
     monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "20")
     assert plan_of(4, 4096, 4096).describe().startswith("skinny_bf16_16xK")
+    assert plan_of(1, 4096, 4096).describe().startswith("skinny_bf16_gemv_row ")
     monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "22")
     assert plan_of(8, 4096, 4096).describe().startswith("skinny_bf16_gemv_rows_xlds")
     assert plan_of(9, 4096, 4096).describe().startswith("skinny_bf16_16xK")
