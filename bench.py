@@ -19,7 +19,8 @@ decode lines, and --only copy runs an
 elementwise copy-like kernel (y = -x, 512 MiB bf16 in, 512 MiB out) whose known traffic calibrates the
 FETCH_SIZE / WRITE_SIZE counters against which the C3 kernel's HBM traffic is read. --only dispatch times a bf16
 Linear + GELU(tanh) over prefill-like shapes under every kernel configuration (forced through KUDNN_HIP_FORCE_CFG and
-KUDNN_HIP_FORCE_STREAMK) and under the planner's own choice, one JSON line per shape, then an f32 Gemm over grids of
+KUDNN_HIP_FORCE_STREAMK, K slices by the planner's rule or none through KUDNN_HIP_FORCE_KSLICES) and under the
+planner's own choice, one JSON line per shape, then an f32 Gemm over grids of
 256-640 tiles of 128 x 128 under the 128 x 128 and 64 x 64 configurations: the measurements the dispatcher's rules are
 drawn from. --only refperf times KuDNN::Gemm on the reference's own perf shape sets (the matmul gtest's freParas and
 freParasMulti) in f32 and bf16, under the planner and under every forced configuration, one JSON line per shape and
@@ -426,8 +427,9 @@ def _with_env(settings):
 def bench_dispatch(args, torch, K):
     """Every bf16 kernel configuration against the planner's choice over prefill-like shapes (microseconds per call;
     CUDA events around `--steps` back-to-back calls after 30 ms and `--warmup` calls untimed)."""
-    configs = [("pingpong", "4", "0"), ("pingpong_split", "4", "1"), ("4wave_256x128", "2", "0"),
-               ("4wave_128x128", "3", "0"), ("4wave_256x256", "1", "0"), ("planner", None, None)]
+    configs = [("pingpong", "4", "0", "0"), ("pingpong_split", "4", "1", "0"), ("pingpong_kslices", "4", "0", None),
+               ("4wave_256x128", "2", "0", None), ("4wave_128x128", "3", "0", None), ("4wave_256x256", "1", "0", None),
+               ("planner", None, None, None)]
     g = torch.Generator(device="cuda").manual_seed(0)
     for M in (256, 512, 1024, 2048, 3072):
         for N, Kd in ((4096, 4096), (11008, 4096), (4096, 11008), (14336, 4096), (4096, 14336), (2048, 2048),
@@ -436,8 +438,9 @@ def bench_dispatch(args, torch, K):
             w = (torch.randn(N, Kd, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
             y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
             line = {"M": M, "N": N, "K": Kd}
-            for name, cfg, split in configs:
-                saved = _with_env((("KUDNN_HIP_FORCE_CFG", cfg), ("KUDNN_HIP_FORCE_STREAMK", split)))
+            for name, cfg, split, slices in configs:
+                saved = _with_env((("KUDNN_HIP_FORCE_CFG", cfg), ("KUDNN_HIP_FORCE_STREAMK", split),
+                                   ("KUDNN_HIP_FORCE_KSLICES", slices)))
                 plan = K.LinearPostOps(K.desc([M, Kd], K.BF16), K.desc([Kd, N], K.BF16, "BA"), K.desc([M, N], K.BF16),
                                        None, act=K.ACT_GELU_TANH)
                 line[name] = round(_time_calls(lambda: plan.run(x, w, y), args.steps, args.warmup, torch), 1)
@@ -459,9 +462,9 @@ def bench_refperf(args, torch, K):
     """KuDNN::Gemm on the reference's perf shapes, f32 and bf16, with the weight [K][N] as the reference's Matmul mode
     stores it: the planner's choice and every forced configuration (microseconds per call; CUDA events around
     `--steps` back-to-back calls after 30 ms and `--warmup` calls untimed)."""
-    bf16_cfgs = [("ping-pong", "4", "0"), ("ping-pong + K-split", "4", "1"), ("4-wave 256x128", "2", "0"),
-                 ("4-wave 128x128", "3", "0"), ("4-wave 256x256", "1", "0")]
-    f32_cfgs = [("128x128", "10", None), ("64x64", "11", None)]
+    bf16_cfgs = [("ping-pong", "4", "0", "0"), ("ping-pong + K-split", "4", "1", "0"), ("ping-pong + K slices", "4", "0", None),
+                 ("4-wave 256x128", "2", "0", None), ("4-wave 128x128", "3", "0", None), ("4-wave 256x256", "1", "0", None)]
+    f32_cfgs = [("128x128", "10", None, None), ("64x64", "11", None, None)]
     g = torch.Generator(device="cuda").manual_seed(0)
     out = []
     for M, N, Kd in REF_PERF_SHAPES:
@@ -472,8 +475,9 @@ def bench_refperf(args, torch, K):
             b = (torch.randn(1, N, device="cuda", generator=g) * 0.02).to(tdt)
             y = torch.empty(M, N, device="cuda", dtype=tdt)
             line = {"M": M, "N": N, "K": Kd, "dtype": name}
-            for cname, cfg, split in [("planner", None, None)] + cfgs:
-                saved = _with_env((("KUDNN_HIP_FORCE_CFG", cfg), ("KUDNN_HIP_FORCE_STREAMK", split)))
+            for cname, cfg, split, slices in [("planner", None, None, None)] + cfgs:
+                saved = _with_env((("KUDNN_HIP_FORCE_CFG", cfg), ("KUDNN_HIP_FORCE_STREAMK", split),
+                                   ("KUDNN_HIP_FORCE_KSLICES", slices)))
                 plan = K.Gemm(K.desc([M, Kd], kdt), K.desc([Kd, N], kdt), K.desc([M, N], kdt), K.desc([1, N], kdt))
                 us = _time_calls(lambda: plan.run(x, w, y, b), args.steps, args.warmup, torch)
                 _with_env(saved.items())

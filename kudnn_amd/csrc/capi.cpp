@@ -555,12 +555,16 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
             // Measured on MI355X over prefill-like shapes (M 256..3072, N and K 2048..14336): the ping-pong kernel
             // wins from about 80 tiles of 256 x 256 on, even when they fill only part of the 256 CUs (a partly busy
             // chip runs each CU faster); with fewer tiles it still wins when K is long enough for its tail split
-            // (every tile divided over the CUs along K: at most half the CUs would be busy, at least 128 k-tiles, 24 or
-            // more per CU); otherwise the 4-wave 128 x 128 kernel, whose smaller tiles and split-K spread a small grid.
+            // (every tile divided over the CUs along K: at most a quarter of the CUs would be busy, at least 128
+            // k-tiles, 24 or more per CU; s8 only now, the 16-bit types take K slices there); otherwise the 4-wave
+            // 128 x 128 kernel, whose smaller tiles and split-K spread a small grid.
+            // Small grids of 16-bit operands split K into slices instead (kudnn_kslice_rule): the ping-pong kernel
+            // then runs one workgroup per tile and slice and a second launch adds the slices.
             const int64_t t256 = (core.M + 255) / 256 * ((core.N + 255) / 256) * batches;
             const int64_t kt = core.kp * DtSize(core.computeDt) / 128;
-            const bool tailSplit = batches == 1 && t256 * 2 <= 256 && kt >= 128 && (t256 * kt + 255) / 256 >= 24;
-            core.cfg = t256 >= 80 || tailSplit ? KUDNN_CFG_BF16_PINGPONG_256x256 : KUDNN_CFG_BF16_128x128;
+            const bool tailSplit = batches == 1 && t256 <= 64 && kt >= 128 && (t256 * kt + 255) / 256 >= 24;
+            const bool slices = kudnn_kslice_rule(core.M, core.N, kt, batches, core.computeDt) >= 2;
+            core.cfg = t256 >= 80 || tailSplit || slices ? KUDNN_CFG_BF16_PINGPONG_256x256 : KUDNN_CFG_BF16_128x128;
         }
     } else {
         core.engine = ENGINE_MFMA_F32;
@@ -648,9 +652,13 @@ std::string DescribeCore(const GemmCore &c)
         shape.M = c.M;
         shape.N = c.N;
         shape.K = c.kp;
+        shape.b_kmajor = c.B.kmajor ? 1 : 0;
         int dp = 0, tail = 0, iters = 0;
+        const int slices = kudnn_pingpong_slices(shape, c.Batches(), c.computeDt);
         kudnn_pingpong_split(shape, c.Batches(), c.computeDt, &dp, &tail, &iters);
-        if (tail > 0) {
+        if (slices >= 2) {
+            std::snprintf(split, sizeof(split), " kslices=%d", slices);
+        } else if (tail > 0) {
             std::snprintf(split, sizeof(split), " split=%d+%d/%d", dp, tail, iters);
         }
     }
@@ -708,6 +716,9 @@ public:
     }
     Workspace(const Workspace &) {}
     Workspace &operator=(const Workspace &) { return *this; }
+    // Whether this is the fixed memory of the allocation-free entry point, and its size.
+    bool Fixed() const { return fixed_ != nullptr; }
+    size_t FixedBytes() const { return fixedBytes_; }
     ~Workspace()
     {
         if (ptr_ != nullptr) {
@@ -903,7 +914,10 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
     const size_t wsS = mfma4 ? align256(kudnn_gemm_workspace_bytes(shape, batches, core.cfg, core.computeDt)) : 0;
     // the ping-pong kernel's tail split: partial tiles and arrival counters
     const bool pingpong = core.engine == ENGINE_MFMA_BF16 && core.cfg == KUDNN_CFG_BF16_PINGPONG_256x256;
-    const size_t wsK = pingpong ? align256(kudnn_pingpong_workspace_bytes(shape, batches, core.computeDt)) : 0;
+    // K slices write f32 sums of the whole output per slice; in the fixed scratch of the allocation-free entry point
+    // only when they fit (else the launch runs without them)
+    bool slicesOk = true;
+    size_t wsK = pingpong ? align256(kudnn_pingpong_workspace_bytes(shape, batches, core.computeDt, true)) : 0;
     void *ws = nullptr;
     bool acquired = false;
     // u8 operands of an integer GEMM: correction vectors (row sums of the other packed operand, scaled by 128)
@@ -912,6 +926,10 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
     const int64_t copiesA = allBroadcast(core.A) ? 1 : batches, copiesB = allBroadcast(core.B) ? 1 : batches;
     const size_t wsCm = bU8 ? align256(static_cast<size_t>(copiesA * core.M) * sizeof(int32_t)) : 0;
     const size_t wsCn = aU8 ? align256(static_cast<size_t>(copiesB * core.N) * sizeof(int32_t)) : 0;
+    if (pingpong && wsp.Fixed() && wsA + wsB + wsS + wsK + wsCm + wsCn > wsp.FixedBytes()) {
+        slicesOk = false;
+        wsK = align256(kudnn_pingpong_workspace_bytes(shape, batches, core.computeDt, false));
+    }
     uint32_t *counters = nullptr;
     if (wsA + wsB + wsS + wsK + wsCm + wsCn > 0) {
         int arc = KUDNN_STATUS_SUCCESS;
@@ -1033,7 +1051,7 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
         lrc = kudnn_launch_skinny(op, ep, batches, core.computeDt, core.cfg, stream);
     } else if (core.engine == ENGINE_MFMA_BF16) {
         if (core.cfg == KUDNN_CFG_BF16_PINGPONG_256x256 && kudnn_pingpong_eligible(op, core.computeDt)) {
-            lrc = kudnn_launch_gemm_pingpong(op, ep, batches, core.computeDt, tailWs, stream);
+            lrc = kudnn_launch_gemm_pingpong(op, ep, batches, core.computeDt, tailWs, slicesOk, stream);
         } else if (op.b_kmajor) {
             // only the ping-pong kernel reads a K-major B (the plan's conditions make it eligible)
             return Fail(KUDNN_STATUS_UNSUPPORTED, "GEMM: a K-major weight the ping-pong kernel cannot address");

@@ -274,9 +274,9 @@ __device__ __forceinline__ EpiBatch epi_batch_offsets(const EpiParams &e, int64_
 }
 
 // Epilogue forms (the types of every epilogue tensor, fixed at compile time in the fast paths): all bf16, all f32,
-// all f16, or read at run time; EPI_FORM_I32 is the integer epilogue of s8 x s8 -> s32 (further below). Value 3 is
-// taken by the split-K partial stores of gemm_mfma.hip.
-enum { EPI_FORM_BF16 = 0, EPI_FORM_F32 = 1, EPI_FORM_GENERIC = 2, EPI_FORM_I32 = 4, EPI_FORM_F16 = 5 };
+// all f16, or read at run time; EPI_FORM_I32 is the integer epilogue of s8 x s8 -> s32 (further below);
+// EPI_FORM_PARTIAL stores a K slice's f32 sums and no epilogue (the ping-pong kernel's K slices).
+enum { EPI_FORM_BF16 = 0, EPI_FORM_F32 = 1, EPI_FORM_GENERIC = 2, EPI_FORM_PARTIAL = 3, EPI_FORM_I32 = 4, EPI_FORM_F16 = 5 };
 
 template <int FORM>
 constexpr int form_dt()

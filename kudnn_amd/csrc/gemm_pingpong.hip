@@ -324,6 +324,43 @@ __device__ __forceinline__ void epilogue_int(const EpiParams &ep, const EpiBatch
     });
 }
 
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// A K slice's sums of a tile, stored as f32 rows (pitch ld floats) through the same staging as the epilogues: lane ->
+// row rl + 16 * pass, columns col8 .. +8 of each strip, two 16-byte non-temporal stores; an edge tile stores only its
+// elements inside the matrix.
+__device__ __forceinline__ void epilogue_partial(float *out, int64_t ld, const f32x16_t (&acc)[4][2], float *stage,
+                                                 int lane, int64_t mW, int64_t nW, int64_t M, int64_t N)
+{
+    const int lrow = lane & 31, lh = lane >> 5;
+    const int col8 = (lane & 3) * 8, rl = lane >> 2;
+    __syncthreads();  // every wave is done with the tile buffers that the staging area reuses
+    sfor<4>([&](auto jc) __attribute__((always_inline)) {
+        constexpr int j = decltype(jc)::value;
+        const int64_t n = nW + j * 32 + col8;
+        stage_strip(acc[j], stage, lrow, lh);
+        wave_sync();
+#pragma unroll
+        for (int ps = 0; ps < 4; ++ps) {
+            const int r = rl + ps * 16;
+            const int64_t m = mW + r;
+            const float *src = stage + r * kPitch + col8;
+            float *dst = out + m * ld + n;
+            if (m < M && n + 7 < N) {
+                __builtin_nontemporal_store(*reinterpret_cast<const v4f *>(src), reinterpret_cast<v4f *>(dst));
+                __builtin_nontemporal_store(*reinterpret_cast<const v4f *>(src + 4), reinterpret_cast<v4f *>(dst + 4));
+            } else if (m < M) {
+                for (int q = 0; q < 8; ++q) {
+                    if (n + q < N) {
+                        dst[q] = src[q];
+                    }
+                }
+            }
+        }
+        wave_sync();
+    });
+}
+
 // Tail split of the grid. Whole rounds of tiles (one tile per CU) run data-parallel, one workgroup per tile. The
 // k-iterations of the remaining tiles are divided evenly between one workgroup per CU (a second launch), so the last
 // round ends with every CU busy instead of (tiles mod CUs) of them. A tile whose iterations span several workgroups
@@ -342,6 +379,11 @@ struct SkArgs {
     int nTail;      // tiles of the tail
     int L;          // k-iterations per tail workgroup (the last one may have fewer)
     int maxc;       // slots per tail tile: the most workgroups any tail tile spans
+    // K slices (EPI_FORM_PARTIAL): slice z of every tile sums k-tiles z * sliceKT .. + sliceKT - 1 and stores them to
+    // slices + z * sliceFloats, row pitch sliceLd floats
+    float *slices;
+    int64_t sliceFloats, sliceLd;
+    int sliceKT, nSlices;
 };
 
 constexpr int kSlotFloats = kBM * kBN;  // one 256 x 256 accumulator tile
@@ -650,14 +692,30 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
             epilogue_int(ep, ob, acc, stage, lane, mW, nW, M, N);
         } else if constexpr (FORM == EPI_FORM_GENERIC) {
             epilogue_generic(ep, ob, acc, stage, lane, mW, nW, M, N);
-        } else if (m0 + kBM <= M && n0 + kBN <= N && (ep.bias == nullptr || ep.bias_sm == 0)) {
-            epilogue_full<ACT, FORM>(ep, ob, acc, stage, lane, mW, nW);
-        } else {
-            epilogue_edge<ACT, FORM>(ep, ob, acc, stage, lane, mW, nW, M, N);
+        } else if constexpr (FORM != EPI_FORM_PARTIAL) {
+            if (m0 + kBM <= M && n0 + kBN <= N && (ep.bias == nullptr || ep.bias_sm == 0)) {
+                epilogue_full<ACT, FORM>(ep, ob, acc, stage, lane, mW, nW);
+            } else {
+                epilogue_edge<ACT, FORM>(ep, ob, acc, stage, lane, mW, nW, M, N);
+            }
         }
     };
 
-    if constexpr (!SK) {
+    if constexpr (!SK && FORM == EPI_FORM_PARTIAL) {
+        // K slices: logical block z * tiles + t (consecutive logical blocks share an XCD, so one XCD's workgroups work
+        // on neighbouring tiles of one slice and share its A and B panels in L2)
+        const int tiles = tilesM * tilesN;
+        const int lid = xcd_remap(blockIdx.x, gridDim.x);
+        const int z = lid / tiles;
+        int tm, tn;
+        grouped_tile(lid - z * tiles, tilesM, tilesN, group, tm, tn);
+        m0 = tm * kBM;
+        n0 = tn * kBN;
+        kb = z * sk.sliceKT;
+        nk = min(sk.sliceKT, KT - kb);
+        mainloop();
+        epilogue_partial(sk.slices + z * sk.sliceFloats, sk.sliceLd, acc, stage, lane, m0 + p * 64, n0 + g * 128, M, N);
+    } else if constexpr (!SK) {
         int tm, tn;
         grouped_tile(xcd_remap(blockIdx.x, gridDim.x), tilesM, tilesN, group, tm, tn);
         m0 = tm * kBM;
@@ -820,8 +878,9 @@ int cu_count()
     return cus;
 }
 
-// The tail split pays only for grids of at most half the CUs with long K (at least 128 k-tiles, 24 or more per
-// workgroup), measured on MI355X. Behind whole rounds of tiles it loses: the tail's workgroups start at k offsets
+// The tail split pays only for grids of at most a quarter of the CUs with long K (at least 128 k-tiles, 24 or more
+// per workgroup), measured on MI355X: at 128 tiles it lost to the unsplit launch (1024 x 8192 x 8192: 158 against
+// 141 us), and for 16-bit operands the K slices beat it below (512 x 4096 x 14336: 83 against 156 us). Behind whole rounds of tiles it loses: the tail's workgroups start at k offsets
 // spread over the whole K range, so they no longer read the same A and B panels at the same time as their XCD's
 // other workgroups, and the copies that then miss the L2 cost more than the idle CUs did (C3: 441 us split against
 // 324 us unsplit). KUDNN_HIP_FORCE_STREAMK=1 forces it for any tail (tests), =0 turns it off.
@@ -844,7 +903,7 @@ SkPlan sk_plan(const GemmOperands &op, int64_t batches, int ct)
     const int64_t tiles = ((op.M + kBM - 1) / kBM) * ((op.N + kBN - 1) / kBN);
     const int KT = static_cast<int>(op.K * es / kRowBytes);
     const int rem = static_cast<int>(tiles % cus);
-    if (rem == 0 || (force != 1 && (tiles != rem || rem * 2 > cus || KT < 128))) {
+    if (rem == 0 || (force != 1 && (tiles != rem || rem * 4 > cus || KT < 128))) {
         return s;
     }
     const int64_t total = static_cast<int64_t>(rem) * KT;
@@ -864,6 +923,113 @@ SkPlan sk_plan(const GemmOperands &op, int64_t batches, int ct)
     s.slotBytes = align256(static_cast<size_t>(rem) * maxc * kSlotFloats * sizeof(float));
     s.bytes = s.slotBytes + align256(static_cast<size_t>(rem) * sizeof(uint32_t));
     return s;
+}
+
+// K slices of a small grid: every tile's k-tiles are divided into S slices of sliceKT, one workgroup per (tile, slice),
+// all run by the data-parallel kernel's own loop; each stores its f32 sums, and slice_reduce_kernel adds the S slices
+// of every output element in slice order and runs the epilogue. Unlike the tail split, no workgroup waits on or reads
+// another's results inside the launch, and the slices' workgroups keep the data-parallel copy path and L2 sharing.
+// S from kudnn_kslice_rule; KUDNN_HIP_FORCE_KSLICES=S forces S slices (0: none).
+struct SlicePlan {
+    int S = 0, sliceKT = 0;
+    int64_t ld = 0;
+    size_t bytes = 0;
+};
+
+SlicePlan slice_plan(const GemmOperands &op, int64_t batches, int ct)
+{
+    SlicePlan s;
+    if (batches != 1 || ct == KUDNN_DT_S8 || op.K <= 0 || (op.K * 2) % kRowBytes != 0) {
+        return s;
+    }
+    const int KT = static_cast<int>(op.K * 2 / kRowBytes);
+    const char *f = std::getenv("KUDNN_HIP_FORCE_KSLICES");
+    int S = f != nullptr ? std::atoi(f) : kudnn_kslice_rule(op.M, op.N, KT, batches, ct);
+    if (S < 2) {
+        return s;
+    }
+    S = std::min(S, KT);
+    s.sliceKT = (KT + S - 1) / S;
+    s.S = (KT + s.sliceKT - 1) / s.sliceKT;  // no empty slice
+    if (s.S < 2) {
+        return SlicePlan{};
+    }
+    s.ld = (op.N + 7) / 8 * 8;
+    s.bytes = align256(static_cast<size_t>(s.S) * static_cast<size_t>(op.M) * static_cast<size_t>(s.ld) * sizeof(float));
+    return s;
+}
+
+// One thread per run of 8 columns (m, n .. n + 7): the sum of the S slices in slice order, then the epilogue of FORM.
+template <int ACT, int FORM>
+__global__ __launch_bounds__(256) void slice_reduce_kernel(const float *slices, int64_t sliceFloats, int64_t ld, int S,
+                                                           int64_t M, int64_t N, EpiParams ep)
+{
+    const int64_t groupsN = (N + 7) / 8;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= M * groupsN) {
+        return;
+    }
+    const int64_t m = idx / groupsN, n = (idx - m * groupsN) * 8;
+    const float *src = slices + m * ld + n;
+    const EpiBatch ob{0, 0, 0, 0, 0, 0};
+    float v[8];
+    if (n + 7 < N) {
+        v4f lo = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(src));
+        v4f hi = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(src + 4));
+        for (int z = 1; z < S; ++z) {
+            lo += __builtin_nontemporal_load(reinterpret_cast<const v4f *>(src + z * sliceFloats));
+            hi += __builtin_nontemporal_load(reinterpret_cast<const v4f *>(src + z * sliceFloats + 4));
+        }
+        v[0] = lo[0]; v[1] = lo[1]; v[2] = lo[2]; v[3] = lo[3];
+        v[4] = hi[0]; v[5] = hi[1]; v[6] = hi[2]; v[7] = hi[3];
+        if constexpr (FORM == EPI_FORM_GENERIC) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) epi_apply(ep, ob, m, n + q, v[q]);
+        } else {
+            epi_fast8<ACT, FORM>(ep, ob, m, n, v, epi_prefetch8<FORM>(ep, ob, m, n));
+        }
+        return;
+    }
+    for (int q = 0; n + q < N; ++q) {
+        float x = src[q];
+        for (int z = 1; z < S; ++z) x += src[z * sliceFloats + q];
+        if constexpr (FORM == EPI_FORM_GENERIC) {
+            epi_apply(ep, ob, m, n + q, x);
+        } else {
+            epi_elem<ACT, FORM>(ep, ob, m, n + q, x);
+        }
+    }
+}
+
+using SliceReduceKernel = decltype(&slice_reduce_kernel<0, EPI_FORM_GENERIC>);
+
+// The reduce instance of the epilogue's activation and tensor types (the generic one for the others).
+template <int CT>
+SliceReduceKernel select_slice_reduce(const EpiParams &ep)
+{
+    SliceReduceKernel kernel = nullptr;
+    const int form = epi_form(ep);
+    auto pick = [&](auto formc) {
+        constexpr int F = decltype(formc)::value;
+        switch (ep.act) {
+            case KUDNN_ACT_UNIMPLEMENTED: kernel = slice_reduce_kernel<KUDNN_ACT_UNIMPLEMENTED, F>; break;
+            case KUDNN_ACT_RELU: kernel = slice_reduce_kernel<KUDNN_ACT_RELU, F>; break;
+            case KUDNN_ACT_SWISH: kernel = slice_reduce_kernel<KUDNN_ACT_SWISH, F>; break;
+            case KUDNN_ACT_GELU_TANH: kernel = slice_reduce_kernel<KUDNN_ACT_GELU_TANH, F>; break;
+            case KUDNN_ACT_GELU_ERF: kernel = slice_reduce_kernel<KUDNN_ACT_GELU_ERF, F>; break;
+            default: break;
+        }
+    };
+    if constexpr (CT == KUDNN_DT_BF16) {
+        if (form == EPI_FORM_BF16) {
+            pick(std::integral_constant<int, EPI_FORM_BF16>{});
+        } else if (form == EPI_FORM_F32) {
+            pick(std::integral_constant<int, EPI_FORM_F32>{});
+        }
+    } else if (form == EPI_FORM_F16) {
+        pick(std::integral_constant<int, EPI_FORM_F16>{});
+    }
+    return kernel != nullptr ? kernel : slice_reduce_kernel<0, EPI_FORM_GENERIC>;
 }
 
 using PingpongKernel = decltype(&gemm_pingpong_kernel<KUDNN_DT_BF16, 0, EPI_FORM_GENERIC, false>);
@@ -911,10 +1077,30 @@ PingpongKernel select_pingpong(const EpiParams &ep)
 }
 
 template <int CT>
-int launch_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, void *ws, hipStream_t stream)
+int launch_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, void *ws, bool slicesOk,
+                    hipStream_t stream)
 {
     const int tilesM = static_cast<int>((op.M + kBM - 1) / kBM);
     const int tilesN = static_cast<int>((op.N + kBN - 1) / kBN);
+    if constexpr (CT != KUDNN_DT_S8) {
+        const SlicePlan sl = ws != nullptr && slicesOk ? slice_plan(op, batches, CT) : SlicePlan{};
+        if (sl.S >= 2) {
+            SkArgs args{};
+            args.slices = static_cast<float *>(ws);
+            args.sliceFloats = op.M * sl.ld;
+            args.sliceLd = sl.ld;
+            args.sliceKT = sl.sliceKT;
+            args.nSlices = sl.S;
+            const PingpongKernel part = op.b_kmajor ? gemm_pingpong_kernel<CT, 0, EPI_FORM_PARTIAL, false, true>
+                                                    : gemm_pingpong_kernel<CT, 0, EPI_FORM_PARTIAL, false, false>;
+            hipLaunchKernelGGL(part, dim3(static_cast<unsigned>(tilesM * tilesN * sl.S)), dim3(512), 0, stream, op, ep,
+                               tilesM, tilesN, 8, args);
+            const int64_t threads = op.M * ((op.N + 7) / 8);
+            hipLaunchKernelGGL(select_slice_reduce<CT>(ep), dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256),
+                               0, stream, static_cast<const float *>(ws), args.sliceFloats, sl.ld, sl.S, op.M, op.N, ep);
+            return hipGetLastError() == hipSuccess ? 0 : -1;
+        }
+    }
     const SkPlan s = ws != nullptr ? sk_plan(op, batches, CT) : SkPlan{};
     SkArgs args{};
     if (s.nTail > 0) {
@@ -950,9 +1136,15 @@ int launch_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches
 
 }  // namespace
 
-size_t kudnn_pingpong_workspace_bytes(const GemmOperands &op, int64_t batches, int ct)
+size_t kudnn_pingpong_workspace_bytes(const GemmOperands &op, int64_t batches, int ct, bool slicesOk)
 {
-    return sk_plan(op, batches, ct).bytes;
+    const SlicePlan sl = slicesOk ? slice_plan(op, batches, ct) : SlicePlan{};
+    return sl.S >= 2 ? sl.bytes : sk_plan(op, batches, ct).bytes;
+}
+
+int kudnn_pingpong_slices(const GemmOperands &op, int64_t batches, int ct)
+{
+    return slice_plan(op, batches, ct).S;
 }
 
 void kudnn_pingpong_split(const GemmOperands &op, int64_t batches, int ct, int *dpTiles, int *tailTiles, int *iters)
@@ -964,15 +1156,15 @@ void kudnn_pingpong_split(const GemmOperands &op, int64_t batches, int ct, int *
 }
 
 int kudnn_launch_gemm_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, int ct, void *ws,
-                               hipStream_t stream)
+                               bool slicesOk, hipStream_t stream)
 {
     if (!kudnn_pingpong_eligible(op, ct)) {
         return -1;
     }
     switch (ct) {
-        case KUDNN_DT_BF16: return launch_pingpong<KUDNN_DT_BF16>(op, ep, batches, ws, stream);
-        case KUDNN_DT_F16: return launch_pingpong<KUDNN_DT_F16>(op, ep, batches, ws, stream);
-        case KUDNN_DT_S8: return launch_pingpong<KUDNN_DT_S8>(op, ep, batches, ws, stream);
+        case KUDNN_DT_BF16: return launch_pingpong<KUDNN_DT_BF16>(op, ep, batches, ws, slicesOk, stream);
+        case KUDNN_DT_F16: return launch_pingpong<KUDNN_DT_F16>(op, ep, batches, ws, slicesOk, stream);
+        case KUDNN_DT_S8: return launch_pingpong<KUDNN_DT_S8>(op, ep, batches, ws, slicesOk, stream);
         default: return -1;
     }
 }

@@ -34,14 +34,42 @@ int kudnn_launch_gemm_mfma(const GemmOperands &op, const EpiParams &ep, int64_t 
 // 8-wave ping-pong schedule, 256x256 tile (gemm_pingpong.hip). Needs K a whole number of 128-byte k-tiles, 16-byte
 // aligned rows and 32-bit operand offsets; kudnn_pingpong_eligible says whether `op` qualifies.
 bool kudnn_pingpong_eligible(const GemmOperands &op, int ct);
-// Bytes of workspace the launch wants for its tail split (0: one data-parallel launch); `ws` of at least that many
-// bytes, or nullptr to run without the split.
-size_t kudnn_pingpong_workspace_bytes(const GemmOperands &op, int64_t batches, int ct);
+// Bytes of workspace the launch wants for its K slices (slicesOk) or its tail split (0: one data-parallel launch);
+// `ws` of at least that many bytes, or nullptr to run without either. The launch takes the same slicesOk.
+size_t kudnn_pingpong_workspace_bytes(const GemmOperands &op, int64_t batches, int ct, bool slicesOk);
 // The split the launch would make: tiles of the data-parallel launch, tail tiles, k-iterations per tail workgroup
 // (all 0 when it makes none).
 void kudnn_pingpong_split(const GemmOperands &op, int64_t batches, int ct, int *dpTiles, int *tailTiles, int *iters);
+// The K slices the launch would make when allowed (0: none).
+int kudnn_pingpong_slices(const GemmOperands &op, int64_t batches, int ct);
+// The planner's K-slice count for the ping-pong kernel (0: none) of an M x N grid with KT k-tiles of 128 bytes.
+// Measured on MI355X over 26 shapes (M 256..4096, N 1152..14336, K 2048..14336, against the unsliced ping-pong, its
+// tail split and the 4-wave kernel): up to 64 tiles of 256 x 256, as many slices as keep tiles x slices <= 128 (at
+// most 8), each of at least 16 k-tiles, were 1.07-2.4x faster than the best of those, except at 64 tiles with fewer
+// than 64 k-tiles, where the 4-wave kernel's 128 x 128 tiles fill the CUs (2048 x 2048 x 2048: 49 against 38 us);
+// 80-96 tiles with M >= 1024 and at least 48 k-tiles: two slices, 7-23 % faster (M = 512 lost 3 %, 112-128 tiles up
+// to 47 %).
+inline int kudnn_kslice_rule(int64_t M, int64_t N, int64_t KT, int64_t batches, int ct)
+{
+    if (batches != 1 || ct == KUDNN_DT_S8 || M <= 0 || N <= 0) {
+        return 0;
+    }
+    const int64_t tiles = (M + 255) / 256 * ((N + 255) / 256);
+    int64_t S = 0;
+    if (tiles <= 64) {
+        S = 128 / tiles;
+        S = S < 8 ? S : 8;
+        S = S < KT / 16 ? S : KT / 16;
+        if (tiles * 4 >= 256 && KT < 64) {
+            S = 0;
+        }
+    } else if (tiles <= 96 && M >= 1024 && KT >= 48) {
+        S = 2;
+    }
+    return S >= 2 ? static_cast<int>(S) : 0;
+}
 int kudnn_launch_gemm_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, int ct, void *ws,
-                               hipStream_t stream);
+                               bool slicesOk, hipStream_t stream);
 int kudnn_launch_gemm_f32(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, void *ws,
                           uint32_t *counters, hipStream_t stream);
 // f32, one 16 x 32 tile per workgroup with K split over its waves (gemm_kslice.hip): no workspace. Needs K a multiple

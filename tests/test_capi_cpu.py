@@ -172,6 +172,20 @@ def test_decode_kernel_rule(monkeypatch):
     assert plan_of(64, 4096, 4096).describe().startswith("mfma_bf16")
 
 
+def test_kslice_rule():
+    # small 16-bit grids: the ping-pong kernel with K slices (tiles x slices <= 128, slices of >= 16 k-tiles); not at
+    # 64 tiles with < 64 k-tiles (the 4-wave kernel), nor from 97 tiles on, nor for M < 1024 above 64 tiles
+    for (M, N, Kd), S in {(256, 4096, 4096): 4, (256, 4096, 14336): 8, (512, 4096, 14336): 4, (1024, 4096, 11008): 2,
+                          (256, 11008, 4096): 2, (4096, 1152, 4608): 2, (4096, 1536, 5120): 2}.items():
+        d = plan_of(M, Kd, N).describe()
+        assert d.startswith("mfma_bf16_pingpong") and f" kslices={S}" in d, d
+        assert f" kslices={S}" in plan_of(M, Kd, N, K.F16).describe()
+    for M, N, Kd in ((2048, 2048, 2048), (512, 11008, 4096), (2048, 4096, 4096), (4096, 11008, 4096)):
+        assert "kslices" not in plan_of(M, Kd, N).describe(), (M, N, Kd)
+    assert plan_of(2048, 2048, 2048).describe().startswith("mfma_bf16_128x128")
+    assert "kslices" not in plan_of(256, 4096, 4096, K.F32).describe()
+
+
 def test_forced_mfma_config_keeps_decode_plans(monkeypatch):
     # a forced 4-wave or ping-pong configuration needs whole k-tiles, which only the prefill plans pack for: a
     # 16-bit plan with M <= 16 keeps its decode kernel
@@ -217,16 +231,17 @@ def test_dispatcher_choices():
 @pytest.mark.parametrize("M,Kd,N,cfg", [
     (512, 4096, 11008, "pingpong"),   # 2 x 43 = 86 tiles of 256 x 256: from 80 on, the ping-pong kernel
     (3072, 14336, 4096, "pingpong"),  # 192 tiles: a partial round still goes to the ping-pong kernel
-    (1024, 4096, 4096, "128x128"),    # 64 tiles, 64 k-tiles: too short for the K-split
-    (1024, 11008, 4096, "pingpong"),  # 64 tiles, 172 k-tiles (43 per CU): the K-split
-    (512, 14336, 4096, "pingpong"),   # 32 tiles, 224 k-tiles (28 per CU): the K-split
-    (512, 11008, 4096, "128x128"),    # 32 tiles, 172 k-tiles: 21.5 per CU, below the 24 the K-split needs
-    (256, 8192, 8192, "128x128"),     # 32 tiles, 128 k-tiles: 16 per CU
-    (2048, 2048, 2048, "128x128"),    # 64 tiles, 32 k-tiles
+    (1024, 4096, 4096, "pingpong"),   # 64 tiles, 64 k-tiles: K slices
+    (1024, 11008, 4096, "pingpong"),  # 64 tiles, 172 k-tiles: K slices
+    (512, 14336, 4096, "pingpong"),   # 32 tiles, 224 k-tiles: K slices
+    (512, 11008, 4096, "pingpong"),   # 32 tiles, 172 k-tiles: K slices
+    (256, 8192, 8192, "pingpong"),    # 32 tiles, 128 k-tiles: K slices
+    (2048, 2048, 2048, "128x128"),    # 64 tiles, 32 k-tiles: the 4-wave kernel fills the CUs
+    (256, 256, 2048, "128x128"),      # 8 tiles, 4 k-tiles: too short to slice
 ])
 def test_dispatch_rule(M, Kd, N, cfg):
-    # the planner's measured rule (bench.py --only dispatch): ping-pong from 80 tiles of 256 x 256, or with long K on
-    # at most half the CUs (the K-split itself is decided at launch, on the device's CU count); else 4-wave 128 x 128
+    # the planner's measured rule (bench.py --only dispatch): ping-pong from 80 tiles of 256 x 256, or with K slices
+    # on small grids (kudnn_kslice_rule), or with long K for its tail split; else 4-wave 128 x 128
     assert plan_of(M, Kd, N).describe().startswith(f"mfma_bf16_{cfg}"), plan_of(M, Kd, N).describe()
     assert plan_of(M, Kd, N, K.F16).describe().startswith(f"mfma_f16_{cfg}")
 

@@ -1,0 +1,162 @@
+"""GPU parity of the ping-pong kernel's K slices (KUDNN_HIP_FORCE_KSLICES=S): every tile's k-tiles divided into S
+slices run as separate workgroups of the data-parallel kernel, each storing its f32 sums, then one element-wise launch
+adding the slices in slice order and running the epilogue. Edge tiles, uneven slices, the fixed and generic epilogue
+forms, f16 operands and a K-major weight read in place, each against the oracle. Reference semantics:
+src/dnn/src/kudnn_gemm.cpp:208-241 and the post-op stages of kudnn_linear_activationlayer.cpp:40-56 restated by the
+oracle.
+"""
+import numpy as np
+import pytest
+
+import kudnn_amd as K
+import oracle as O
+from support import Case, compare, dense_rows, explainer, from_device, sample_rows
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    K.lib()  # fail loudly if the HIP library is missing
+
+
+@pytest.fixture
+def slices(monkeypatch):
+    monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "4")  # the ping-pong kernel, also where the planner would not take it
+
+    def force(S):
+        monkeypatch.setenv("KUDNN_HIP_FORCE_KSLICES", str(S))
+
+    return force
+
+
+def _run(M, N, Kd, post, dt=O.BF16, wl="BA", seed=600):
+    ydt = O.F32 if post == "gemm_beta" and dt == O.BF16 else dt
+    x = Case([M, Kd], dt, seed=seed, dist="normal", lo=0.0, hi=1.0)
+    w = Case([Kd, N], dt, wl, seed=seed + 1, dist="normal", lo=0.0, hi=0.03)
+    b = Case([1, N], ydt, seed=seed + 2, lo=-0.2, hi=0.2)
+    y = Case([M, N], ydt, seed=seed + 3, lo=-1.0, hi=1.0) if post == "gemm_beta" else Case([M, N], ydt, zero=True)
+    s = Case([M, N], ydt, seed=seed + 4, lo=-1.0, hi=1.0)
+    dy = torch.from_numpy(y.t.buf.view(np.int16).copy() if ydt != O.F32 else y.t.buf.copy()).cuda()
+    ref = O.Tensor(y.t.dims, y.t.strides, ydt, y.t.buf.copy())
+    why = None
+    if post == "bias_gelu_add":
+        plan = K.LinearPostOps(x.desc, w.desc, y.desc, b.desc, act=K.ACT_GELU_TANH, binary=K.BIN_ADD, src=s.desc)
+        plan.run(x.device(), w.device(), dy, b.device(), s.device())
+        O.linear_postops(x.t, w.t, ref, b.t, O.ACT_GELU_TANH, 0.0, O.BIN_ADD, s.t)
+        why = explainer(ydt, x.t, w.t, b.t, (M, N), act=O.ACT_GELU_TANH, binary=O.BIN_ADD, src=s.t)
+    elif post == "relu":
+        plan = K.LinearActivation(x.desc, w.desc, y.desc, b.desc, 0.0, 0.0, K.ACT_RELU)
+        plan.run(x.device(), w.device(), dy, b.device())
+        O.linear_act(x.t, w.t, ref, b.t, O.ACT_RELU, 0.0)
+    else:
+        plan = K.Gemm(x.desc, w.desc, y.desc, b.desc)
+        plan.run(x.device(), w.device(), dy, b.device(), alpha=0.5, beta=0.25)
+        O.gemm(x.t, w.t, ref, b.t, 0.5, 0.25)
+    torch.cuda.synchronize()
+    compare(from_device(dy, ydt), ref.buf, ydt, f"M={M} N={N} K={Kd} {post} {plan.describe()}", explain=why)
+    return plan.describe()
+
+
+@pytest.mark.parametrize("S", [2, 3, 5])
+@pytest.mark.parametrize("post", ["bias_gelu_add", "gemm_beta"])
+def test_kslices_edges(slices, S, post):
+    # 600 x 700: edge tiles along both dims; K = 2048 is 32 k-tiles, so S = 3 and 5 leave a shorter last slice
+    slices(S)
+    desc = _run(600, 700, 2048, post)
+    assert f"kslices={S}" in desc, desc
+
+
+@pytest.mark.parametrize("S", [2, 4])
+def test_kslices_f16_and_kmajor(slices, S):
+    slices(S)
+    assert f"kslices={S}" in _run(300, 512, 1024, "relu", dt=O.F16, seed=610)
+    # a [K][N] weight (N a multiple of 256, K of 64) is read in place by the sliced launch too
+    desc = _run(512, 512, 4096, "bias_gelu_add", wl="AB", seed=620)
+    assert f"kslices={S}" in desc and "kmajorB" in desc, desc
+
+
+def test_kslices_one_k_tile_each(slices):
+    # as many slices as k-tiles: one k-tile per workgroup
+    slices(8)
+    assert "kslices=8" in _run(256, 256, 512, "bias_gelu_add", seed=630)
+
+
+def test_kslices_match_unsliced(monkeypatch, slices):
+    # the same inputs with and without slices: the f32 sums are added in another order, so the bf16 GEMM stages can
+    # differ by one ulp, and only rarely
+    outs = []
+    for S in (0, 3):
+        slices(S)
+        M, N, Kd = 512, 768, 3072
+        x = Case([M, Kd], O.BF16, seed=640, dist="normal", lo=0.0, hi=1.0)
+        w = Case([Kd, N], O.BF16, "BA", seed=641, dist="normal", lo=0.0, hi=0.03)
+        y = Case([M, N], O.BF16, zero=True)
+        plan = K.LinearActivation(x.desc, w.desc, y.desc, None, 0.0, 0.0, K.ACT_RELU)
+        assert ("kslices=3" in plan.describe()) == (S == 3), plan.describe()
+        dy = torch.zeros(M * N, dtype=torch.int16, device="cuda")
+        plan.run(x.device(), w.device(), dy)
+        torch.cuda.synchronize()
+        outs.append(from_device(dy, O.BF16))
+    assert np.mean(outs[0] == outs[1]) > 0.99
+
+
+@pytest.mark.parametrize("mnk,S", [((1024, 4096, 11008), 2), ((512, 4096, 14336), 4), ((256, 4096, 4096), 4),
+                                   ((4096, 1152, 4608), 2)])
+def test_planner_kslices(mnk, S):
+    # the planner's own choice: 64 tiles x 172 k-tiles, 32 x 224, 16 x 64 and one of the reference's perf shapes
+    # (80 tiles, M >= 1024); large outputs checked on sampled rows of every 256-row band
+    M, N, Kd = mnk
+    x = Case([M, Kd], O.BF16, seed=650, dist="normal", lo=0.0, hi=1.0)
+    w = Case([Kd, N], O.BF16, "BA", seed=651, dist="normal", lo=0.0, hi=0.02)
+    b = Case([1, N], O.BF16, seed=652, lo=-0.2, hi=0.2)
+    y = Case([M, N], O.BF16, zero=True)
+    plan = K.LinearActivation(x.desc, w.desc, y.desc, b.desc, 0.0, 0.0, K.ACT_GELU_TANH)
+    assert plan.describe().startswith("mfma_bf16_pingpong") and f"kslices={S}" in plan.describe(), plan.describe()
+    dy = torch.zeros(M * N, dtype=torch.int16, device="cuda")
+    plan.run(x.device(), w.device(), dy, b.device())
+    torch.cuda.synchronize()
+    got = from_device(dy, O.BF16).reshape(M, N)
+    rows = sample_rows(M, 24)
+    xr = dense_rows(x.t, rows)
+    ref = O.empty((len(rows), N), (N, 1), O.BF16)
+    O.linear_act(xr, w.t, ref, b.t, O.ACT_GELU_TANH, 0.0)
+    why = explainer(O.BF16, xr, w.t, b.t, (len(rows), N), act=O.ACT_GELU_TANH)
+    compare(got[rows].reshape(-1), ref.buf, O.BF16, plan.describe(), explain=why)
+
+
+def test_kslices_graph_replays(slices):
+    # both launches captured in a HIP graph (no memset nodes): every replay, with eager work between replays, equals
+    # the eager result
+    slices(3)
+    M, N, Kd = 300, 520, 2048
+    x = Case([M, Kd], O.BF16, seed=660, dist="normal", lo=0.0, hi=1.0)
+    w = Case([Kd, N], O.BF16, "BA", seed=661, dist="normal", lo=0.0, hi=0.05)
+    s = Case([M, N], O.BF16, seed=662, lo=-1.0, hi=1.0)
+    y = Case([M, N], O.BF16, zero=True)
+    plan = K.LinearPostOps(x.desc, w.desc, y.desc, None, act=K.ACT_GELU_TANH, binary=K.BIN_ADD, src=s.desc)
+    assert "kslices=3" in plan.describe(), plan.describe()
+    dx, dw, ds = x.device(), w.device(), s.device()
+    stream = torch.cuda.Stream()
+    eager = torch.zeros(M * N, dtype=torch.int16, device="cuda")
+    with torch.cuda.stream(stream):
+        plan.run(dx, dw, eager, None, ds, stream=stream)
+    torch.cuda.synchronize()
+    out = torch.zeros(M * N, dtype=torch.int16, device="cuda")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        plan.run(dx, dw, out, None, ds, stream=stream)  # warm: the plan's workspace exists before capture
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            plan.run(dx, dw, out, None, ds, stream=stream)
+    for r in range(3):
+        out.zero_()
+        plan.run(dx, dw, torch.zeros_like(eager), None, ds)  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {r}"

@@ -407,9 +407,9 @@ def test_m1_row_gemv_batched_broadcast_weight():
 def test_split_k_small_grids(monkeypatch, dt, mnk, post):
     # grids of fewer than 128 tiles with at least 8 k-tiles run split along K: raw f32 partials in the plan's
     # workspace, then one pass that sums them in split order and applies the whole epilogue (f32 forced onto the
-    # 64 x 64 kernel, which the planner gives to the k-slice kernel where that one makes 128 tiles or more)
-    if dt == O.F32:
-        monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "11")
+    # 64 x 64 kernel, which the planner gives to the k-slice kernel where that one makes 128 tiles or more; bf16 forced
+    # onto the 128 x 128 kernel, which the planner replaces by the ping-pong kernel's K slices from 32 k-tiles on)
+    monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "11" if dt == O.F32 else "3")
     M, N, Kd = mnk
     x = Case([M, Kd], dt, seed=220, dist="normal", lo=0.0, hi=1.0)
     w = Case([Kd, N], dt, "BA", seed=221, dist="normal", lo=0.0, hi=1.0 / 32)

@@ -27,6 +27,7 @@ def _gpu():
 @pytest.fixture
 def pingpong(monkeypatch):
     monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "4")
+    monkeypatch.setenv("KUDNN_HIP_FORCE_KSLICES", "0")  # the tail split, not the K slices the planner prefers
 
 
 def run_linear(M, N, Kd, dt=O.BF16, ydt=None, act=O.ACT_GELU_TANH, alpha=0.0, beta=0.0, bias="1N", binary=True,
@@ -124,12 +125,24 @@ def test_forced_tail_split_s8_exact(monkeypatch, pingpong):
         compare(from_device(dc, O.S32), ref.buf, O.S32, f"{plan.describe()} run {r}")
 
 
-@pytest.mark.parametrize("mnk", [(1024, 4096, 11008), (512, 4096, 14336)])
-def test_planner_tail_split(mnk):
-    # the planner's own choice on 256 CUs: 64 tiles x 172 k-tiles (43 per CU) and 32 tiles x 224 k-tiles (28 per CU),
-    # where the split beat both the unsplit ping-pong grid and the 4-wave kernels
-    M, N, Kd = mnk
-    run_linear(M, N, Kd, seed=60, runs=2)
+def test_planner_tail_split_s8():
+    # the planner's own choice on 256 CUs for an s8 GEMM (the 16-bit types take K slices instead): 64 tiles x 128
+    # k-tiles of 128 bytes, 32 per CU; integer results exact on sampled rows of every 256-row band
+    M, N, Kd = 1024, 4096, 16384
+    x = Case([M, Kd], O.S8, seed=62, lo=-128, hi=127)
+    w = Case([Kd, N], O.S8, "BA", seed=63, lo=-128, hi=127)
+    c = Case([M, N], O.S32, zero=True)
+    plan = K.Gemm(x.desc, w.desc, c.desc)
+    assert "s8_pingpong" in plan.describe() and " split=0+64/32" in plan.describe(), plan.describe()
+    rows = sample_rows(M, 24)
+    ref = O.empty((len(rows), N), (N, 1), O.S32)
+    O.gemm(dense_rows(x.t, rows), w.t, ref)
+    for r in range(2):
+        dc = zeros_device(c)
+        plan.run(x.device(), w.device(), dc)
+        torch.cuda.synchronize()
+        got = from_device(dc, O.S32).reshape(M, N)[rows].reshape(-1)
+        compare(got, ref.buf, O.S32, f"{plan.describe()} run {r}")
 
 
 def test_forced_split_behind_whole_rounds(monkeypatch):

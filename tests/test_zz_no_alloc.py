@@ -1,6 +1,7 @@
 """GPU test of kudnn_linear_postops_run_noalloc, the entry point that allocates nothing: through the C ABI its
-results equal kudnn_linear_postops_run's bit for bit (same kernels) on two calls in a row, the second smaller, with
-plans that use the workspace (operand packs and split-K partials, which it takes from its static device scratch)."""
+results equal kudnn_linear_postops_run's bit for bit (same kernels) on calls in a row, each smaller than the one
+before, with plans that use the workspace (the ping-pong kernel's K-slice sums, operand packs and the 4-wave kernel's
+split-K partials, which it takes from its static device scratch)."""
 import ctypes
 
 import numpy as np
@@ -30,7 +31,6 @@ def _run_both(M, N, Kd, seed):
     s = Case([M, N], O.BF16, seed=seed + 3, lo=-1.0, hi=1.0)
     y = Case([M, N], O.BF16, zero=True)
     plan = K.LinearPostOps(x.desc, w.desc, y.desc, b.desc, act=K.ACT_GELU_TANH, binary=K.BIN_ADD, src=s.desc)
-    assert "packB" in plan.describe(), plan.describe()
     dx, dw, db, ds = x.device(), w.device(), b.device(), s.device()
     want, got = zeros_device(y), zeros_device(y)
     plan.run(dx, dw, want, db, ds, gamma=1.0)
@@ -46,17 +46,23 @@ def _run_both(M, N, Kd, seed):
 
 
 def test_noalloc_matches_run_on_two_calls():
-    # 256 x 1024 x 2048 (4-wave kernel, split along K, packed weight) then a smaller 64 x 512 x 1000 (K tail: both
-    # operands packed with zero padding); the second call reuses the scratch the first left behind
+    # 256 x 1024 x 2048 (ping-pong kernel, K-major weight read in place, 2 K slices), then a smaller 256 x 1024 x 512
+    # (4-wave kernel split along K, packed weight), then 64 x 512 x 1000 (K tail: both operands packed with zero
+    # padding); each call reuses the scratch the one before left behind
     p1 = _run_both(256, 1024, 2048, seed=500)
-    p2 = _run_both(64, 512, 1000, seed=510)
-    assert "packA" in p2.describe()
+    assert "kslices=2" in p1.describe(), p1.describe()
+    p2 = _run_both(256, 1024, 512, seed=505)
+    assert p2.describe().startswith("mfma_bf16_128x128") and "packB" in p2.describe(), p2.describe()
+    p3 = _run_both(64, 512, 1000, seed=510)
+    assert "packA" in p3.describe()
 
 
 def test_noalloc_refuses_what_it_cannot_do():
-    # a packed weight of 128 MiB exceeds the scratch: refused before anything runs
-    M, N, Kd = 64, 16384, 4096
+    # a packed weight of 128 MiB exceeds the scratch: refused before anything runs (N not a multiple of 256, so the
+    # K-major weight cannot be read in place)
+    M, N, Kd = 64, 16392, 4096
     plan = K.LinearPostOps(K.desc([M, Kd], K.BF16), K.desc([Kd, N], K.BF16, "AB"), K.desc([M, N], K.BF16))
+    assert "packB" in plan.describe(), plan.describe()
     x = torch.zeros(M * Kd, dtype=torch.int16, device="cuda")
     w = torch.zeros(Kd * N, dtype=torch.int16, device="cuda")
     y = torch.zeros(M * N, dtype=torch.int16, device="cuda")
