@@ -12,7 +12,8 @@
 //    addressing, X loaded by every wave;
 //  - 6 <= M <= 16, skinny_rows_(compact_)kernel: 16 weight rows per workgroup, K split over its waves in blocks of
 //    256; whole-row loads go through a per-wave LDS tile into the operand layout of v_mfma_f32_16x16x32_bf16, X (rows
-//    m < M, cache-resident) is the second operand, and the waves' partial 16 x 16 tiles are summed through LDS;
+//    m < M, cache-resident) is the second operand (in the 2-wave form also loaded by whole rows through a second
+//    tile), and the waves' partial 16 x 16 tiles are summed through LDS;
 //  - operands of 2^31 bytes or more, skinny_bf16_kernel: loads straight into the MFMA operand layout (16 rows x 64
 //    bytes per instruction) with 64-bit addressing, UNR k-steps in flight.
 // Wave 0 (lane m of each wave for the GEMV kernels) runs the fused epilogue.
@@ -375,7 +376,14 @@ template <int CT, int KW, bool PIPE, int ACT, int FORM>
 __device__ __forceinline__ void skinny_rows_body(const GemmOperands &op, const EpiParams &ep)
 {
     constexpr int kPitch = 33;  // chunks per LDS row
+    // XR: X's rows are loaded like the weight's (two rows of 512 contiguous bytes per instruction) and go through a
+    // second LDS tile into the MFMA operand layout, instead of being loaded in that layout (16 rows x 64 bytes per
+    // instruction). Measured on MI355X at M = 16, N = 14336: the operand-layout X loads cost 6.4 of the kernel's 27 us
+    // (20.6 us with them removed, 26.8 us with all of them reading one cache-resident block: the instructions, not
+    // the bytes), since the vector memory path serves 64-byte row pieces at half the rate of whole lines.
+    constexpr bool XR = PIPE;
     __shared__ u32x4_t tile[KW][16 * kPitch];
+    __shared__ u32x4_t xtile[XR ? KW : 1][XR ? 16 * kPitch : 1];
     __shared__ f32x4_t part[KW][64];
 
     const int lane = threadIdx.x & 63;
@@ -415,6 +423,8 @@ __device__ __forceinline__ void skinny_rows_body(const GemmOperands &op, const E
         wrow[i] = static_cast<uint32_t>(row < N ? row : N - 1) * rowBytes;
     }
     u32x4_t *tw = tile[wave];
+    u32x4_t *tx = xtile[XR ? wave : 0];
+    const uint32_t xpitch = static_cast<uint32_t>(op.lda) * 2u;
 
     // wave 0 runs the epilogue: its bias and binary operand are loaded right after its first block's loads, so their
     // latency overlaps that block's instead of following the K loop
@@ -439,11 +449,22 @@ __device__ __forceinline__ void skinny_rows_body(const GemmOperands &op, const E
     auto block = [&](int b, const u32x4_t (&wv)[8], u32x4_t (&wn)[8]) {
         const int c0 = b * 32;
         u32x4_t xv[8];
+        if constexpr (XR) {
+            // rows 2i + half of X, chunk c0 + c32 (rows m >= M read zero)
+            const bool kin = c0 + c32 < chunks;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {  // k-step k of the block: chunk c0 + 4k + q
-            const int kc = c0 + 4 * k + q;
-            const bool in = r16 < M && kc < chunks;
-            xv[k] = __builtin_amdgcn_raw_buffer_load_b128(xrs, in ? xrow + static_cast<uint32_t>(kc) * 16u : kOut, 0, 0);
+            for (int i = 0; i < 8; ++i) {
+                const int m = 2 * i + half;
+                xv[i] = __builtin_amdgcn_raw_buffer_load_b128(
+                    xrs, kin && m < M ? static_cast<uint32_t>(m) * xpitch + static_cast<uint32_t>(c0 + c32) * 16u : kOut, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {  // k-step k of the block: chunk c0 + 4k + q
+                const int kc = c0 + 4 * k + q;
+                const bool in = r16 < M && kc < chunks;
+                xv[k] = __builtin_amdgcn_raw_buffer_load_b128(xrs, in ? xrow + static_cast<uint32_t>(kc) * 16u : kOut, 0, 0);
+            }
         }
         if constexpr (PIPE) {
             load_w(b + KW, wn);
@@ -454,13 +475,21 @@ __device__ __forceinline__ void skinny_rows_body(const GemmOperands &op, const E
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
         for (int i = 0; i < 8; ++i) tw[(2 * i + half) * kPitch + c32] = wv[i];
+        if constexpr (XR) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) tx[(2 * i + half) * kPitch + c32] = xv[i];
+        }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const u32x4_t wf = tw[r16 * kPitch + 4 * k + q];
-            acc = mfma16<CT>(wf, xv[k], acc);
+            if constexpr (XR) {
+                acc = mfma16<CT>(wf, tx[r16 * kPitch + 4 * k + q], acc);
+            } else {
+                acc = mfma16<CT>(wf, xv[k], acc);
+            }
         }
     };
     u32x4_t w0[8], w1[8];
@@ -865,10 +894,11 @@ int launch_skinny(const GemmOperands &op, const EpiParams &ep, int64_t batches, 
     if (fits) {
         // fewer than 2 row groups per CU: split K over 16 waves (one workgroup per CU); otherwise 8 (two per CU)
         const int64_t groups = (op.N + 15) / 16 * batches;
-        // measured at M = 4 and 16, N = 4096 and 14336, K = 4096: with more than 8 rows of X, 2-wave workgroups with
-        // the next block's weights in flight (145 VGPRs, 12 waves and 6 workgroups per CU, one round of workgroups)
-        // beat the 8- and 16-wave forms by 8-9 %; at M = 4 they lose 1-4 %, and with few row groups they leave CUs idle
-        if (op.M > 8 && groups >= 256) {
+        // measured at K = 4096: with more than 8 rows of X, 2-wave workgroups with the next block's weights in flight
+        // and X's rows through an LDS tile (169 VGPRs, 36 KB of LDS: 4 workgroups per CU) beat the 8- and 16-wave
+        // forms (M = 16, N = 14336: 23.9 against 27.0 us); at M = 7 and 8 they win from 512 row groups on (M = 8,
+        // N = 8192: 13.4 against 15.0 us) and lose at 256 (N = 4096: 9.4 against 9.0 us); at M = 6 they are even
+        if ((op.M > 8 && groups >= 256) || (op.M >= 7 && groups >= 512)) {
             launch_rows<CT, 2, true>(op, ep, batches, stream);
         } else if (groups < 512) {
             launch_rows<CT, 16, false>(op, ep, batches, stream);

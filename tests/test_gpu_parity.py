@@ -300,11 +300,14 @@ def test_c4_skinny_mul(M, N):
     compare(from_device(dy, O.BF16), ref.buf, O.BF16, f"C4 M={M} N={N}")
 
 
-@pytest.mark.parametrize("M,N,Kd", [(9, 4112, 2100), (12, 4096, 2304), (16, 4104, 4096), (12, 1024, 2100)])
+@pytest.mark.parametrize("M,N,Kd", [(9, 4112, 2100), (12, 4096, 2304), (16, 4104, 4096), (12, 1024, 2100),
+                                    (8, 8200, 2100), (7, 8192, 4096), (6, 8192, 2304)])
 def test_skinny_rows_forms(M, N, Kd):
-    # M > 8 with >= 256 row groups runs 2-wave workgroups with the next weight block in flight: an odd count of
-    # 256-element K blocks (K = 2100 packs to 9 blocks, 2304 is exactly 9) ends one wave on a block with no successor;
-    # N not a multiple of 16 leaves a ragged last row group. N = 1024 (64 row groups) stays on the 16-wave form.
+    # M > 8 with >= 256 row groups, and M = 7, 8 with >= 512, run 2-wave workgroups with the next weight block in
+    # flight and X's rows loaded whole through a second LDS tile (rows m >= M read zero): an odd count of 256-element
+    # K blocks (K = 2100 packs to 9 blocks, 2304 is exactly 9) ends one wave on a block with no successor; N not a
+    # multiple of 16 leaves a ragged last row group. N = 1024 (64 row groups) stays on the 16-wave form, M = 6 on the
+    # 8-wave form.
     # The chain is bias + ReLU + add: a 1-ULP difference of the bf16 GEMM result (f32 summation order) stays 1 ULP,
     # where GELU's extra rounding could double it; a lost or repeated K block would move almost every element.
     x = Case([M, Kd], O.BF16, seed=210, dist="normal", lo=0.0, hi=1.0)
