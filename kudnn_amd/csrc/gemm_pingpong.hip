@@ -223,6 +223,64 @@ __device__ __forceinline__ void epilogue_full(const EpiParams &ep, const EpiBatc
     });
 }
 
+// The same for the 16-bit forms, with every residual load and output store covering 8 rows x 128 bytes (whole cache
+// lines) instead of 16 rows x 64 bytes (a 32-column strip of 16-bit values): two strips' 32-row halves are staged at a
+// time (32 rows x 64 columns, row pitch 68 floats), and lane -> row rl + 8 * pass, columns col8 .. +8 of the pair.
+// The vector memory path serves 64-byte row pieces at half the rate of whole lines. Four units (strip pair jj, row
+// half i), the binary operand of two units in flight; the bias of a strip pair is loaded once.
+template <int ACT, int FORM>
+__device__ __forceinline__ void epilogue_full_rows(const EpiParams &ep, const EpiBatch &ob, const f32x16_t (&acc)[4][2],
+                                                   float *stage, int lane, int64_t mW, int64_t nW)
+{
+    constexpr int P = 68;  // staging pitch in floats (64 columns + 4)
+    const int lrow = lane & 31, lh = lane >> 5;
+    const int col8 = (lane & 7) * 8, rl = lane >> 3;
+    Raw8 src[2][4], bias[2];
+    auto fetch = [&](auto uc) __attribute__((always_inline)) {
+        constexpr int u = decltype(uc)::value, jj = u / 2, i = u % 2;
+        const int64_t n = nW + jj * 64 + col8;
+        if constexpr (i == 0) {
+            bias[jj] = epi_prefetch8_bias<FORM>(ep, ob, mW + rl, n);
+        }
+        sfor<4>([&](auto pc) __attribute__((always_inline)) {
+            constexpr int ps = decltype(pc)::value;
+            src[u % 2][ps] = epi_prefetch8_src<FORM>(ep, ob, mW + i * 32 + rl + ps * 8, n);
+        });
+    };
+    fetch(std::integral_constant<int, 0>{});
+    fetch(std::integral_constant<int, 1>{});
+    constexpr int64_t ES = 2;
+    char *yLane = static_cast<char *>(ep.y) + (ob.y + (mW + rl) * ep.y_sm + nW + col8) * ES;
+    __syncthreads();  // every wave is done with the tile buffers that the staging area reuses
+    sfor<4>([&](auto uc) __attribute__((always_inline)) {
+        constexpr int u = decltype(uc)::value, jj = u / 2, i = u % 2;
+#pragma unroll
+        for (int sh = 0; sh < 2; ++sh) {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                float *dst = stage + lrow * P + sh * 32 + q4 * 8 + lh * 4;
+                const f32x16_t &a = acc[2 * jj + sh][i];
+                *reinterpret_cast<float4 *>(dst) = make_float4(a[4 * q4 + 0], a[4 * q4 + 1], a[4 * q4 + 2], a[4 * q4 + 3]);
+            }
+        }
+        float bv[8];
+        epi_bias8<FORM>(ep, bias[jj], bv);
+        wave_sync();
+        sfor<4>([&](auto pc) __attribute__((always_inline)) {
+            constexpr int ps = decltype(pc)::value;
+            const float *sp = stage + (rl + ps * 8) * P + col8;
+            const float4 lo = *reinterpret_cast<const float4 *>(sp);
+            const float4 hi = *reinterpret_cast<const float4 *>(sp + 4);
+            const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            epi_fast8_core<ACT, FORM>(ep, yLane + ((i * 32 + ps * 8) * ep.y_sm + jj * 64) * ES, v, src[u % 2][ps], bv);
+        });
+        if constexpr (u + 2 < 4) {
+            fetch(std::integral_constant<int, u + 2>{});
+        }
+        wave_sync();
+    });
+}
+
 // Epilogue of a tile that crosses the matrix edge, in a fixed form: whole 8-column groups as in a full tile, the
 // last partial group of a row one element at a time; rolled loops keep the code small.
 template <int ACT, int FORM>
@@ -694,7 +752,11 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
             epilogue_generic(ep, ob, acc, stage, lane, mW, nW, M, N);
         } else if constexpr (FORM != EPI_FORM_PARTIAL) {
             if (m0 + kBM <= M && n0 + kBN <= N && (ep.bias == nullptr || ep.bias_sm == 0)) {
-                epilogue_full<ACT, FORM>(ep, ob, acc, stage, lane, mW, nW);
+                if constexpr (FORM == EPI_FORM_F32) {
+                    epilogue_full<ACT, FORM>(ep, ob, acc, stage, lane, mW, nW);  // 32 f32 columns: whole lines already
+                } else {
+                    epilogue_full_rows<ACT, FORM>(ep, ob, acc, stage, lane, mW, nW);
+                }
             } else {
                 epilogue_edge<ACT, FORM>(ep, ob, acc, stage, lane, mW, nW, M, N);
             }
