@@ -605,13 +605,14 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
         }
     }
     // A K-major weight (B stored [K][N], N contiguous: C5's W{1,K,N} ABC) is read in place by the ping-pong kernel,
-    // through transposing LDS reads, instead of being packed on every run; it needs whole 256-column tiles and
-    // 64-deep k-tiles, 16-byte aligned k-rows and batches, and 32-bit offsets.
+    // through transposing LDS reads, instead of being packed on every run; it needs 64-deep k-tiles, N a multiple of
+    // 8 (whole 16-byte column chunks; an edge tile's columns past N are computed and never stored), 16-byte aligned
+    // k-rows and batches, and 32-bit offsets.
     const bool bBatchAligned = core.B.bs[0] % 8 == 0 && core.B.bs[1] % 8 == 0 && core.B.bs[2] % 8 == 0;
     if (core.engine == ENGINE_MFMA_BF16 && core.cfg == KUDNN_CFG_BF16_PINGPONG_256x256 &&
         (core.computeDt == KUDNN_DT_BF16 || core.computeDt == KUDNN_DT_F16) && core.B.dt == core.computeDt &&
         core.B.s_r == 1 && core.B.s_k >= core.N && core.B.s_k % 8 == 0 && bBatchAligned && core.K % 64 == 0 &&
-        core.N % 256 == 0 && core.K * core.B.s_k * 2 < (int64_t(1) << 31) &&
+        core.N % 8 == 0 && core.K * core.B.s_k * 2 < (int64_t(1) << 31) &&
         core.M * std::max<int64_t>(core.A.s_r, core.kp) * 2 < (int64_t(1) << 31) && !std::getenv("KUDNN_HIP_PACK_KMAJOR")) {
         core.B.kmajor = true;
         core.B.staticPack = false;

@@ -453,7 +453,10 @@ constexpr int kSlotFloats = kBM * kBN;  // one 256 x 256 accumulator tile
 // a = 4 jj + q reads 4 consecutive n (n0 + 4q .. +3) of row k0 + jj, and output lane i receives element i % 4 of
 // address lane 4 jj + i / 4 for jj = 0..3, that is n0 + i at k0 .. k0 + 3 (measured on gfx950). Two such reads give
 // a lane its 8 k. In a half-wave the four rows sit at four distinct 64-byte offsets modulo 256 bytes, so the reads are
-// free of bank conflicts. Needs N a multiple of 256 and K of 64 (no edge along n or k).
+// free of bank conflicts. Needs K a multiple of 64 (no edge along k) and N of 8. At an edge along n, a k-row's copy
+// runs past column N into the first columns of the next k-row (the last k-row's into zeros: the resource ends at the
+// operand's last byte, so the range check blanks the rest); those values reach only accumulator columns >= N, which
+// the epilogues never store.
 //
 // CT: operand type, KUDNN_DT_BF16 / F16 / S8. SK: false for the data-parallel launch (block -> one whole tile),
 // true for the tail launch (block -> a range of k-iterations over one or more tiles). BKM: B is K-major (bf16 / f16,
@@ -895,13 +898,13 @@ __global__ void sk_zero_kernel(uint32_t *cnt, int n)
 bool kudnn_pingpong_eligible(const GemmOperands &op, int ct)
 {
     // whole k-tiles, 16-byte aligned rows, 32-bit buffer offsets (the offset of the first byte past each operand's
-    // last row, and that of the row after it, which an edge tile's copies compute); a K-major B also whole 256-column
-    // tiles
+    // last row, and that of the row after it, which an edge tile's copies compute); a K-major B also whole 64-deep
+    // k-tiles and whole 16-byte chunks of columns, so that its copies are wholly inside the operand or wholly past it
     const int64_t es = ct == KUDNN_DT_S8 ? 1 : 2;
     const int64_t lim = int64_t(1) << 31;
     const bool aFits = op.M * op.lda * es < lim && ((op.M - 1) * op.lda + op.K) * es < lim;
     if (op.b_kmajor) {
-        return (ct == KUDNN_DT_BF16 || ct == KUDNN_DT_F16) && op.K > 0 && op.K % 64 == 0 && op.N % kBN == 0 &&
+        return (ct == KUDNN_DT_BF16 || ct == KUDNN_DT_F16) && op.K > 0 && op.K % 64 == 0 && op.N % 8 == 0 &&
                (op.lda * es) % 16 == 0 && (op.ldb * es) % 16 == 0 && op.ldb >= op.N && aFits &&
                op.K * op.ldb * es < lim && reinterpret_cast<uintptr_t>(op.b) % 16 == 0;
     }

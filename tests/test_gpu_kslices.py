@@ -75,9 +75,11 @@ def test_kslices_edges(slices, S, post):
 def test_kslices_f16_and_kmajor(slices, S):
     slices(S)
     assert f"kslices={S}" in _run(300, 512, 1024, "relu", dt=O.F16, seed=610)
-    # a [K][N] weight (N a multiple of 256, K of 64) is read in place by the sliced launch too
-    desc = _run(512, 512, 4096, "bias_gelu_add", wl="AB", seed=620)
-    assert f"kslices={S}" in desc and "kmajorB" in desc, desc
+    # a [K][N] weight (N a multiple of 8, K of 64) is read in place by the sliced launch too, also with an edge tile
+    # along N (1152 = 4.5 tiles: the reference's performance shapes)
+    for N, seed in ((512, 620), (1152, 625)):
+        desc = _run(512, N, 4096, "bias_gelu_add", wl="AB", seed=seed)
+        assert f"kslices={S}" in desc and "kmajorB" in desc, desc
 
 
 def test_kslices_one_k_tile_each(slices):

@@ -490,11 +490,13 @@ def _kmajor_case(dt, lead, M, Kd, N, wlead, act, bias, seed):
 
 @pytest.mark.parametrize("dt", [O.BF16, O.F16])
 @pytest.mark.parametrize("shape", [([], 256, 64, 256, []), ([], 300, 640, 768, []), ([], 1000, 256, 1536, []),
-                                   ([2], 260, 192, 512, [2]), ([3], 128, 128, 256, [1])])
+                                   ([2], 260, 192, 512, [2]), ([3], 128, 128, 256, [1]), ([], 300, 640, 1160, []),
+                                   ([], 256, 128, 136, []), ([2], 260, 192, 520, [2]), ([3], 128, 128, 264, [1])])
 @pytest.mark.parametrize("act", [K.ACT_UNIMPLEMENTED, K.ACT_SWISH, K.ACT_GELU_TANH])
 def test_kmajor_weight_in_place(monkeypatch, dt, shape, act):
-    # a [K][N] weight read in place by the ping-pong kernel (M edges, batched and broadcast weights, every fixed
-    # epilogue form) against the oracle, and bit for bit against the same plan with the weight packed to [N][K]:
+    # a [K][N] weight read in place by the ping-pong kernel (M edges, N edges with 8 or 136 columns in the last tile,
+    # where the copies of the last k-row run past the operand's end, batched and broadcast weights, every
+    # fixed epilogue form) against the oracle, and bit for bit against the same plan with the weight packed to [N][K]:
     # both feed the MFMAs the same k groups in the same order
     monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "4")
     lead, M, Kd, N, wlead = shape
@@ -516,6 +518,20 @@ def test_kmajor_weight_in_place(monkeypatch, dt, shape, act):
     compare(outs[0], ref.buf, dt, "kmajor " + plan.describe(),
             explain=explainer(dt, x.t, w.t, b.t if b else None, tuple(y.t.dims[-2:]), act=act, act_alpha=1.0)
             if not lead and dt == O.BF16 else None)
+
+
+def test_kmajor_weight_ragged_n_is_packed(monkeypatch):
+    # N not a multiple of 8 splits the last 16-byte column chunk of each k-row: the weight is packed to [N][K] instead
+    monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "4")
+    x, w, b, y = _kmajor_case(O.BF16, [], 300, 640, 1156, [], K.ACT_GELU_TANH, True, 710)
+    plan = K.LinearPostOps(x.desc, w.desc, y.desc, b.desc, act=K.ACT_GELU_TANH, act_alpha=1.0)
+    assert "packB" in plan.describe(), plan.describe()
+    dy = zeros_device(y)
+    plan.run(x.device(), w.device(), dy, b.device())
+    torch.cuda.synchronize()
+    ref = y.clone_empty()
+    O.linear_postops(x.t, w.t, ref, b.t, K.ACT_GELU_TANH, 1.0, O.BIN_NONE, None)
+    compare(from_device(dy, O.BF16), ref.buf, O.BF16, plan.describe())
 
 
 # ---------------------------------------------------------------------------------------------------

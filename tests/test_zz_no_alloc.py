@@ -58,9 +58,9 @@ def test_noalloc_matches_run_on_two_calls():
 
 
 def test_noalloc_refuses_what_it_cannot_do():
-    # a packed weight of 128 MiB exceeds the scratch: refused before anything runs (N not a multiple of 256, so the
+    # a packed weight of 128 MiB exceeds the scratch: refused before anything runs (N not a multiple of 8, so the
     # K-major weight cannot be read in place)
-    M, N, Kd = 64, 16392, 4096
+    M, N, Kd = 64, 16388, 4096
     plan = K.LinearPostOps(K.desc([M, Kd], K.BF16), K.desc([Kd, N], K.BF16, "AB"), K.desc([M, N], K.BF16))
     assert "packB" in plan.describe(), plan.describe()
     x = torch.zeros(M * Kd, dtype=torch.int16, device="cuda")
