@@ -657,7 +657,10 @@ std::string DescribeCore(const GemmCore &c)
         int dp = 0, tail = 0, iters = 0;
         const int slices = kudnn_pingpong_slices(shape, c.Batches(), c.computeDt);
         kudnn_pingpong_split(shape, c.Batches(), c.computeDt, &dp, &tail, &iters);
-        if (slices >= 2) {
+        const int sliceTail = slices >= 2 ? kudnn_pingpong_slice_tail(shape, c.Batches(), c.computeDt) : 0;
+        if (slices >= 2 && sliceTail > 0) {
+            std::snprintf(split, sizeof(split), " kslices=%d tail=%d", slices, sliceTail);
+        } else if (slices >= 2) {
             std::snprintf(split, sizeof(split), " kslices=%d", slices);
         } else if (tail > 0) {
             std::snprintf(split, sizeof(split), " split=%d+%d/%d", dp, tail, iters);

@@ -442,6 +442,10 @@ struct SkArgs {
     float *slices;
     int64_t sliceFloats, sliceLd;
     int sliceKT, nSlices;
+    // tail slices: the sliced tiles are logical tiles tileBase .. tileBase + nTiles - 1, and slice z of sliced tile i
+    // is a 256 x 256 block at slices + (z * nTiles + i) * kSlotFloats (row pitch 256); tileBase = 0: every tile,
+    // stored at slices + z * sliceFloats with the matrix's own coordinates
+    int tileBase, nTiles;
 };
 
 constexpr int kSlotFloats = kBM * kBN;  // one 256 x 256 accumulator tile
@@ -769,17 +773,22 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
     if constexpr (!SK && FORM == EPI_FORM_PARTIAL) {
         // K slices: logical block z * tiles + t (consecutive logical blocks share an XCD, so one XCD's workgroups work
         // on neighbouring tiles of one slice and share its A and B panels in L2)
-        const int tiles = tilesM * tilesN;
+        const int tiles = sk.nTiles;
         const int lid = xcd_remap(blockIdx.x, gridDim.x);
-        const int z = lid / tiles;
+        const int z = lid / tiles, ti = lid - z * tiles;
         int tm, tn;
-        grouped_tile(lid - z * tiles, tilesM, tilesN, group, tm, tn);
+        grouped_tile(sk.tileBase + ti, tilesM, tilesN, group, tm, tn);
         m0 = tm * kBM;
         n0 = tn * kBN;
         kb = z * sk.sliceKT;
         nk = min(sk.sliceKT, KT - kb);
         mainloop();
-        epilogue_partial(sk.slices + z * sk.sliceFloats, sk.sliceLd, acc, stage, lane, m0 + p * 64, n0 + g * 128, M, N);
+        if (sk.tileBase == 0) {
+            epilogue_partial(sk.slices + z * sk.sliceFloats, sk.sliceLd, acc, stage, lane, m0 + p * 64, n0 + g * 128, M, N);
+        } else {
+            epilogue_partial(sk.slices + static_cast<int64_t>(z * tiles + ti) * kSlotFloats, kBN, acc, stage, lane, p * 64,
+                             g * 128, M - m0, N - n0);
+        }
     } else if constexpr (!SK) {
         int tm, tn;
         grouped_tile(xcd_remap(blockIdx.x, gridDim.x), tilesM, tilesN, group, tm, tn);
@@ -994,11 +1003,14 @@ SkPlan sk_plan(const GemmOperands &op, int64_t batches, int ct)
 // all run by the data-parallel kernel's own loop; each stores its f32 sums, and slice_reduce_kernel adds the S slices
 // of every output element in slice order and runs the epilogue. Unlike the tail split, no workgroup waits on or reads
 // another's results inside the launch, and the slices' workgroups keep the data-parallel copy path and L2 sharing.
-// S from kudnn_kslice_rule; KUDNN_HIP_FORCE_KSLICES=S forces S slices (0: none).
+// S from kudnn_kslice_rule; KUDNN_HIP_FORCE_KSLICES=S forces S slices (0: none). Where that gives none, a grid of
+// more tiles than CUs may slice only its last partial round (kudnn_tail_slice_rule; KUDNN_HIP_FORCE_TAILSLICES=S):
+// the full rounds run first as one data-parallel launch of whole tiles.
 struct SlicePlan {
     int S = 0, sliceKT = 0;
     int64_t ld = 0;
     size_t bytes = 0;
+    int tileBase = 0, tail = 0;  // tail slices: tiles tileBase .. tileBase + tail - 1 sliced, the others whole
 };
 
 SlicePlan slice_plan(const GemmOperands &op, int64_t batches, int ct)
@@ -1011,6 +1023,27 @@ SlicePlan slice_plan(const GemmOperands &op, int64_t batches, int ct)
     const char *f = std::getenv("KUDNN_HIP_FORCE_KSLICES");
     int S = f != nullptr ? std::atoi(f) : kudnn_kslice_rule(op.M, op.N, KT, batches, ct);
     if (S < 2) {
+        // the last partial round of a grid larger than the CUs: its tiles split into slices, the full rounds run whole
+        const char *ft = std::getenv("KUDNN_HIP_FORCE_TAILSLICES");
+        const int cus = cu_count();
+        if (cus <= 0 || (ft == nullptr && (f != nullptr || std::getenv("KUDNN_HIP_FORCE_STREAMK") != nullptr))) {
+            return s;
+        }
+        const int64_t tiles = ((op.M + kBM - 1) / kBM) * ((op.N + kBN - 1) / kBN);
+        const int rem = static_cast<int>(tiles % cus);
+        const int St = ft != nullptr ? std::atoi(ft) : kudnn_tail_slice_rule(op.M, op.N, KT, batches, ct, cus);
+        if (tiles <= cus || rem == 0 || St < 2) {
+            return s;
+        }
+        s.sliceKT = (KT + std::min(St, KT) - 1) / std::min(St, KT);
+        s.S = (KT + s.sliceKT - 1) / s.sliceKT;
+        if (s.S < 2) {
+            return SlicePlan{};
+        }
+        s.tail = rem;
+        s.tileBase = static_cast<int>(tiles - rem);
+        s.ld = kBN;
+        s.bytes = align256(static_cast<size_t>(s.S) * static_cast<size_t>(rem) * kSlotFloats * sizeof(float));
         return s;
     }
     S = std::min(S, KT);
@@ -1024,18 +1057,43 @@ SlicePlan slice_plan(const GemmOperands &op, int64_t batches, int ct)
     return s;
 }
 
+// Tail slices as the reduction sees them: sliced tiles tileBase .. tileBase + nTiles - 1 of the grouped tile order
+// (nTiles = 0: the whole matrix is sliced).
+struct SliceTiles {
+    int tileBase, nTiles, tilesM, tilesN, group;
+};
+
 // One thread per run of 8 columns (m, n .. n + 7): the sum of the S slices in slice order, then the epilogue of FORM.
+// Whole-matrix slices: threads in row-major order over the matrix. Tail slices: 32 workgroups per sliced tile, each
+// 8 rows of it (32 threads per row).
 template <int ACT, int FORM>
 __global__ __launch_bounds__(256) void slice_reduce_kernel(const float *slices, int64_t sliceFloats, int64_t ld, int S,
-                                                           int64_t M, int64_t N, EpiParams ep)
+                                                           int64_t M, int64_t N, EpiParams ep, SliceTiles st)
 {
-    const int64_t groupsN = (N + 7) / 8;
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (idx >= M * groupsN) {
-        return;
+    int64_t m, n;
+    const float *src;
+    if (st.nTiles == 0) {
+        const int64_t groupsN = (N + 7) / 8;
+        const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+        if (idx >= M * groupsN) {
+            return;
+        }
+        m = idx / groupsN;
+        n = (idx - m * groupsN) * 8;
+        src = slices + m * ld + n;
+    } else {
+        const int ti = static_cast<int>(blockIdx.x / 32);
+        const int r = static_cast<int>(blockIdx.x % 32) * 8 + static_cast<int>(threadIdx.x / 32);
+        const int c = static_cast<int>(threadIdx.x % 32) * 8;
+        int tm, tn;
+        grouped_tile(st.tileBase + ti, st.tilesM, st.tilesN, st.group, tm, tn);
+        m = static_cast<int64_t>(tm) * kBM + r;
+        n = static_cast<int64_t>(tn) * kBN + c;
+        if (m >= M || n >= N) {
+            return;
+        }
+        src = slices + static_cast<int64_t>(ti) * kSlotFloats + r * kBN + c;
     }
-    const int64_t m = idx / groupsN, n = (idx - m * groupsN) * 8;
-    const float *src = slices + m * ld + n;
     const EpiBatch ob{0, 0, 0, 0, 0, 0};
     float v[8];
     if (n + 7 < N) {
@@ -1158,11 +1216,28 @@ int launch_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches
             args.nSlices = sl.S;
             const PingpongKernel part = op.b_kmajor ? gemm_pingpong_kernel<CT, 0, EPI_FORM_PARTIAL, false, true>
                                                     : gemm_pingpong_kernel<CT, 0, EPI_FORM_PARTIAL, false, false>;
-            hipLaunchKernelGGL(part, dim3(static_cast<unsigned>(tilesM * tilesN * sl.S)), dim3(512), 0, stream, op, ep,
+            SliceTiles st{0, 0, tilesM, tilesN, 8};
+            if (sl.tail > 0) {
+                // the full rounds as whole tiles, then the last round's tiles in slices
+                const PingpongKernel dp = op.b_kmajor ? select_pingpong<CT, false, true>(ep) : select_pingpong<CT, false>(ep);
+                if (dp == nullptr) {
+                    return -1;
+                }
+                hipLaunchKernelGGL(dp, dim3(static_cast<unsigned>(sl.tileBase)), dim3(512), 0, stream, op, ep, tilesM,
+                                   tilesN, 8, args);
+                args.tileBase = sl.tileBase;
+                args.nTiles = sl.tail;
+                args.sliceFloats = static_cast<int64_t>(sl.tail) * kSlotFloats;
+                st.tileBase = sl.tileBase;
+                st.nTiles = sl.tail;
+            } else {
+                args.nTiles = tilesM * tilesN;
+            }
+            hipLaunchKernelGGL(part, dim3(static_cast<unsigned>(args.nTiles * sl.S)), dim3(512), 0, stream, op, ep,
                                tilesM, tilesN, 8, args);
-            const int64_t threads = op.M * ((op.N + 7) / 8);
-            hipLaunchKernelGGL(select_slice_reduce<CT>(ep), dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256),
-                               0, stream, static_cast<const float *>(ws), args.sliceFloats, sl.ld, sl.S, op.M, op.N, ep);
+            const int64_t blocks = sl.tail > 0 ? static_cast<int64_t>(sl.tail) * 32 : (op.M * ((op.N + 7) / 8) + 255) / 256;
+            hipLaunchKernelGGL(select_slice_reduce<CT>(ep), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                               static_cast<const float *>(ws), args.sliceFloats, sl.ld, sl.S, op.M, op.N, ep, st);
             return hipGetLastError() == hipSuccess ? 0 : -1;
         }
     }
@@ -1210,6 +1285,11 @@ size_t kudnn_pingpong_workspace_bytes(const GemmOperands &op, int64_t batches, i
 int kudnn_pingpong_slices(const GemmOperands &op, int64_t batches, int ct)
 {
     return slice_plan(op, batches, ct).S;
+}
+
+int kudnn_pingpong_slice_tail(const GemmOperands &op, int64_t batches, int ct)
+{
+    return slice_plan(op, batches, ct).tail;
 }
 
 void kudnn_pingpong_split(const GemmOperands &op, int64_t batches, int ct, int *dpTiles, int *tailTiles, int *iters)

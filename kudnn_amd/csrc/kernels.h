@@ -42,6 +42,8 @@ size_t kudnn_pingpong_workspace_bytes(const GemmOperands &op, int64_t batches, i
 void kudnn_pingpong_split(const GemmOperands &op, int64_t batches, int ct, int *dpTiles, int *tailTiles, int *iters);
 // The K slices the launch would make when allowed (0: none).
 int kudnn_pingpong_slices(const GemmOperands &op, int64_t batches, int ct);
+// Tiles in slices when only the last partial round is sliced (0: none, or every tile).
+int kudnn_pingpong_slice_tail(const GemmOperands &op, int64_t batches, int ct);
 // The planner's K-slice count for the ping-pong kernel (0: none) of an M x N grid with KT k-tiles of 128 bytes.
 // Measured on MI355X over 26 shapes (M 256..4096, N 1152..14336, K 2048..14336, against the unsliced ping-pong, its
 // tail split and the 4-wave kernel): up to 64 tiles of 256 x 256, as many slices as keep tiles x slices <= 128 (at
@@ -68,6 +70,29 @@ inline int kudnn_kslice_rule(int64_t M, int64_t N, int64_t KT, int64_t batches, 
     }
     return S >= 2 ? static_cast<int>(S) : 0;
 }
+
+// Slices of the last partial round of a 16-bit grid of more tiles than CUs, whose full rounds run whole tiles (0:
+// none). With R tiles in that round (R = tiles mod CUs): R at most an eighth of the CUs, S = min(CUs / 2 / R, 8,
+// KT / 16) when that is at least 2. Measured on MI355X against the unsliced grid (bf16, bias): 3072 x 11008 x 4096
+// (R = 4) 265 -> 231 us, 4352 x 4096 x 4096 (R = 16) 168 -> 136 us, 4096 x 4608 x 4096 and 2304 x 8192 x 4096
+// (R = 32) 168 -> 148-149 us; R = 64 with 48 k-tiles even, with 24 k-tiles 15 % slower; R = 88, 128 and 176 (C3)
+// slower at every S; 18 k-tiles slower at every S.
+inline int kudnn_tail_slice_rule(int64_t M, int64_t N, int64_t KT, int64_t batches, int ct, int cus)
+{
+    if (batches != 1 || ct == KUDNN_DT_S8 || M <= 0 || N <= 0 || cus <= 0) {
+        return 0;
+    }
+    const int64_t tiles = (M + 255) / 256 * ((N + 255) / 256);
+    const int64_t rem = tiles % cus;
+    if (tiles <= cus || rem == 0 || rem * 8 > cus) {
+        return 0;
+    }
+    int64_t S = cus / 2 / rem;
+    S = S < 8 ? S : 8;
+    S = S < KT / 16 ? S : KT / 16;
+    return S >= 2 ? static_cast<int>(S) : 0;
+}
+
 int kudnn_launch_gemm_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, int ct, void *ws,
                                bool slicesOk, hipStream_t stream);
 int kudnn_launch_gemm_f32(const GemmOperands &op, const EpiParams &ep, int64_t batches, int cfg, void *ws,
