@@ -1,7 +1,7 @@
 """GPU test of kudnn_linear_postops_run_noalloc, the entry point that allocates nothing: through the C ABI its
 results equal kudnn_linear_postops_run's bit for bit (same kernels) on calls in a row, each smaller than the one
-before, with plans that use the workspace (the ping-pong kernel's K-slice sums, operand packs and the 4-wave kernel's
-split-K partials, which it takes from its static device scratch)."""
+before, with plans that use the workspace (the ping-pong kernel's K-slice sums, whole-grid or of the last partial
+round only, operand packs and the 4-wave kernel's split-K partials, which it takes from its static device scratch)."""
 import ctypes
 
 import numpy as np
@@ -55,6 +55,15 @@ def test_noalloc_matches_run_on_two_calls():
     assert p2.describe().startswith("mfma_bf16_128x128") and "packB" in p2.describe(), p2.describe()
     p3 = _run_both(64, 512, 1000, seed=510)
     assert "packA" in p3.describe()
+
+
+def test_noalloc_tail_slices_then_smaller():
+    # 4352 x 4096 x 4096: 272 tiles, the last round's 16 in 4 K slices (16 MB of partial blocks in the scratch), then
+    # a smaller call in 2 whole-grid slices over the same scratch
+    p1 = _run_both(4352, 4096, 4096, seed=520)
+    assert "kslices=4 tail=16" in p1.describe(), p1.describe()
+    p2 = _run_both(512, 1024, 2048, seed=525)
+    assert "kslices=" in p2.describe() and "tail=" not in p2.describe(), p2.describe()
 
 
 def test_noalloc_refuses_what_it_cannot_do():
