@@ -314,6 +314,8 @@ static void TestNumericHostBuffers()
 int main(int argc, char **argv)
 {
     const bool gpu = argc > 1 && std::strcmp(argv[1], "--gpu") == 0;
+    // unbuffered: a crash (here or at process exit) still leaves every line printed before it in the captured output
+    std::setvbuf(stdout, nullptr, _IONBF, 0);
     TestTensorInfo();
     TestLinearActivationNegative();
     TestLinearResNegative();
@@ -322,5 +324,6 @@ int main(int argc, char **argv)
         TestNumericHostBuffers();
     }
     std::printf("%d checks passed, %d failed\n", g_passed, g_failed);
+    std::printf("exiting\n");
     return g_failed == 0 ? 0 : 1;
 }
