@@ -384,6 +384,7 @@ def cpu_baseline(args, np):
             e["GB/s"] = round(2.0 * (n * k + r * k + 2 * r * n) / t / 1e9, 3)
         per.append(e)
     return {"value": tflops, "unit": "TFLOP/s", "cores": threads, "kind": "port", "cpu_model": cpu_model(),
+            "cflags": O.build_flags(),
             "sample": f"{rows} of {M} rows of C3 (bf16 Linear+GELU_tanh+residual, K={Kd}, N={N}); naive f32-accumulate "
                       f"loop of the reference gtest oracle, OpenMP over rows, {dt:.1f} s; the aarch64 SVE/KML path "
                       f"cannot build on this x86 host",
@@ -572,13 +573,21 @@ def main():
                                                    [bench_c3_dtype(args, torch, K, c) for c in ("C3-f16", "C3-s8")])
     cpu = None if (args.no_cpu_baseline or only) else cpu_baseline(args, np)
 
-    traffic = None
+    # the calibrated counter bytes of the C3 kernel, reported only when they were captured from a library built from
+    # the same kernel sources as the one benched (the digest compiled into libkudnn_hip.so)
+    traffic, traffic_note = None, "no counter capture (profiles/traffic_c3.json) for this build"
     tf = ROOT / "profiles" / "traffic_c3.json"
+    built = K.lib().kudnn_pingpong_source_digest().decode()
     if tf.exists():
         try:
-            traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
-        except Exception:
-            traffic = None
+            rec = json.loads(tf.read_text())
+            if rec.get("source_digest") == built:
+                traffic, traffic_note = rec.get("hbm_bytes_per_launch"), f"captured from kernel sources {built}"
+            else:
+                traffic_note = (f"profiles/traffic_c3.json was captured from kernel sources {rec.get('source_digest')}, "
+                                f"the library was built from {built}")
+        except Exception as e:
+            traffic_note = f"profiles/traffic_c3.json unreadable: {e}"
 
     out = {
         "metric": METRIC,
@@ -599,6 +608,7 @@ def main():
                    "weight_layout": "BA ([N][K], nn.Linear)", "plan": c3["plan"]},
         "roofline": {"bound": "mfma", "achieved": round(c3["tflops"], 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(c3["tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                     "traffic_note": traffic_note,
                      "kernel_ms": round(c3["ms"], 4), "alg_flops": c3["flops"], "alg_bytes": c3["alg_bytes"]},
         "cpu_baseline": cpu,
         "decode": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()} for d in decode],

@@ -241,6 +241,10 @@ KUDNN_HIP_API int kudnn_linear_postops_run_noalloc(kudnn_linear_postops_t plan, 
 /* Name of the kernel family the dispatcher chose for a plan ("mfma_bf16_256x256", "skinny_bf16_nt", ...).
  * Writes at most `len` bytes including the terminating NUL. */
 KUDNN_HIP_API int kudnn_plan_describe(const void *plan, char *buf, int len);
+/* Digest of the source files the ping-pong GEMM kernel was compiled from (16 hex digits; "unknown" when built
+ * without one). No counterpart in the reference: it lets a measurement record say which kernel build its counters
+ * came from, so counters captured from another build are not reported as this one's. */
+KUDNN_HIP_API const char *kudnn_pingpong_source_digest(void);
 
 #ifdef __cplusplus
 }

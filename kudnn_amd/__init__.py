@@ -132,6 +132,7 @@ _SIGS = {
     "kudnn_linear_postops_destroy": ([_P], ctypes.c_int),
     "kudnn_linear_postops_run_noalloc": ([_P, _P, _P, _P, _P, _P, ctypes.c_float, _P], ctypes.c_int),
     "kudnn_plan_describe": ([_P, ctypes.c_char_p, ctypes.c_int], ctypes.c_int),
+    "kudnn_pingpong_source_digest": ([], ctypes.c_char_p),
 }
 
 

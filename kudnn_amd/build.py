@@ -10,6 +10,7 @@ Run ``python -m kudnn_amd.build`` or call :func:`build_all`.
 from __future__ import annotations
 
 import concurrent.futures
+import hashlib
 import os
 import shutil
 import subprocess
@@ -40,6 +41,20 @@ HIP_FLAGS = [
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-fvisibility=hidden", "-Wall", "-Wextra"]
 
 
+# The ping-pong kernel's translation unit and the headers it compiles from: their digest is compiled into the library
+# (kudnn_pingpong_source_digest) and recorded with the C3 traffic counters, which bench.py reports only for a library
+# built from the same sources.
+PINGPONG_SOURCES = ["gemm_pingpong.hip", "device_common.h", "kmajor_copy.h", "kernels.h", "plan_types.h"]
+
+
+def pingpong_digest() -> str:
+    """SHA-256 (first 16 hex digits) over the names and bytes of PINGPONG_SOURCES."""
+    h = hashlib.sha256()
+    for name in PINGPONG_SOURCES:
+        h.update(name.encode() + b"\0" + (CSRC / name).read_bytes() + b"\0")
+    return h.hexdigest()[:16]
+
+
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -68,7 +83,8 @@ def build_hip(verbose: bool = False) -> Path:
     for src in HIP_SOURCES:
         obj = BUILD / (Path(src).stem + ".o")
         objs.append(obj)
-        jobs.append([hipcc, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        extra = [f'-DKUDNN_PINGPONG_DIGEST="{pingpong_digest()}"'] if src == "gemm_pingpong.hip" else []
+        jobs.append([hipcc, *HIP_FLAGS, *extra, "-c", str(CSRC / src), "-o", str(obj)])
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(4, len(jobs))) as ex:
         list(ex.map(lambda c: _run(c, verbose), jobs))
     out = LIB / "libkudnn_hip.so"

@@ -918,10 +918,11 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
     const size_t wsS = mfma4 ? align256(kudnn_gemm_workspace_bytes(shape, batches, core.cfg, core.computeDt)) : 0;
     // the ping-pong kernel's tail split: partial tiles and arrival counters
     const bool pingpong = core.engine == ENGINE_MFMA_BF16 && core.cfg == KUDNN_CFG_BF16_PINGPONG_256x256;
-    // K slices write f32 sums of the whole output per slice; in the fixed scratch of the allocation-free entry point
-    // only when they fit (else the launch runs without them)
-    bool slicesOk = true;
-    size_t wsK = pingpong ? align256(kudnn_pingpong_workspace_bytes(shape, batches, core.computeDt, true)) : 0;
+    // K slices write f32 sums of the whole output per slice. The allocation-free entry point runs the same kernels
+    // as the allocating one, so a plan whose slices and packs exceed its fixed scratch is refused there (Acquire),
+    // never run unsliced: that would change the f32 summation order and so the results.
+    const bool slicesOk = true;
+    const size_t wsK = pingpong ? align256(kudnn_pingpong_workspace_bytes(shape, batches, core.computeDt, true)) : 0;
     void *ws = nullptr;
     bool acquired = false;
     // u8 operands of an integer GEMM: correction vectors (row sums of the other packed operand, scaled by 128)
@@ -930,10 +931,6 @@ int LaunchCore(const GemmCore &core, const EpiExtras &x, const void *a, const vo
     const int64_t copiesA = allBroadcast(core.A) ? 1 : batches, copiesB = allBroadcast(core.B) ? 1 : batches;
     const size_t wsCm = bU8 ? align256(static_cast<size_t>(copiesA * core.M) * sizeof(int32_t)) : 0;
     const size_t wsCn = aU8 ? align256(static_cast<size_t>(copiesB * core.N) * sizeof(int32_t)) : 0;
-    if (pingpong && wsp.Fixed() && wsA + wsB + wsS + wsK + wsCm + wsCn > wsp.FixedBytes()) {
-        slicesOk = false;
-        wsK = align256(kudnn_pingpong_workspace_bytes(shape, batches, core.computeDt, false));
-    }
     uint32_t *counters = nullptr;
     if (wsA + wsB + wsS + wsK + wsCm + wsCn > 0) {
         int arc = KUDNN_STATUS_SUCCESS;

@@ -52,6 +52,7 @@
 
 #include "device_common.h"
 #include "kernels.h"
+#include "kmajor_copy.h"
 
 using namespace kudnn_dev;
 
@@ -458,9 +459,9 @@ constexpr int kSlotFloats = kBM * kBN;  // one 256 x 256 accumulator tile
 // address lane 4 jj + i / 4 for jj = 0..3, that is n0 + i at k0 .. k0 + 3 (measured on gfx950). Two such reads give
 // a lane its 8 k. In a half-wave the four rows sit at four distinct 64-byte offsets modulo 256 bytes, so the reads are
 // free of bank conflicts. Needs K a multiple of 64 (no edge along k) and N of 8. At an edge along n, a k-row's copy
-// runs past column N into the first columns of the next k-row (the last k-row's into zeros: the resource ends at the
-// operand's last byte, so the range check blanks the rest); those values reach only accumulator columns >= N, which
-// the epilogues never store.
+// runs past column N into the first columns of the next k-row; the last k-row's copy goes through a resource that
+// starts at its own first row and ends at the operand's last byte, so the range check blanks the chunks past the end
+// (kmajor_copy.h). Those values reach only accumulator columns >= N, which the epilogues never store.
 //
 // CT: operand type, KUDNN_DT_BF16 / F16 / S8. SK: false for the data-parallel launch (block -> one whole tile),
 // true for the tail launch (block -> a range of k-iterations over one or more tiles). BKM: B is K-major (bf16 / f16,
@@ -514,12 +515,10 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
     const int lr = lane >> 3, ls = lane & 7;
     const uint32_t loA0 = lr * lda + static_cast<uint32_t>((ls ^ (lr >> 1)) * 16);
     const uint32_t loA1 = lr * lda + static_cast<uint32_t>((ls ^ (4 + (lr >> 1))) * 16);
-    // K-major B: a 1 KB copy covers rows 2q, 2q+1 of the k-tile; lane -> row 2q + lane / 32, LDS slot lane % 32,
-    // source chunk slot ^ (4 * (row % 4)), where row % 4 = 2 (q & 1) + lane / 32
-    const uint32_t kmRow = static_cast<uint32_t>(lane >> 5), kmSlot = static_cast<uint32_t>(lane & 31);
-    const uint32_t loB0 = BKM ? kmRow * ldb + ((kmSlot ^ (4u * kmRow)) * 16u)
+    // K-major B: a 1 KB copy covers rows 2q, 2q+1 of the k-tile (kmajor_copy.h); the lane offsets of even and odd q
+    const uint32_t loB0 = BKM ? kudnn_km::lane_voff(ldb, static_cast<uint32_t>(lane), 0u)
                               : lr * ldb + static_cast<uint32_t>((ls ^ (lr >> 1)) * 16);
-    const uint32_t loB1 = BKM ? kmRow * ldb + ((kmSlot ^ (4u * (2u + kmRow))) * 16u)
+    const uint32_t loB1 = BKM ? kudnn_km::lane_voff(ldb, static_cast<uint32_t>(lane), 1u)
                               : lr * ldb + static_cast<uint32_t>((ls ^ (4 + (lr >> 1))) * 16);
     auto copyA = [&](int q, int t, uint4 *dst) __attribute__((always_inline)) {
         const uint32_t off = static_cast<uint32_t>(m0 + q * 8) * lda + static_cast<uint32_t>((kb + t) * kRowBytes);
@@ -530,7 +529,8 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
         }
     };
     auto copyB = [&](int q, int t, uint4 *dst) __attribute__((always_inline)) {
-        const uint32_t off = BKM ? static_cast<uint32_t>((kb + t) * 64 + 2 * q) * ldb + static_cast<uint32_t>(n0) * ES
+        const uint32_t off = BKM ? kudnn_km::block_off(ldb, static_cast<uint32_t>(n0) * ES, static_cast<uint32_t>(kb + t),
+                                                       static_cast<uint32_t>(q))
                                  : static_cast<uint32_t>(n0 + q * 8) * ldb + static_cast<uint32_t>((kb + t) * kRowBytes);
         if constexpr (SK) {
             copy_block(B, bytesB, off, (q & 1) ? loB1 : loB0, dst + q * 8 * kKC);
@@ -545,6 +545,7 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
     const uint32_t sLo0 = g == 0 ? loA0 : loB0, sLo1 = g == 0 ? loA1 : loB1;
 
     bool fullTile = false;  // the segment's tile lies wholly inside the matrix (set per segment)
+    bool fullN = false;     // the segment's tile lies wholly inside the matrix along n (set per segment)
     // LDS byte address of the buffer k-tile I goes to: operand 0 = A (double-buffered), 1 = B (triple-buffered)
     auto ldsOf = [&](auto ic, int operand) __attribute__((always_inline)) -> uint32_t {
         constexpr int I = decltype(ic)::value;
@@ -616,18 +617,30 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
                                                                       : ldsOf(std::integral_constant<int, I + 2>{}, 1));
             if (tt < nk) {
                 const uint32_t kofs = static_cast<uint32_t>((kb + tt) * kRowBytes);
-                if (BKM && g == 1) {
-                    // K-major B (never at an edge): the k-tile's 64 rows from its first byte at column n0, two rows
-                    // per copy
-                    const uint32_t tileOff = static_cast<uint32_t>((kb + tt) * 64) * sLd +
-                                             static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(n0)) * ES;
+                if (BKM && g == 1 && fullN) {
+                    // K-major B, a tile inside the matrix along n: the k-tile's 64 rows through one resource from its
+                    // first byte at column n0, two rows per copy, the row pair in the scalar offset (which the range
+                    // check does not cover, so this form is kept to tiles whose columns all lie inside every k-row)
+                    const uint32_t tileOff = kudnn_km::tile_off(
+                        sLd, static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(n0)) * ES, static_cast<uint32_t>(kb + tt));
                     const i32x4_rs_t rs = make_rsrc(sX + tileOff, sBytes - tileOff);
                     asm volatile("s_nop 4" ::: "memory");  // wait states after VALU writes of the SGPRs the copies read
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
                         const int q = p * 8 + j;
-                        copy_lds_fast(rs, (q & 1) ? sLo1 : sLo0, static_cast<uint32_t>(q * 2) * sLd,
+                        copy_lds_fast(rs, (q & 1) ? sLo1 : sLo0, kudnn_km::tile_soff(sLd, static_cast<uint32_t>(q)),
                                       dl + static_cast<uint32_t>(q * 8 * kKC * 16));
+                    }
+                } else if (BKM && g == 1) {
+                    // K-major B, a tile that crosses column N: a resource per copy from the copy's first row, so the
+                    // range check blanks the chunks of the last k-row that lie past the operand's end
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int q = p * 8 + j;
+                        copy_block_edge(sX, sBytes,
+                                        kudnn_km::block_off(sLd, static_cast<uint32_t>(n0) * ES, static_cast<uint32_t>(kb + tt),
+                                                            static_cast<uint32_t>(q)),
+                                        (q & 1) ? sLo1 : sLo0, dl + static_cast<uint32_t>(q * 8 * kKC * 16));
                     }
                 } else if (fullTile) {
                     // one resource from the k-tile's first byte: the lane's row and chunk in the vector offset, the
@@ -719,6 +732,7 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
         }
         const int sR0 = g == 0 ? m0 : n0;
         fullTile = m0 + kBM <= M && n0 + kBN <= N;
+        fullN = kudnn_km::whole_tile(static_cast<uint32_t>(n0), static_cast<uint32_t>(N));
         // prologue: A(0), B(0), B(1); wave w copies 8-row blocks 4w .. 4w+3 of each
 #pragma unroll
         for (int j = 0; j < 4; ++j) copyA(wave * 4 + j, 0, a0);
@@ -1298,6 +1312,15 @@ void kudnn_pingpong_split(const GemmOperands &op, int64_t batches, int ct, int *
     *dpTiles = s.D;
     *tailTiles = s.nTail;
     *iters = s.L;
+}
+
+// The build passes the digest of this file and the headers it compiles from (kudnn_amd/build.py).
+#ifndef KUDNN_PINGPONG_DIGEST
+#define KUDNN_PINGPONG_DIGEST "unknown"
+#endif
+extern "C" __attribute__((visibility("default"))) const char *kudnn_pingpong_source_digest(void)
+{
+    return KUDNN_PINGPONG_DIGEST;
 }
 
 int kudnn_launch_gemm_pingpong(const GemmOperands &op, const EpiParams &ep, int64_t batches, int ct, void *ws,

@@ -87,6 +87,7 @@ def lib() -> ctypes.CDLL:
             "oracle_cpu_baseline": ([ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, P, P, P, P,
                                      ctypes.c_int, P, ctypes.c_int, ctypes.c_float, ctypes.c_int], ctypes.c_int),
             "oracle_max_threads": ([], ctypes.c_int),
+            "oracle_build_flags": ([], ctypes.c_char_p),
         }
         for name, (args, res) in sig.items():
             fn = getattr(l, name)
@@ -272,3 +273,8 @@ def cpu_baseline(dt, M, N, K, X, W, bias, R, Y, act, act_alpha, threads, r_mul=F
 
 def max_threads() -> int:
     return lib().oracle_max_threads()
+
+
+def build_flags() -> str:
+    """The C compiler flags liboracle.so was built with."""
+    return lib().oracle_build_flags().decode()

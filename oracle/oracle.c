@@ -749,6 +749,12 @@ int oracle_cpu_baseline(int dtype, int64_t M, int64_t N, int64_t K, const void *
     return 0;
 }
 
+/* The compiler flags this library was built with (the Makefile passes them), reported beside the CPU baseline. */
+#ifndef ORACLE_BUILD_FLAGS
+#define ORACLE_BUILD_FLAGS "unknown"
+#endif
+const char *oracle_build_flags(void) { return ORACLE_BUILD_FLAGS; }
+
 int oracle_max_threads(void)
 {
 #ifdef _OPENMP

@@ -799,3 +799,55 @@ def test_single_weight_row(M, Kd, expect):
     ref = c.clone_empty()
     O.linear_act(x.t, w.t, ref, b.t, O.ACT_RELU, 0.0)
     compare(from_device(dc, O.BF16), ref.buf, O.BF16, plan.describe())
+
+
+def _integer_case(dims, dt, layout, seed, lo, hi):
+    # integer values in [lo, hi]: every GEMM partial sum is exact in f32 (and the stage value in bf16 when |sum| <= 256)
+    c = Case(dims, dt, layout, zero=True)
+    v = np.random.default_rng(seed).integers(lo, hi + 1, size=c.t.buf.size).astype(np.float32)
+    c.t.buf[:] = O.from_f32_rne(v, dt)
+    return c
+
+
+@pytest.mark.parametrize("dt,cfg,M,N,Kd", [
+    (O.F32, "10", 130, 200, 64), (O.F32, "11", 70, 136, 64), (O.F32, "12", 8, 96, 64),
+    (O.BF16, "4", 300, 520, 128), (O.BF16, "3", 100, 200, 64), (O.BF16, "20", 12, 300, 256),
+    (O.BF16, "22", 4, 300, 256), (O.BF16, None, 1, 300, 256)])
+@pytest.mark.parametrize("op", ["res_ext", "bin_ext"])
+def test_ext_gamma_fma_bit_exact(monkeypatch, dt, cfg, M, N, Kd, op):
+    # RES_EXT / BIN_EXT with gamma = 0.3 (not a power of two, so res * gamma is inexact): the epilogue computes
+    # fmaf(res, gamma, c) with one rounding, as the oracle does (the contraction GCC applies to c + res * gamma on
+    # aarch64). Integer-valued X, W and bias make the GEMM stage exact in any summation order, so the output must equal
+    # the oracle bit for bit; a separate multiply and add would differ wherever the product's rounding matters.
+    if cfg is not None:
+        monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", cfg)
+    gamma = 0.3
+    hi = 1 if dt == O.BF16 else 3
+    x = _integer_case([M, Kd], dt, None, 900 + M, -hi, hi)
+    w = _integer_case([Kd, N], dt, "BA", 901 + M, -hi, hi)
+    b = _integer_case([1, N], dt, None, 902 + M, -2, 2)
+    res = Case([M, N], dt, seed=903 + M, lo=-3.0, hi=3.0)
+    out = Case([M, N], dt, zero=True)
+    if op == "res_ext":
+        c = Case([M, N], dt, zero=True)
+        plan = K.LinearRes(x.desc, w.desc, c.desc, b.desc, res.desc, out.desc, 1.0, 0.0, gamma, O.RES_EXT)
+        dc, dout = zeros_device(c), zeros_device(out)
+        plan.run(x.device(), w.device(), dc, b.device(), res.device(), dout, gamma)
+        rc = c.clone_empty()
+        ref = out.clone_empty()
+        O.linear_res(x.t, w.t, rc, b.t, res.t, ref, O.RES_EXT, gamma)
+    else:
+        plan = K.LinearPostOps(x.desc, w.desc, out.desc, b.desc, binary=K.BIN_EXT, src=res.desc, gamma=gamma)
+        dout = zeros_device(out)
+        plan.run(x.device(), w.device(), dout, b.device(), res.device(), gamma=gamma)
+        ref = out.clone_empty()
+        O.linear_postops(x.t, w.t, ref, b.t, O.ACT_NONE, 0.0, O.BIN_EXT, res.t, gamma)
+    torch.cuda.synchronize()
+    family = {"10": "mfma_f32_128x128", "11": "mfma_f32_64x64", "12": "mfma_f32_kslice_16x32",
+              "4": "mfma_bf16_pingpong", "3": "mfma_bf16_128x128", "20": "skinny_bf16_16xK",
+              "22": "skinny_bf16_gemv_rows_xlds", None: "skinny_bf16_gemv_row"}[cfg]
+    assert plan.describe().startswith(family), plan.describe()
+    got = from_device(dout, dt)
+    diff = np.count_nonzero(got != ref.buf)
+    assert diff == 0, f"{plan.describe()}: {diff} of {got.size} outputs differ from fmaf(res, gamma, c)"
+    assert np.count_nonzero(got) > got.size // 2

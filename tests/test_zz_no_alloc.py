@@ -24,7 +24,8 @@ def _gpu():
 
 
 def _run_both(M, N, Kd, seed):
-    # weight in layout AB (K-major [K][N]): the MFMA kernels read [N][K], so every run packs it into the workspace
+    # weight in layout AB (K-major [K][N]): the ping-pong kernel reads it in place when N is a multiple of 8 and K of
+    # 64 (the plan says kmajorB); the 4-wave kernel, and K tails, pack it into the workspace (packB)
     x = Case([M, Kd], O.BF16, seed=seed, dist="normal", lo=0.0, hi=1.0)
     w = Case([Kd, N], O.BF16, "AB", seed=seed + 1, dist="normal", lo=0.0, hi=0.03)
     b = Case([1, N], O.BF16, seed=seed + 2, lo=-0.1, hi=0.1)
@@ -85,3 +86,24 @@ def test_noalloc_refuses_what_it_cannot_do():
                                               ctypes.c_float(1.0), None)
     assert st == K.BAD_ARGUMENTS
     torch.cuda.synchronize()
+
+
+def test_noalloc_refuses_slices_that_do_not_fit():
+    # 2048 x 8192 x 2560: 80 tiles in 2 K slices (40 MiB of f32 sums) plus the source packed from its [K][M] layout
+    # (32 MiB) exceed the 64 MiB scratch. The allocation-free entry point refuses the plan instead of running it
+    # unsliced, which would change the summation order; the allocating entry point runs it sliced.
+    M, N, Kd = 2048, 2560, 8192
+    dx, dw, dy = K.desc([M, Kd], K.BF16, "BA"), K.desc([Kd, N], K.BF16, "AB"), K.desc([M, N], K.BF16)
+    plan = K.LinearPostOps(dx, dw, dy)
+    assert "kslices=2" in plan.describe() and "packA" in plan.describe(), plan.describe()
+    x = torch.zeros(M * Kd, dtype=torch.int16, device="cuda")
+    w = torch.zeros(Kd * N, dtype=torch.int16, device="cuda")
+    y = torch.full((M * N,), 7, dtype=torch.int16, device="cuda")
+    st = K.lib().kudnn_linear_postops_run_noalloc(plan.handle, x.data_ptr(), w.data_ptr(), y.data_ptr(), None, None,
+                                                  ctypes.c_float(1.0), None)
+    assert st == K.UNSUPPORTED and "workspace" in K.last_error(), K.last_error()
+    torch.cuda.synchronize()
+    assert bool((y == 7).all()), "a refused call wrote its output"
+    plan.run(x, w, y)
+    torch.cuda.synchronize()
+    assert not bool(y.any()), "the allocating entry point did not run the plan"
