@@ -62,6 +62,13 @@ def parse():
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--no-others", action="store_true", help="skip the informational C1 / C2 / C5 lines")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU-baseline sample time")
+    p.add_argument("--summarize-traffic", metavar="DIR", default=None,
+                   help="read rocprofv3 FETCH_SIZE / WRITE_SIZE captures of --only c3 and --only copy from "
+                        "DIR/{c3,copy}_{fetch,write}/run_counter_collection.csv and write profiles/traffic_c3.json "
+                        "(no GPU needed; the digest is the built library's)")
+    p.add_argument("--summarize-counters", metavar="CSV", default=None,
+                   help="print per-dispatch means of every counter of the C3 kernel in a rocprofv3 "
+                        "run_counter_collection.csv, with its duration, clock and MFMA busy fraction (no GPU needed)")
     return p.parse_args()
 
 
@@ -300,6 +307,83 @@ def bench_c3_dtype(args, torch, K, name):
             "frac_peak": rate / peak}
 
 
+C3_KERNEL = "gemm_pingpong_kernel<3, 20, 0, false, false>"  # bf16 operands, GELU_tanh, all-bf16 epilogue form
+
+
+def counter_dispatches(csv_path, kernel_sub):
+    """{dispatch id: {"counters": {name: value summed over the dispatch's rows}, "ns": duration}} for the dispatches
+    of a rocprofv3 run_counter_collection.csv whose kernel name contains kernel_sub."""
+    import csv
+
+    out = {}
+    with open(csv_path, newline="") as f:
+        for row in csv.DictReader(f):
+            if kernel_sub not in row["Kernel_Name"]:
+                continue
+            d = out.setdefault(row["Dispatch_Id"], {"counters": {}, "ns": 0})
+            c = d["counters"]
+            c[row["Counter_Name"]] = c.get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+            d["ns"] = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+    return out
+
+
+def _mean(xs):
+    xs = list(xs)
+    return sum(xs) / len(xs) if xs else float("nan")
+
+
+def summarize_counters(path):
+    """Per-dispatch means of the C3 kernel's counters in one capture, with the clock that GRBM_GUI_ACTIVE gives over
+    the dispatch time (the counter is summed over the 8 XCCs) and the MFMA busy fraction of the 1024 SIMDs."""
+    ds = counter_dispatches(path, C3_KERNEL)
+    names = sorted({n for d in ds.values() for n in d["counters"]})
+    res = {"kernel": C3_KERNEL, "dispatches": len(ds), "mean_us": _mean(d["ns"] / 1e3 for d in ds.values())}
+    for n in names:
+        res[n] = _mean(d["counters"][n] for d in ds.values() if n in d["counters"])
+    if "GRBM_GUI_ACTIVE" in res:
+        clocks = [d["counters"]["GRBM_GUI_ACTIVE"] / 8 / d["ns"] for _, d in sorted(ds.items(), key=lambda kv: int(kv[0]))]
+        res["clock_ghz"] = _mean(clocks)
+        res["clock_ghz_min_max"] = [min(clocks), max(clocks)]
+        res["clock_ghz_last_half"] = _mean(clocks[len(clocks) // 2:])
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in res:
+            res["mfma_busy"] = _mean(d["counters"]["SQ_VALU_MFMA_BUSY_CYCLES"] /
+                                     (d["counters"]["GRBM_GUI_ACTIVE"] / 8 * 1024) for d in ds.values())
+    print(json.dumps(res, indent=1))
+    return res
+
+
+def summarize_traffic(d):
+    """profiles/traffic_c3.json from FETCH_SIZE / WRITE_SIZE captures of the C3 kernel and of the copy-like calibration
+    kernel (torch.neg over 512 MiB bf16: its known bytes give each counter's scale on this part)."""
+    import kudnn_amd as K
+
+    d = Path(d)
+    cap = {k: d / k / "run_counter_collection.csv" for k in ("c3_fetch", "c3_write", "copy_fetch", "copy_write")}
+    c3f = counter_dispatches(cap["c3_fetch"], C3_KERNEL)
+    c3w = counter_dispatches(cap["c3_write"], C3_KERNEL)
+    cpf = counter_dispatches(cap["copy_fetch"], "neg_kernel")
+    cpw = counter_dispatches(cap["copy_write"], "neg_kernel")
+    fetch = _mean(x["counters"]["FETCH_SIZE"] for x in c3f.values())
+    write = _mean(x["counters"]["WRITE_SIZE"] for x in c3w.values())
+    cfetch = _mean(x["counters"]["FETCH_SIZE"] for x in cpf.values())
+    cwrite = _mean(x["counters"]["WRITE_SIZE"] for x in cpw.values())
+    copy_bytes = 512 << 20
+    fs, ws = copy_bytes / (cfetch * 1024), copy_bytes / (cwrite * 1024)
+    rd, wr = fetch * 1024 * fs, write * 1024 * ws
+    alg = 2 * (4096 * 4096 + 11008 * 4096 + 2 * 4096 * 11008)
+    rec = {"kernel": C3_KERNEL, "workload": "C3 4096x4096x11008 bf16 Linear+GELU_tanh+residual add",
+           "source_digest": K.lib().kudnn_pingpong_source_digest().decode(),
+           "dispatches": {"fetch": len(c3f), "write": len(c3w)},
+           "fetch_kib_per_dispatch": round(fetch, 1), "write_kib_per_dispatch": round(write, 1),
+           "copy_fetch_kib_per_dispatch": round(cfetch, 1), "copy_write_kib_per_dispatch": round(cwrite, 1),
+           "copy_bytes_each_way": copy_bytes, "fetch_scale": round(fs, 5), "write_scale": round(ws, 5),
+           "hbm_read_bytes_per_launch": int(rd), "hbm_write_bytes_per_launch": int(wr),
+           "hbm_bytes_per_launch": int(rd + wr), "algorithmic_bytes_per_launch": alg,
+           "traffic_over_algorithmic": round((rd + wr) / alg, 3)}
+    (ROOT / "profiles" / "traffic_c3.json").write_text(json.dumps(rec, indent=1) + "\n")
+    print(json.dumps(rec, indent=1))
+
+
 def cpu_model():
     """The host CPU's model name (as lscpu prints it), from /proc/cpuinfo."""
     try:
@@ -536,6 +620,12 @@ def main():
     import kudnn_amd as K
 
     K.lib()  # no fallback: fail if the HIP library is missing
+    if args.summarize_traffic:
+        summarize_traffic(args.summarize_traffic)
+        return
+    if args.summarize_counters:
+        summarize_counters(args.summarize_counters)
+        return
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
