@@ -15,7 +15,8 @@ the GPU raises its clocks over the first ~100 ms of sustained load, and a timed 
 reports the ramp rather than the kernel (10-15 % slower per step over the first tens of milliseconds).
 
 For profiling, --only c3 runs just the C3 step (JSON line without decode or CPU baseline), --only decode just the
-decode lines, and --only copy runs an
+decode lines (--only decode-sweep: the decode step over M in 2..16 and N in 4096..28672, one JSON line each, the
+measurements behind the skinny dispatch rule), and --only copy runs an
 elementwise copy-like kernel (y = -x, 512 MiB bf16 in, 512 MiB out) whose known traffic calibrates the
 FETCH_SIZE / WRITE_SIZE counters against which the C3 kernel's HBM traffic is read. --only dispatch times a bf16
 Linear + GELU(tanh) over prefill-like shapes under every kernel configuration (forced through KUDNN_HIP_FORCE_CFG and
@@ -27,7 +28,7 @@ freParasMulti) in f32 and bf16, under the planner and under every forced configu
 type.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--prewarm-ms 300]
-                       [--only c3|copy|decode|dispatch|refperf]
+                       [--only c3|copy|decode|decode-sweep|dispatch|refperf]
 """
 from __future__ import annotations
 
@@ -56,7 +57,7 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--prewarm-ms", type=float, default=300.0, help="untimed run time before warmup (clock ramp)")
-    p.add_argument("--only", choices=["c3", "copy", "decode", "dispatch", "refperf"], default=None,
+    p.add_argument("--only", choices=["c3", "copy", "decode", "decode-sweep", "dispatch", "refperf"], default=None,
                    help="profiling modes (see module docstring)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-decode", action="store_true")
@@ -647,6 +648,15 @@ def main():
 
     if args.only == "refperf":
         bench_refperf(args, torch, K)
+        return
+
+    if args.only == "decode-sweep":
+        # the decode step (Linear then element-wise multiply, K = 4096) over M and N, under the planner's choice or
+        # the configuration KUDNN_HIP_FORCE_CFG names: the measurements the skinny dispatch rule is drawn from
+        for m in (2, 3, 4, 5, 6, 8, 10, 12, 16):
+            for n in (4096, 8192, 14336, 28672):
+                d = bench_decode(args, torch, K, n, m)
+                print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}), flush=True)
         return
 
     if args.only == "decode":

@@ -547,9 +547,21 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
     if (core.computeDt != KUDNN_DT_F32) {
         if (core.M <= 16 && lowp16) {
             core.engine = ENGINE_SKINNY_BF16;
-            // M <= 5: the GEMV with X staged in LDS (measured on MI355X at K = 4096, N = 4096 and 14336, it beats the
-            // 16-row MFMA kernel by 1-11 % up to M = 5 and loses from M = 6 on); above, 16-row MFMA tiles
-            core.cfg = core.M == 1 ? KUDNN_CFG_GEMV_BF16 : (core.M <= 5 ? KUDNN_CFG_GEMV_MULTI_BF16 : KUDNN_CFG_SKINNY_BF16);
+            // Measured on MI355X at K = 4096 over M = 2..16 and N = 4096..28672 (bench.py --only decode-sweep):
+            // - M <= 5: the GEMV with X staged in LDS, ahead of the 16-row MFMA kernel by 1-17 % (M = 4, N = 14336:
+            //   20.0 against 22.1 us) and of the K-split GEMV;
+            // - M >= 6, one batch, K <= 4096: the K-split GEMV with X in registers (M = 16, N = 14336: 21.7 against
+            //   23.8 us; N = 4096: 8.9 against 9.5 us);
+            // - otherwise 16-row MFMA tiles.
+            // (its operands addressed with 32-bit offsets: the row pitch is the packed one when an operand is packed)
+            const int64_t chunks = (core.K + 7) / 8;
+            const int64_t lda = core.A.staticPack ? core.kp : core.A.s_r, ldb = core.B.staticPack ? core.kp : core.B.s_r;
+            const bool kgemv = batches == 1 && (chunks + 3) / 4 <= 128 &&
+                               ((core.N - 1) * ldb + chunks * 8) * 2 < (int64_t(1) << 31) &&
+                               ((core.M - 1) * lda + chunks * 8) * 2 < (int64_t(1) << 31);
+            core.cfg = core.M == 1 ? KUDNN_CFG_GEMV_BF16
+                                   : (core.M <= 5 ? KUDNN_CFG_GEMV_MULTI_BF16
+                                                  : (kgemv ? KUDNN_CFG_GEMV_KSPLIT_BF16 : KUDNN_CFG_SKINNY_BF16));
         } else {
             core.engine = ENGINE_MFMA_BF16;
             // Measured on MI355X over prefill-like shapes (M 256..3072, N and K 2048..14336): the ping-pong kernel
@@ -595,13 +607,14 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
                       (((f == KUDNN_CFG_BF16_256x256 || f == KUDNN_CFG_BF16_256x128 || f == KUDNN_CFG_BF16_128x128 ||
                          f == KUDNN_CFG_BF16_PINGPONG_256x256) && mfmaOk) ||
                        (f == KUDNN_CFG_SKINNY_BF16 && core.M >= 2 && core.M <= 16 && lowp16) ||
-                       (f == KUDNN_CFG_GEMV_MULTI_BF16 && core.M >= 2 && core.M <= 8 && lowp16));
+                       (f == KUDNN_CFG_GEMV_MULTI_BF16 && core.M >= 2 && core.M <= 8 && lowp16) ||
+                       (f == KUDNN_CFG_GEMV_KSPLIT_BF16 && core.M >= 2 && core.M <= 16 && lowp16));
         bool okF32 = core.computeDt == KUDNN_DT_F32 &&
                      (f == KUDNN_CFG_F32_128x128 || f == KUDNN_CFG_F32_64x64 || f == KUDNN_CFG_F32_KSLICE_16x32);
         if (okBf16 || okF32) {
             core.cfg = f;
-            core.engine = f == KUDNN_CFG_SKINNY_BF16 || f == KUDNN_CFG_GEMV_MULTI_BF16 ? ENGINE_SKINNY_BF16
-                                                     : (okF32 ? ENGINE_MFMA_F32 : ENGINE_MFMA_BF16);
+            const bool skinny = f == KUDNN_CFG_SKINNY_BF16 || f == KUDNN_CFG_GEMV_MULTI_BF16 || f == KUDNN_CFG_GEMV_KSPLIT_BF16;
+            core.engine = skinny ? ENGINE_SKINNY_BF16 : (okF32 ? ENGINE_MFMA_F32 : ENGINE_MFMA_BF16);
         }
     }
     // A K-major weight (B stored [K][N], N contiguous: C5's W{1,K,N} ABC) is read in place by the ping-pong kernel,
@@ -633,6 +646,7 @@ const char *CfgName(int cfg)
         case KUDNN_CFG_SKINNY_BF16: return "skinny_bf16_16xK";
         case KUDNN_CFG_GEMV_BF16: return "skinny_bf16_gemv_row";
         case KUDNN_CFG_GEMV_MULTI_BF16: return "skinny_bf16_gemv_rows_xlds";
+        case KUDNN_CFG_GEMV_KSPLIT_BF16: return "skinny_bf16_kgemv_xreg";
         default: return "unknown";
     }
 }

@@ -18,6 +18,7 @@ enum {
     KUDNN_CFG_SKINNY_BF16 = 20,
     KUDNN_CFG_GEMV_BF16 = 21,  // M == 1: one wave per weight row, X staged in LDS (skinny engine)
     KUDNN_CFG_GEMV_MULTI_BF16 = 22,  // 2 <= M <= 5 (M <= 8 forced): one wave per weight row, X staged in LDS
+    KUDNN_CFG_GEMV_KSPLIT_BF16 = 23,  // 2 <= M <= 16, K <= 4096, one batch: K split over 8 waves, X in registers
 };
 
 // Returns 0 on success, -1 if the launch failed or cfg is unknown. `ct` is the operand (compute) type of the 16- and

@@ -17,6 +17,7 @@
 //  - operands of 2^31 bytes or more, skinny_bf16_kernel: loads straight into the MFMA operand layout (16 rows x 64
 //    bytes per instruction) with 64-bit addressing, UNR k-steps in flight.
 // Wave 0 (lane m of each wave for the GEMV kernels) runs the fused epilogue.
+#include <algorithm>
 #include <cstdlib>
 #include <utility>
 
@@ -832,6 +833,317 @@ void launch_gemv_multi(const GemmOperands &op, const EpiParams &ep, int64_t batc
     launch_gemv_multi_wv<CT, MR, kMgWaves>(op, ep, batches, stream);
 }
 
+// 2 <= M <= 16, K <= 4096, one batch: the K-split GEMV. The weight is read once, by whole rows, and X stays in
+// registers:
+//  - A workgroup of 8 waves splits K into 8 slices of at most 16 steps of 32 (512 elements). Wave w keeps the X
+//    fragments of its slice (lane: row lane % 16, 8 elements at 32 s + 8 (lane / 16); 64 VGPRs) for every weight row
+//    it reduces. It loads them once, one 1 KB row slice per instruction, through its LDS tile.
+//  - The workgroups (one per CU) take the rows in rounds of 16 G: in round j workgroup b takes the 16 rows from
+//    16 (j G + b), so each round's loads cover one contiguous part of the weight; a last partial round is divided
+//    evenly in whole quads. For each of its rows, wave w loads the row's slice (1 KB, one instruction, non-temporal),
+//    writes the group's 16 rows into its LDS tile and reads them back in the operand layout of
+//    v_mfma_f32_16x16x32_bf16: one MFMA per step sums 32 k of 16 weight rows against 16 rows of X.
+//  - Two groups' loads stay in flight: the registers of a group's rows take the loads of the group two ahead as
+//    soon as the rows are in the tile.
+//  - Each wave keeps its partial 16 x 16 tile of every group in registers; the waves stream without a barrier and
+//    sum their tiles once, through LDS, at the end; then all 512 threads run the epilogue on runs of 4 columns, its
+//    operands loaded at the start.
+// Rows past a slot's count, rows m >= M of X and chunks past K load through an out-of-range buffer offset, which reads
+// zero and fetches nothing.
+// Measured on MI355X at K = 4096 (bench.py --only decode-sweep): M = 16, N = 14336 21.7 us against 23.8 us for the
+// 16-row kernel below (X reloaded per 16 weight rows: as many X bytes as weight bytes); M = 4 loses to the GEMV with
+// X staged in LDS. Variants measured and dropped: the weight loaded straight into the operand layout (16 rows x 64
+// bytes per instruction, 24.4 us), 16 waves with 8-step slices (23.0 us), fewer rows per workgroup for less X per
+// weight byte (each CU's stream is the limit: 192 workgroups 26.2 us). A v_dot2 GEMV does not fit these M: 16 rows
+// of products at N = 14336 are about 13 us of VALU issue against a 17.6 us weight stream.
+constexpr int kKgWaves = 8;        // waves per workgroup: K slices
+constexpr int kKgStepsAll = 128;   // 32-element k-steps of a workgroup at most: K <= 4096, KW waves x KS steps
+constexpr int kKgGroups = 8;       // rounds (16-row groups) per workgroup at most
+
+template <int... I, typename F>
+__device__ __forceinline__ void sfor_kg_impl(std::integer_sequence<int, I...>, F &&f)
+{
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void sfor_kg(F &&f)
+{
+    sfor_kg_impl(std::make_integer_sequence<int, N>{}, f);
+}
+
+template <int CT, int KW, int NG, int ACT, int FORM>
+__device__ __forceinline__ void kgemv_body(const GemmOperands &op, const EpiParams &ep, int interleave)
+{
+    // LDS: a tile of 16 rows x kXPitch chunks per wave (133 KB), which stages the wave's X slice, then each group's
+    // weight rows, then the waves' partial tiles; and the result tile (NG groups x 16 rows x 16 floats)
+    constexpr int KS = kKgStepsAll / KW;        // k-steps per wave at most
+    constexpr int kSliceCh = 4 * KS;           // chunks of a row in a wave's slice
+    constexpr int RPI = 64 / kSliceCh;         // rows per load instruction (1 KB per instruction)
+    constexpr int kXPitch = kSliceCh + 1;      // chunks per tile row: the 16 rows of a fragment read hit distinct banks
+    __shared__ u32x4_t wtile[KW * 16 * kXPitch];
+    __shared__ float res[NG * 16][16];
+    u32x4_t *lds = wtile;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r16 = lane & 15, q = lane >> 4;
+    const int M = static_cast<int>(op.M);
+    const int chunks = static_cast<int>((op.K + 7) / 8);
+    const int steps = (chunks + 3) / 4;
+    const int s0 = steps * wave / KW, ns = steps * (wave + 1) / KW - s0;  // ns <= KS (host-checked)
+    // Slot g of the workgroup holds rows n0(g) .. n0(g) + cnt(g) - 1 (cnt 0: none), every slot starting on a whole quad
+    // (each run of 4 columns keeps the alignment the vector epilogue assumes). Two ways to deal the rows:
+    //  - contiguous (interleave 0): workgroup b takes quads Q b / G .. Q (b + 1) / G - 1 (G = gridDim.x), slot g the
+    //    16 rows from the range's start + 16 g;
+    //  - in rounds (interleave 1): in round j workgroup b takes the 16 rows from 16 (j G + b), so each round's loads
+    //    cover one contiguous part of the weight across the GPU; the rows of a last partial round are divided evenly
+    //    in whole quads. The host takes it when each workgroup's range would span a multiple of 128 KB: workgroups
+    //    walking such ranges in step load a few memory channels at a time (N = 8192, K = 4096: 17.3 us contiguous
+    //    against 13.8-14.9 in rounds; N = 14336: 21.7 against 22.2).
+    const int64_t G = gridDim.x, b = blockIdx.x;
+    const int64_t quads = (op.N + 3) / 4;
+    const int64_t rbeg = quads * b / G * 4, rend = min(quads * (b + 1) / G * 4, op.N);
+    const int64_t full = op.N / (16 * G);                     // whole rounds
+    const int64_t remQuads = (op.N - full * 16 * G + 3) / 4;  // quads of the last partial round (at most 4 G)
+    auto slot = [&](int g, int64_t &n0, int64_t &cnt) __attribute__((always_inline)) {
+        if (!interleave) {
+            n0 = rbeg + 16 * g;
+            cnt = max(min(rend - n0, int64_t(16)), int64_t(0));
+        } else if (g < full) {
+            n0 = 16 * (g * G + b);
+            cnt = 16;
+        } else if (g == full && remQuads > 0) {
+            const int64_t q0 = remQuads * b / G, q1 = remQuads * (b + 1) / G;
+            n0 = full * 16 * G + 4 * q0;
+            cnt = min(4 * (q1 - q0), op.N - n0);
+        } else {
+            n0 = 0;
+            cnt = 0;
+        }
+    };
+    constexpr uint32_t kOut = 0xFFFFFFF0u;  // past any range below: reads zero
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void *>(op.b), (short)0, static_cast<int>(operand_extent(op.N, op.ldb, chunks)), 0x00020000);
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void *>(op.a), (short)0, static_cast<int>(operand_extent(op.M, op.lda, chunks)), 0x00020000);
+    const uint32_t wpitch = static_cast<uint32_t>(op.ldb) * 2u, xpitch = static_cast<uint32_t>(op.lda) * 2u;
+
+    // the epilogue's runs of 4 columns: run t is row t % M, quad (t / M) % 4 of slot t / (4 M); the first KW x 64 runs
+    // (all of them at the decode shapes) load their operands before the loop
+    const int runs = 4 * M * NG;
+    const EpiBatch ob{0, 0, 0, 0, 0, 0};
+    auto run_at = [&](int t, int &m, int64_t &n, int64_t &lim) __attribute__((always_inline)) {
+        int64_t n0, cnt;
+        slot(t / (4 * M), n0, cnt);
+        m = t % M;
+        n = n0 + 4 * ((t / M) % 4);
+        lim = n0 + cnt;
+    };
+    EpiPre4 pre{make_uint2(0u, 0u), make_uint2(0u, 0u), make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
+    if (tid < runs) {
+        int em;
+        int64_t en, elim;
+        run_at(tid, em, en, elim);
+        if (en < elim) {
+            pre = epi_prefetch4(ep, ob, em, en, elim);
+        }
+    }
+
+    // the weight loads of slot g: instruction i reads rows RPI i .. RPI i + RPI - 1 of the slot over the slice, one
+    // chunk per lane (lane -> row RPI i + lane / kSliceCh, chunk lane % kSliceCh: 1 KB of whole rows per instruction);
+    // rows past the slot's count load nothing
+    const int lrow = lane / kSliceCh, lch = lane % kSliceCh;
+    const int wkc = 4 * s0 + lch;
+    const uint32_t wcol = lch < 4 * ns && wkc < chunks ? static_cast<uint32_t>(wkc) * 16u : kOut;
+    auto load_w = [&](int g, u32x4_t (&w)[KS]) __attribute__((always_inline)) {
+        int64_t n0, cnt;
+        slot(g, n0, cnt);
+#pragma unroll
+        for (int i = 0; i < KS; ++i) {
+            const int r = RPI * i + lrow;
+            const bool in = r < cnt && wcol != kOut;
+            w[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, in ? static_cast<uint32_t>(n0 + r) * wpitch + wcol : kOut, 0, 2);
+        }
+    };
+    // X fragments of this wave's slice, loaded once: each of the slice's 16 rows by one instruction (the slice's up to 64
+    // chunks of the row, one per lane, whole cache lines), through the wave's LDS area into the operand layout (lane:
+    // row lane % 16, chunk 4 s + lane / 16). Loading the fragments directly reads 16 rows x 64 bytes per instruction,
+    // which the memory path serves at half the rate of whole lines.
+    u32x4_t xf[KS], w0[KS], w1[KS];
+    {
+        u32x4_t xrow[KS];
+#pragma unroll
+        for (int i = 0; i < KS; ++i) {
+            const int m = RPI * i + lrow;
+            xrow[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, wcol != kOut && m < M ? static_cast<uint32_t>(m) * xpitch + wcol : kOut,
+                                                           0, 0);
+        }
+        // the first two groups' weight loads go out behind X's: waiting for X (the older loads) leaves them in flight;
+        // the wave's tile takes X first, then (after the fragment reads below) the weight rows
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(0, w0);
+        load_w(1, w1);
+        __builtin_amdgcn_sched_barrier(0);
+        u32x4_t *xs = lds + wave * 16 * kXPitch;
+#pragma unroll
+        for (int i = 0; i < KS; ++i) xs[(RPI * i + lrow) * kXPitch + lch] = xrow[i];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int s = 0; s < KS; ++s) xf[s] = xs[r16 * kXPitch + 4 * s + q];
+        // the first group's weight rows overwrite the tile after these reads
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    // one group: its rows (in flight since two groups earlier) through the wave's LDS tile into the operand layout
+    // (lane: row lane % 16, chunk 4 s + lane / 16); as soon as the rows are in the tile their registers take the loads
+    // of the group two ahead, so two groups' loads stay in flight through this group's fragment reads and MFMAs. Each
+    // wave keeps its partial tile of every group in registers: the waves stream independently, with no barrier until
+    // the end.
+    f32x4_t acc[NG];
+    auto group = [&](int g, f32x4_t &a, u32x4_t (&wc)[KS]) __attribute__((always_inline)) {
+        a = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        u32x4_t *wt = wtile + wave * 16 * kXPitch;
+#pragma unroll
+        for (int i = 0; i < KS; ++i) wt[(RPI * i + lrow) * kXPitch + lch] = wc[i];
+        // the loads are issued before any fragment read or MFMA of this group (the scheduler otherwise sank them below
+        // the MFMAs and reused their registers, which made each group wait for the one before)
+        __builtin_amdgcn_sched_barrier(0);
+        if (g + 2 < NG) {
+            load_w(g + 2, wc);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        u32x4_t wf[KS];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) wf[s] = wt[r16 * kXPitch + 4 * s + q];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) a = mfma16<CT>(wf[s], xf[s], a);
+        // the next group's tile writes come after these reads (the MFMAs consumed them)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    // NG groups, unrolled and unconditional (a slot without rows loads nothing and stores nothing): two named register
+    // sets alternate, and with straight-line code the compiler's wait counts stay exact (at a loop head, or after a
+    // skipped group, it waited for every load in flight, the next group's included)
+    sfor_kg<NG>([&](auto gc) __attribute__((always_inline)) {
+        constexpr int g = decltype(gc)::value;
+        if constexpr (g % 2 == 0) {
+            group(g, acc[g], w0);
+        } else {
+            group(g, acc[g], w1);
+        }
+    });
+    // the waves' partial tiles, in the tiles' place once every wave is done with its own; then their sum per element
+    // (lane l of a partial tile holds D[n = 4 (l / 16) + i][m = l % 16] in component i) into the result tile
+    __syncthreads();
+    f32x4_t(*part)[KW][64] = reinterpret_cast<f32x4_t(*)[KW][64]>(wtile);
+    static_assert(sizeof(wtile) >= sizeof(f32x4_t) * NG * KW * 64, "partial tiles fit the weight tiles");
+#pragma unroll
+    for (int g = 0; g < NG; ++g) part[g][wave][lane] = acc[g];
+    __syncthreads();
+    for (int t = tid; t < NG * 256; t += KW * 64) {
+        const int g = t >> 8, l = (t >> 2) & 63, i = t & 3;
+        float sum = part[g][0][l][i];
+#pragma unroll
+        for (int w = 1; w < KW; ++w) sum += part[g][w][l][i];
+        res[16 * g + 4 * (l >> 4) + i][l & 15] = sum;
+    }
+    __syncthreads();
+    for (int t = tid; t < runs; t += KW * 64) {
+        int m;
+        int64_t n, lim;
+        run_at(t, m, n, lim);
+        if (n >= lim) {
+            continue;
+        }
+        const int r = 16 * (t / (4 * M)) + 4 * ((t / M) % 4);  // the run's first row in the result tile
+        const float v[4] = {res[r][m], res[r + 1][m], res[r + 2][m], res[r + 3][m]};
+        const EpiPre4 p = t == tid ? pre : epi_prefetch4(ep, ob, m, n, lim);
+        if constexpr (FORM == EPI_FORM_GENERIC) {
+            epi_apply4_pre(ep, ob, m, n, lim, v, p);
+        } else {
+            epi_fixed4<ACT, FORM>(ep, ob, m, n, lim, v, p);
+        }
+    }
+}
+
+template <int CT, int KW, int NG, int ACT, int FORM>
+__global__ __launch_bounds__(KW * 64) void kgemv_compact_kernel(RowsArgs r, int interleave)
+{
+    GemmOperands op;
+    EpiParams ep;
+    unpack_rows_args<ACT, FORM>(r, op, ep);
+    kgemv_body<CT, KW, NG, ACT, FORM>(op, ep, interleave);
+}
+
+template <int CT, int KW, int NG>
+__global__ __launch_bounds__(KW * 64) void kgemv_kernel(GemmOperands op, EpiParams ep, int interleave)
+{
+    kgemv_body<CT, KW, NG, 0, EPI_FORM_GENERIC>(op, ep, interleave);
+}
+
+// Whether the K-split GEMV takes the call: one batch, 2 <= M <= 16, at most kKgStepsAll k-steps (K <= 4096),
+// operands with 32-bit offsets.
+bool kgemv_eligible(const GemmOperands &op, int64_t batches)
+{
+    const int64_t chunks = (op.K + 7) / 8;
+    return batches == 1 && op.M >= 2 && op.M <= 16 && (chunks + 3) / 4 <= kKgStepsAll &&
+           operand_extent(op.N, op.ldb, chunks) < (int64_t(1) << 31) && operand_extent(op.M, op.lda, chunks) < (int64_t(1) << 31);
+}
+
+template <int CT, int KW, int NG>
+void launch_kgemv_ng(const GemmOperands &op, const EpiParams &ep, dim3 grid, int interleave, hipStream_t stream)
+{
+    decltype(&kgemv_compact_kernel<CT, KW, NG, 0, EPI_FORM_BF16>) ck = nullptr;
+    if constexpr (CT == KUDNN_DT_BF16) {
+        ck = pick_compact(ep, compact_call(ep, grid), [](auto actc, auto formc) {
+            return kgemv_compact_kernel<CT, KW, NG, decltype(actc)::value, decltype(formc)::value>;
+        });
+    }
+    if (ck != nullptr) {
+        hipLaunchKernelGGL(ck, grid, dim3(KW * 64), 0, stream, rows_args(op, ep), interleave);
+    } else {
+        hipLaunchKernelGGL((kgemv_kernel<CT, KW, NG>), grid, dim3(KW * 64), 0, stream, op, ep, interleave);
+    }
+}
+
+template <int CT>
+int launch_kgemv(const GemmOperands &op, const EpiParams &ep, hipStream_t stream)
+{
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0) {
+        (void)hipGetLastError();
+        cus = 256;
+    }
+    // one workgroup per CU (8 waves of about 210 VGPRs and 133 KB of LDS fill a CU), more when N needs more than
+    // kKgGroups rounds of 16 rows each; never more workgroups than quads of rows
+    const int64_t quads = (op.N + 3) / 4;
+    const int64_t G = std::min<int64_t>(quads, std::max<int64_t>(cus, (op.N + 16 * kKgGroups - 1) / (16 * kKgGroups)));
+    const dim3 grid(static_cast<unsigned>(G));
+    // rows dealt in rounds when each workgroup's contiguous range would span a multiple of 128 KB (the kernel's slot
+    // rule); slots: the whole rounds plus one for a partial round, or the range's 16-row groups; instances for 1-4, 8
+    const int64_t rows = (quads + G - 1) / G * 4;
+    const int interleave = (rows * op.ldb * 2) % (int64_t(128) << 10) == 0 ? 1 : 0;
+    const int64_t full = op.N / (16 * G);
+    const int64_t ng = interleave ? full + (op.N > full * 16 * G ? 1 : 0) : (rows + 15) / 16;
+    switch (ng) {
+        case 1: launch_kgemv_ng<CT, kKgWaves, 1>(op, ep, grid, interleave, stream); break;
+        case 2: launch_kgemv_ng<CT, kKgWaves, 2>(op, ep, grid, interleave, stream); break;
+        case 3: launch_kgemv_ng<CT, kKgWaves, 3>(op, ep, grid, interleave, stream); break;
+        case 4: launch_kgemv_ng<CT, kKgWaves, 4>(op, ep, grid, interleave, stream); break;
+        default: launch_kgemv_ng<CT, kKgWaves, kKgGroups>(op, ep, grid, interleave, stream); break;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 // Launches the row kernel of form (KW, PIPE): the compact kernel when the call is single-batch in a fixed form with one
 // of the compiled activations, the generic kernel otherwise.
 template <int CT, int KW, bool PIPE>
@@ -890,6 +1202,9 @@ int launch_skinny(const GemmOperands &op, const EpiParams &ep, int64_t batches, 
     }
     if (gemv_eligible(op)) {
         return launch_gemv<CT>(op, ep, batches, stream);
+    }
+    if (cfg == KUDNN_CFG_GEMV_KSPLIT_BF16 && kgemv_eligible(op, batches)) {
+        return launch_kgemv<CT>(op, ep, stream);
     }
     if (fits) {
         // fewer than 2 row groups per CU: split K over 16 waves (one workgroup per CU); otherwise 8 (two per CU)

@@ -155,20 +155,29 @@ def test_batch_dim_of_output_must_match_operands():
 
 
 def test_decode_kernel_rule(monkeypatch):
-    # M <= 5: the GEMV with X staged in LDS (M = 1 named apart); 6 <= M <= 16: 16-row MFMA tiles (bf16 and f16)
+    # M <= 5: the GEMV with X staged in LDS (M = 1 named apart); 6 <= M <= 16, one batch, K <= 4096: the K-split GEMV
+    # with X in registers; otherwise 16-row MFMA tiles (bf16 and f16)
     assert plan_of(1, 4096, 4096).describe().startswith("skinny_bf16_gemv_row ")
     for M in (2, 3, 4, 5):
         assert plan_of(M, 4096, 14336).describe().startswith("skinny_bf16_gemv_rows_xlds"), M
         assert plan_of(M, 1000, 300, K.F16).describe().startswith("skinny_f16_gemv_rows_xlds"), M
     for M in (6, 8, 16):
-        assert plan_of(M, 4096, 14336).describe().startswith("skinny_bf16_16xK"), M
-    # the overrides: the 16-row kernel for 2 <= M <= 16, the staged GEMV for 2 <= M <= 8
+        assert plan_of(M, 4096, 14336).describe().startswith("skinny_bf16_kgemv_xreg"), M
+        assert plan_of(M, 1000, 300, K.F16).describe().startswith("skinny_f16_kgemv_xreg"), M
+    assert plan_of(16, 4104, 4096).describe().startswith("skinny_bf16_16xK")  # K > 4096
+    batched = K.LinearPostOps(K.desc([2, 8, 512], K.BF16, "ABC"), K.desc([2, 512, 300], K.BF16, "ACB"),
+                              K.desc([2, 8, 300], K.BF16, "ABC"))
+    assert batched.describe().startswith("skinny_bf16_16xK"), batched.describe()
+    # the overrides: the 16-row kernel and the K-split GEMV for 2 <= M <= 16, the staged GEMV for 2 <= M <= 8
     monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "20")
     assert plan_of(4, 4096, 4096).describe().startswith("skinny_bf16_16xK")
+    assert plan_of(12, 4096, 4096).describe().startswith("skinny_bf16_16xK")
     assert plan_of(1, 4096, 4096).describe().startswith("skinny_bf16_gemv_row ")
+    monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "23")
+    assert plan_of(2, 4096, 4096).describe().startswith("skinny_bf16_kgemv_xreg")
     monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "22")
     assert plan_of(8, 4096, 4096).describe().startswith("skinny_bf16_gemv_rows_xlds")
-    assert plan_of(9, 4096, 4096).describe().startswith("skinny_bf16_16xK")
+    assert plan_of(9, 4096, 4096).describe().startswith("skinny_bf16_kgemv_xreg")
     assert plan_of(64, 4096, 4096).describe().startswith("mfma_bf16")
 
 

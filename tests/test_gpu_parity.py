@@ -302,7 +302,9 @@ def test_c4_skinny_mul(M, N):
 
 @pytest.mark.parametrize("M,N,Kd", [(9, 4112, 2100), (12, 4096, 2304), (16, 4104, 4096), (12, 1024, 2100),
                                     (8, 8200, 2100), (7, 8192, 4096), (6, 8192, 2304)])
-def test_skinny_rows_forms(M, N, Kd):
+def test_skinny_rows_forms(monkeypatch, M, N, Kd):
+    # the 16-row kernel (forced: the planner takes the K-split GEMV for these one-batch calls with K <= 4096)
+    monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "20")
     # M > 8 with >= 256 row groups, and M = 7, 8 with >= 512, run 2-wave workgroups with the next weight block in
     # flight and X's rows loaded whole through a second LDS tile (rows m >= M read zero): an odd count of 256-element
     # K blocks (K = 2100 packs to 9 blocks, 2304 is exactly 9) ends one wave on a block with no successor; N not a
@@ -778,13 +780,18 @@ def test_operands_of_2_gib(case):
     compare(got, ref.buf, dt, f"{case} {plan.describe()}")
 
 
-@pytest.mark.parametrize("M,Kd,expect", [(20480, 128, "mfma_bf16_pingpong"), (16, 4096, "skinny_bf16_16xK"),
-                                         (9, 256, "skinny_bf16_16xK"), (6, 64, "skinny_bf16_16xK"),
+@pytest.mark.parametrize("M,Kd,expect", [(20480, 128, "mfma_bf16_pingpong"), (16, 4096, "skinny_bf16_kgemv_xreg"),
+                                         (9, 256, "skinny_bf16_kgemv_xreg"), (6, 64, "skinny_bf16_kgemv_xreg"),
+                                         (16, 4096, "skinny_bf16_16xK"), (9, 256, "skinny_bf16_16xK"),
+                                         (6, 64, "skinny_bf16_16xK"), (16, 4104, "skinny_bf16_16xK"),
                                          (3, 64, "skinny_bf16_gemv_rows_xlds"), (5, 4104, "skinny_bf16_gemv_rows_xlds"),
                                          (1, 520, "skinny_bf16_gemv_row")])
-def test_single_weight_row(M, Kd, expect):
+def test_single_weight_row(monkeypatch, M, Kd, expect):
     # N = 1: the weight descriptor's row pitch is 0 (a dimension of size one), so the kernels that bound their reads by
-    # a buffer range take the operand's extent from its last row, not from rows x pitch (which is 0)
+    # a buffer range take the operand's extent from its last row, not from rows x pitch (which is 0); the 16-row
+    # kernel is forced where the planner takes the K-split GEMV
+    if expect == "skinny_bf16_16xK" and Kd <= 4096:
+        monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "20")
     N = 1
     x = Case([M, Kd], O.BF16, seed=270, dist="normal", lo=0.0, hi=1.0)
     w = Case([Kd, N], O.BF16, "BA", seed=271, dist="normal", lo=0.0, hi=0.05)
