@@ -15,7 +15,7 @@ the GPU raises its clocks over the first ~100 ms of sustained load, and a timed 
 reports the ramp rather than the kernel (10-15 % slower per step over the first tens of milliseconds).
 
 For profiling, --only c3 runs just the C3 step (JSON line without decode or CPU baseline), --only decode just the
-decode lines (--only decode-sweep: the decode step over M in 2..16 and N in 4096..28672, one JSON line each, the
+decode lines (--only decode-sweep: the decode step over M in 1..16 and N in 4096..28672, one JSON line each, the
 measurements behind the skinny dispatch rule), and --only copy runs an
 elementwise copy-like kernel (y = -x, 512 MiB bf16 in, 512 MiB out) whose known traffic calibrates the
 FETCH_SIZE / WRITE_SIZE counters against which the C3 kernel's HBM traffic is read. --only dispatch times a bf16
@@ -25,10 +25,11 @@ planner's own choice, one JSON line per shape, then an f32 Gemm over grids of
 256-640 tiles of 128 x 128 under the 128 x 128 and 64 x 64 configurations: the measurements the dispatcher's rules are
 drawn from. --only refperf times KuDNN::Gemm on the reference's own perf shape sets (the matmul gtest's freParas and
 freParasMulti) in f32 and bf16, under the planner and under every forced configuration, one JSON line per shape and
-type.
+type. --only torch times C3's shape through PyTorch's own ops (the bf16 GEMM alone, then GEMM + GELU + add unfused)
+for comparison.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--prewarm-ms 300]
-                       [--only c3|copy|decode|decode-sweep|dispatch|refperf]
+                       [--only c3|copy|decode|decode-sweep|dispatch|refperf|torch]
 """
 from __future__ import annotations
 
@@ -57,7 +58,8 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--prewarm-ms", type=float, default=300.0, help="untimed run time before warmup (clock ramp)")
-    p.add_argument("--only", choices=["c3", "copy", "decode", "decode-sweep", "dispatch", "refperf"], default=None,
+    p.add_argument("--only", choices=["c3", "copy", "decode", "decode-sweep", "dispatch", "refperf", "torch"],
+                   default=None,
                    help="profiling modes (see module docstring)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-decode", action="store_true")
@@ -197,6 +199,27 @@ def bench_c3(args, torch, K):
         "flops": flops,
         "alg_bytes": alg_bytes,
     }
+
+
+def bench_torch_c3(args, torch):
+    """C3's shape through PyTorch's own ops, for comparison only (not this library): the bf16 GEMM alone
+    (`torch.nn.functional.linear`, which ROCm's PyTorch hands to hipBLASLt), and the whole C3 step as that GEMM
+    followed by separate GELU_tanh and add kernels. Same inputs and timing as the C3 line."""
+    M, Kd, N = 4096, 4096, 11008
+    bf = torch.bfloat16
+    x = synth(torch, (M, Kd), 0, "normal", 0.0, 1.0, bf)
+    w = synth(torch, (N, Kd), 1, "normal", 0.0, 0.02, bf)
+    r = synth(torch, (M, N), 3, "normal", 0.0, 1.0, bf)
+    y = torch.empty(M, N, device="cuda", dtype=bf)
+    stream = torch.cuda.current_stream()
+    F = torch.nn.functional
+    flops = 2.0 * M * N * Kd
+    for name, fn in (("torch linear (bf16 GEMM only)", lambda i=0: torch.matmul(x, w.t(), out=y)),
+                     ("torch linear + gelu(tanh) + add (unfused)",
+                      lambda i=0: torch.add(F.gelu(F.linear(x, w), approximate="tanh"), r, out=y))):
+        ms, _ = time_launches(fn, args.steps, args.warmup, torch, stream, args.prewarm_ms)
+        print(json.dumps({"op": name, "M": M, "K": Kd, "N": N, "ms": round(ms, 4),
+                          "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1)}), flush=True)
 
 
 def bench_decode(args, torch, K, N, M=1):
@@ -650,10 +673,14 @@ def main():
         bench_refperf(args, torch, K)
         return
 
+    if args.only == "torch":
+        bench_torch_c3(args, torch)
+        return
+
     if args.only == "decode-sweep":
         # the decode step (Linear then element-wise multiply, K = 4096) over M and N, under the planner's choice or
         # the configuration KUDNN_HIP_FORCE_CFG names: the measurements the skinny dispatch rule is drawn from
-        for m in (2, 3, 4, 5, 6, 8, 10, 12, 16):
+        for m in (1, 2, 3, 4, 5, 6, 8, 10, 12, 16):
             for n in (4096, 8192, 14336, 28672):
                 d = bench_decode(args, torch, K, n, m)
                 print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}), flush=True)
