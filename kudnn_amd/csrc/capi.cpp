@@ -338,7 +338,7 @@ struct OperandSpec {
     int64_t s_k = 0;       // stride along k
     int64_t bs[3] = {0, 0, 0};
     bool staticPack = false;  // must be packed whatever the pointer alignment
-    bool kmajor = false;      // B read in place as [K][N] (N contiguous) by the ping-pong kernel
+    bool kmajor = false;      // B read in place as [K][N] (N contiguous): ping-pong (16-bit) or 4-wave fp32 kernels
 };
 
 struct TensorSpec {
@@ -627,6 +627,17 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
         core.B.s_r == 1 && core.B.s_k >= core.N && core.B.s_k % 8 == 0 && bBatchAligned && core.K % 64 == 0 &&
         core.N % 8 == 0 && core.K * core.B.s_k * 2 < (int64_t(1) << 31) &&
         core.M * std::max<int64_t>(core.A.s_r, core.kp) * 2 < (int64_t(1) << 31) && !std::getenv("KUDNN_HIP_PACK_KMAJOR")) {
+        core.B.kmajor = true;
+        core.B.staticPack = false;
+    }
+    // The same for an fp32 weight stored [K][N] (the reference's Matmul mode passes W in ABCDE,
+    // matmul_gtest.cpp:248-257), read in place by the 4-wave fp32 kernels (128 x 128 and 64 x 64): it needs K a
+    // multiple of the 32-deep k-tile, N a multiple of 4 (whole 16-byte column chunks), 16-byte aligned k-rows and
+    // batches. The k-slice kernel of the smallest grids still packs it.
+    if (core.engine == ENGINE_MFMA_F32 && (core.cfg == KUDNN_CFG_F32_128x128 || core.cfg == KUDNN_CFG_F32_64x64) &&
+        core.B.dt == KUDNN_DT_F32 && core.B.s_r == 1 && core.B.s_k >= core.N && core.B.s_k % 4 == 0 &&
+        core.B.bs[0] % 4 == 0 && core.B.bs[1] % 4 == 0 && core.B.bs[2] % 4 == 0 && core.K % 32 == 0 &&
+        core.N % 4 == 0 && !std::getenv("KUDNN_HIP_PACK_KMAJOR")) {
         core.B.kmajor = true;
         core.B.staticPack = false;
     }

@@ -33,6 +33,8 @@
 //    accumulators in its slot of the workspace and takes a ticket from the tile's arrival counter, and the split that
 //    draws the last ticket sums the slots in split order (the same bits whichever split finishes last) and runs the
 //    epilogue. No workgroup waits for another.
+//  - fp32 weights stored [K][N] (N contiguous) are read in place (BKM): each k-tile of B is copied as 32 k-rows of the
+//    tile's columns and read one float per k (see the kernel's comment).
 // Requirements (the dispatcher packs operands otherwise): K a multiple of the k-tile, rows 16-byte
 // aligned. Rows past M / N are clamped (read but never stored).
 #include <algorithm>
@@ -112,11 +114,18 @@ constexpr bool kSplittable = (CT == KUDNN_DT_F32 && BM == 64 && BN == 64) ||
                              ((CT == KUDNN_DT_BF16 || CT == KUDNN_DT_F16) && BM == 128 && BN == 128);
 
 // CT: compute (operand) type, KUDNN_DT_F32 / BF16 / F16 / S8. SPLIT: grid.z splits K (see SplitArgs).
-template <int CT, int BM, int BN, int WM, int WN, int ST, int ACT, int FORM, bool SPLIT = false>
+// BKM (fp32 only): B is stored [K][N] (N contiguous, k-row pitch ldb) and read in place. A k-tile of B is then 32
+// k-rows of the tile's BN columns; the LDS DMA copies them as they lie, k-row k's 128-byte column segments in the
+// order seg ^ ((k >> 2) & 1), and a lane reads its column's 4 consecutive k as 4 single floats (gfx950 has no 32-bit
+// transposing LDS read). The segment order puts the two lane halves' reads (k and k + 4, see read_frags) in different
+// halves of the 64 banks, so each ds_read_b32 is conflict-free. Needs K a multiple of 32, N of 4 (columns past N are
+// clamped to the last whole chunk, read but never stored), 16-byte aligned k-rows and batches.
+template <int CT, int BM, int BN, int WM, int WN, int ST, int ACT, int FORM, bool SPLIT = false, bool BKM = false>
 __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands op, EpiParams ep, int tilesM,
                                                                   int tilesN, int group, SplitArgs sa)
 {
     constexpr bool F32 = CT == KUDNN_DT_F32;
+    static_assert(!BKM || (F32 && BN >= 64), "the in-place K-major B is an fp32 path with at least two column segments");
     using T = typename std::conditional<F32, float, typename std::conditional<CT == KUDNN_DT_S8, int8_t, uint16_t>::type>::type;
     constexpr int EPC = 16 / static_cast<int>(sizeof(T));  // elements per 16-byte chunk
     constexpr int kBK = kChunks * EPC;                      // k-tile in elements
@@ -168,9 +177,20 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
     }
 #pragma unroll
     for (int j = 0; j < GB; ++j) {
-        int64_t r = n0 + (wave * GB + j) * 8 + lrow8;
-        r = r < N ? r : N - 1;
-        pb[j] = B + r * op.ldb + lchunk * EPC;
+        if constexpr (BKM) {
+            // LDS chunk p of the B tile holds k-row p / (BN / 4), segment position (p % (BN / 4)) / 8, chunk p % 8
+            constexpr int kCpr = BN / 4;  // 16-byte chunks per k-row of the tile
+            const int p = (wave * GB + j) * 64 + lane;
+            const int k = p / kCpr, rem = p % kCpr;
+            const int seg = (rem >> 3) ^ ((k >> 2) & 1);
+            int64_t n = n0 + seg * 32 + (rem & 7) * 4;
+            n = n + 4 <= N ? n : N - 4;
+            pb[j] = B + k * op.ldb + n;
+        } else {
+            int64_t r = n0 + (wave * GB + j) * 8 + lrow8;
+            r = r < N ? r : N - 1;
+            pb[j] = B + r * op.ldb + lchunk * EPC;
+        }
     }
 
     auto issue_tile = [&](int buf, int64_t k0) {
@@ -181,7 +201,7 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
         }
 #pragma unroll
         for (int j = 0; j < GB; ++j) {
-            __builtin_amdgcn_global_load_lds(static_cast<const void *>(pb[j] + k0),
+            __builtin_amdgcn_global_load_lds(static_cast<const void *>(pb[j] + (BKM ? k0 * op.ldb : k0)),
                                              (lds_void *)(&sB[buf][(wave * GB + j) * 64]), 16, 0, 0);
         }
     };
@@ -233,8 +253,17 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
             }
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
-                const int row = wn * TN + j * 32 + lrow;
-                vb[slot][j] = sB[cur][row * kChunks + swz(row, c)];
+                if constexpr (BKM) {
+                    // column wn TN + j 32 + lrow at k = 8 s + 4 h + q, q = 0..3: segment wn TN / 32 + j, stored at
+                    // position segment ^ h in k-rows 8 s + 4 h .. + 3
+                    const float *col = reinterpret_cast<const float *>(&sB[cur][0]) + (8 * s + 4 * lhalf) * BN +
+                                       (((wn * TN) / 32 + j) ^ lhalf) * 32 + lrow;
+                    vb[slot][j] = make_uint4(__builtin_bit_cast(uint32_t, col[0]), __builtin_bit_cast(uint32_t, col[BN]),
+                                             __builtin_bit_cast(uint32_t, col[2 * BN]), __builtin_bit_cast(uint32_t, col[3 * BN]));
+                } else {
+                    const int row = wn * TN + j * 32 + lrow;
+                    vb[slot][j] = sB[cur][row * kChunks + swz(row, c)];
+                }
             }
         };
         read_frags(0, 0);
@@ -471,31 +500,31 @@ int splitk_splits(const GemmOperands &op, int64_t batches, int BM, int BN, int k
 }
 
 // Launches the variant of the kernel that the epilogue's activation and tensor types select.
-template <int CT, int BM, int BN, int WM, int WN, int ST, bool SPLIT>
+template <int CT, int BM, int BN, int WM, int WN, int ST, bool SPLIT, bool BKM = false>
 int launch_kernel(const GemmOperands &op, const EpiParams &ep, dim3 grid, int group, int tilesM, int tilesN,
                   const SplitArgs &sa, hipStream_t stream)
 {
-    decltype(&gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, 0, EPI_FORM_GENERIC, SPLIT>) kernel = nullptr;
+    decltype(&gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, 0, EPI_FORM_GENERIC, SPLIT, BKM>) kernel = nullptr;
     // the fixed form compiled for this compute type
     constexpr int kForm = CT == KUDNN_DT_F32 ? EPI_FORM_F32 : (CT == KUDNN_DT_F16 ? EPI_FORM_F16 : EPI_FORM_BF16);
     if (epi_form(ep) == kForm) {
         switch (ep.act) {
             case KUDNN_ACT_UNIMPLEMENTED:
-                kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_UNIMPLEMENTED, kForm, SPLIT>;
+                kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_UNIMPLEMENTED, kForm, SPLIT, BKM>;
                 break;
-            case KUDNN_ACT_RELU: kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_RELU, kForm, SPLIT>; break;
-            case KUDNN_ACT_SWISH: kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_SWISH, kForm, SPLIT>; break;
+            case KUDNN_ACT_RELU: kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_RELU, kForm, SPLIT, BKM>; break;
+            case KUDNN_ACT_SWISH: kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_SWISH, kForm, SPLIT, BKM>; break;
             case KUDNN_ACT_GELU_TANH:
-                kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_GELU_TANH, kForm, SPLIT>;
+                kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_GELU_TANH, kForm, SPLIT, BKM>;
                 break;
             case KUDNN_ACT_GELU_ERF:
-                kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_GELU_ERF, kForm, SPLIT>;
+                kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, KUDNN_ACT_GELU_ERF, kForm, SPLIT, BKM>;
                 break;
             default: break;
         }
     }
     if (kernel == nullptr) {
-        kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, 0, EPI_FORM_GENERIC, SPLIT>;  // activation read at run time
+        kernel = gemm_mfma_kernel<CT, BM, BN, WM, WN, ST, 0, EPI_FORM_GENERIC, SPLIT, BKM>;  // activation read at run time
     }
     hipLaunchKernelGGL(kernel, grid, dim3(WM * WN * 64), 0, stream, op, ep, tilesM, tilesN, group, sa);
     return hipGetLastError() == hipSuccess ? 0 : -1;
@@ -530,6 +559,19 @@ int launch_cfg(const GemmOperands &op, const EpiParams &ep, int64_t batches, int
             grid.z = static_cast<unsigned>(splits);
             sa.part = static_cast<float *>(ws);
             sa.cnt = counters;
+        }
+        if constexpr (CT == KUDNN_DT_F32) {
+            if (op.b_kmajor) {
+                // the weight read in place as [K][N] (the planner checked the kernel's requirements)
+                if constexpr (kSplittable<CT, BM, BN>) {
+                    if (splits > 1) {
+                        return launch_kernel<CT, BM, BN, WM, WN, ST, true, true>(op, ep, grid, group, tilesM, tilesN, sa, stream);
+                    }
+                }
+                return launch_kernel<CT, BM, BN, WM, WN, ST, false, true>(op, ep, grid, group, tilesM, tilesN, sa, stream);
+            }
+        } else if (op.b_kmajor) {
+            return -1;  // only the ping-pong kernel reads a 16-bit K-major weight
         }
         if constexpr (kSplittable<CT, BM, BN>) {
             if (splits > 1) {

@@ -50,7 +50,8 @@ struct GemmOperands {
     int64_t M, N, K;
     int64_t lda, ldb;
     int64_t a_bs[3], b_bs[3];  // batch strides (elements), same batch dims as EpiParams::bdim
-    int b_kmajor;  // 1: B is stored [K][N] (N contiguous, row pitch ldb along k); only the ping-pong kernel reads it
+    int b_kmajor;  // 1: B is stored [K][N] (N contiguous, row pitch ldb along k): the 16-bit ping-pong kernel and the
+                   // 4-wave fp32 kernels read it
 };
 
 #endif  // KUDNN_PLAN_TYPES_H
