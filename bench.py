@@ -26,10 +26,10 @@ planner's own choice, one JSON line per shape, then an f32 Gemm over grids of
 drawn from. --only refperf times KuDNN::Gemm on the reference's own perf shape sets (the matmul gtest's freParas and
 freParasMulti) in f32 and bf16, under the planner and under every forced configuration, one JSON line per shape and
 type. --only torch times C3's shape through PyTorch's own ops (the bf16 GEMM alone, then GEMM + GELU + add unfused)
-for comparison.
+for comparison. --only c1 prints the C1 line alone.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--prewarm-ms 300]
-                       [--only c3|copy|decode|decode-sweep|dispatch|refperf|torch]
+                       [--only c3|c1|copy|decode|decode-sweep|dispatch|refperf|torch]
 """
 from __future__ import annotations
 
@@ -58,7 +58,7 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--prewarm-ms", type=float, default=300.0, help="untimed run time before warmup (clock ramp)")
-    p.add_argument("--only", choices=["c3", "copy", "decode", "decode-sweep", "dispatch", "refperf", "torch"],
+    p.add_argument("--only", choices=["c3", "c1", "copy", "decode", "decode-sweep", "dispatch", "refperf", "torch"],
                    default=None,
                    help="profiling modes (see module docstring)")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -675,6 +675,11 @@ def main():
 
     if args.only == "torch":
         bench_torch_c3(args, torch)
+        return
+
+    if args.only == "c1":
+        d = bench_config(args, torch, K, "C1")
+        print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}))
         return
 
     if args.only == "decode-sweep":

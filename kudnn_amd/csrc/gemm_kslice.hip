@@ -1,9 +1,10 @@
 // f32 GEMM for grids too small to fill the chip with output tiles (the fp32 Linear of the reference's
 // LinearActivationTests, 128 x 1024 x 1024, is 32 tiles of 64 x 64): one workgroup per 16 x 32 output tile, its NW
-// waves splitting K into interleaved 16-element chunks (chunk c goes to wave c % NW). Each wave accumulates the whole
-// 16 x 32 tile on v_mfma_f32_16x16x4_f32 from operands loaded straight into registers, the NW partial tiles are summed
-// through LDS in wave order, and the generic epilogue stores the tile. There is no workspace and no hand-off between
-// workgroups, so the kernel's latency is one pass of loads and MFMAs plus one LDS reduction.
+// waves splitting K. Each wave accumulates the whole 16 x 32 tile on v_mfma_f32_16x16x4_f32, the NW partial tiles are
+// summed through LDS in wave order, and the epilogue stores the tile. There is no workspace and no hand-off between
+// workgroups, so the kernel's latency is one pass of loads and MFMAs plus one LDS reduction. Two forms (kslice_body):
+// K a multiple of 256 up to 2048 (C1), 8 waves loading whole 128-byte lines through a per-wave LDS tile; otherwise 4
+// waves loading interleaved 16-element chunks (chunk c goes to wave c % NW) straight into the operand layout.
 //
 // Operand layout: A [M][K] and B [N][K], both contiguous along K, 16-byte aligned rows, K a multiple of 16 (the
 // planner packs otherwise, with zero padding up to a whole number of 32-element k-tiles).
@@ -31,12 +32,27 @@ constexpr int kAhead = 2;          // chunks per batch of loads (two batches in 
 // ACT / FORM: a fixed epilogue form (the activation and the tensor types compiled in) or EPI_FORM_GENERIC. The generic
 // epilogue is a long chain of run-time branches whose first pass on each CU misses the instruction cache: for a
 // kernel this short that is a large part of its time, so the common forms are compiled out.
-template <int NW, int ACT, int FORM>
+// CPW > 0 (K = 16 NW CPW, CPW even): K is cut into pairs of chunks (32 k: one 128-byte line of each row) and wave w
+// takes pairs w, w + NW, w + 2 NW, ... (at any time the waves read neighbouring lines of each row). A pair is loaded
+// as whole lines: instruction i reads 8 of the wave's 48 rows (A's 16, then B's 32), lane -> row lane / 8, 16-byte
+// piece lane % 8. All of a wave's loads are issued before its first MFMA, as straight-line code, so the compiler's
+// wait before each pair counts only that pair's loads. Each pair then goes through the wave's own LDS tile (48 rows x
+// 8 pieces, piece j of row r in slot j ^ (r % 8): the row-wise writes and the operand-layout reads are both
+// conflict-free) into the MFMA operand layout. Measured on C1 (graph-replayed), with the MFMAs removed the operand
+// layout's loads (16 rows x 64 bytes per instruction) took 7.35 us and whole lines 4.15 us; the kernel went from 8.0
+// to 6.0-6.1 us (4 waves with contiguous K ranges 6.8, a barrier between the waves' pairs of loads 6.4, 16 waves 6.3).
+// Past the first pair's arrival the MFMAs bound it: C1 is 4096 cycles of v_mfma_f32_16x16x4_f32 per SIMD.
+// CPW = 0: any K, two batches of kAhead interleaved chunks in flight per wave, loaded in the operand layout.
+template <int NW, int CPW, int ACT, int FORM>
 __device__ __forceinline__ void kslice_body(const GemmOperands &op, const EpiParams &ep, int tilesN)
 {
-    constexpr int kPer = kTM * kTN / (NW * 64);  // output elements per thread in the epilogue
-    static_assert(kPer * NW * 64 == kTM * kTN, "the tile must divide over the threads");
+    constexpr int kElems = kTM * kTN;
+    // output elements per thread in the epilogue (with more threads than elements, the first kElems take one each)
+    constexpr int kPer = kElems > NW * 64 ? kElems / (NW * 64) : 1;
+    static_assert(kPer * NW * 64 == kElems || (kPer == 1 && NW * 64 > kElems), "the tile must divide over the threads");
     __shared__ f32x4_t part[NW][2][64];
+    constexpr int kRows = kTM + 2 * 16;  // a wave's rows: A's 16, B's 32
+    __shared__ f32x4_t tile[CPW > 0 ? NW : 1][kRows * 8];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: the K loop's branches are scalar
@@ -64,7 +80,7 @@ __device__ __forceinline__ void kslice_body(const GemmOperands &op, const EpiPar
         const float *psrc = ep.bin != KUDNN_BINARY_NONE ? static_cast<const float *>(ep.src) : fa;
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
-            const int t = threadIdx.x + i * NW * 64;
+            const int t = min(static_cast<int>(threadIdx.x) + i * NW * 64, kElems - 1);
             const int l = t & 63, e = (t >> 6) & 3, h = t >> 8;
             const int64_t m = min(m0 + 4 * (l >> 4) + e, op.M - 1), n = min(n0 + 16 * h + (l & 15), op.N - 1);
             const int64_t bi = ep.bias != nullptr ? ob.bias + m * ep.bias_sm + n * ep.bias_sn : 0;
@@ -113,17 +129,75 @@ __device__ __forceinline__ void kslice_body(const GemmOperands &op, const EpiPar
             }
         }
     };
-    // two register sets alternate: the next batch's loads are in flight while the current batch is multiplied
-    f32x4_t a0[kAhead], p0[kAhead], q0[kAhead], a1[kAhead], p1[kAhead], q1[kAhead];
-    load(wave, a0, p0, q0);
-    for (int c = wave; c < chunks; c += 2 * kStep) {
-        load(c + kStep, a1, p1, q1);
-        compute(c, a0, p0, q0);
-        if (c + kStep >= chunks) {
-            break;
+    if constexpr (CPW > 0) {
+        static_assert(CPW % 2 == 0, "whole chunk pairs");
+        constexpr int NP = CPW / 2;  // pairs of chunks: 32 k, one 128-byte line of each row
+        const int lr = lane >> 3, lp = lane & 7;
+        // the rows of load instruction i: A rows 8 i + lr (i < 2), B rows 8 (i - 2) + lr; past M / N: the last row
+        const float *rowp[6];
+#pragma unroll
+        for (int i = 0; i < 6; ++i) {
+            if (i < 2) {
+                const int64_t m = m0 + 8 * i + lr;
+                rowp[i] = static_cast<const float *>(op.a) + aoff + (m < op.M ? m : op.M - 1) * op.lda;
+            } else {
+                const int64_t n = n0 + 8 * (i - 2) + lr;
+                rowp[i] = static_cast<const float *>(op.b) + boff + (n < op.N ? n : op.N - 1) * op.ldb;
+            }
         }
-        load(c + 2 * kStep, a0, p0, q0);
-        compute(c + kStep, a1, p1, q1);
+        const int64_t kw = static_cast<int64_t>(wave) * 32 + 4 * lp;  // pair p of this wave: k from 32 (wave + NW p)
+        f32x4_t ld[NP][6];
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+#pragma unroll
+            for (int i = 0; i < 6; ++i) ld[p][i] = *reinterpret_cast<const f32x4_t *>(rowp[i] + kw + 32 * NW * p);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        f32x4_t *t = tile[wave];
+        const int sw = r & 7;  // the swizzle of operand row r (and of rows 16 + r, 32 + r)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            // row 8 i + lr, piece lp -> slot lp ^ lr (8 i is a multiple of 8)
+#pragma unroll
+            for (int i = 0; i < 6; ++i) t[(8 * i + lr) * 8 + (lp ^ lr)] = ld[p][i];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            // chunk h of the pair: lane (r, q) takes piece 4 h + q of A row r and of B rows r and 16 + r
+            f32x4_t fa[2], fb0[2], fb1[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int slot = (4 * h + q) ^ sw;
+                fa[h] = t[r * 8 + slot];
+                fb0[h] = t[(16 + r) * 8 + slot];
+                fb1[h] = t[(32 + r) * 8 + slot];
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[h][s], fb0[h][s], acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[h][s], fb1[h][s], acc1, 0, 0, 0);
+                }
+            }
+            // the next pair's writes come after these reads
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+    } else {
+        // two register sets alternate: the next batch's loads are in flight while the current batch is multiplied
+        f32x4_t a0[kAhead], p0[kAhead], q0[kAhead], a1[kAhead], p1[kAhead], q1[kAhead];
+        load(wave, a0, p0, q0);
+        for (int c = wave; c < chunks; c += 2 * kStep) {
+            load(c + kStep, a1, p1, q1);
+            compute(c, a0, p0, q0);
+            if (c + kStep >= chunks) {
+                break;
+            }
+            load(c + 2 * kStep, a0, p0, q0);
+            compute(c + kStep, a1, p1, q1);
+        }
     }
 
     // lane holds D[4 * (lane / 16) + e][lane % 16] (+ 16 columns for acc1), e = 0..3. Element t of the tile is then
@@ -134,6 +208,9 @@ __device__ __forceinline__ void kslice_body(const GemmOperands &op, const EpiPar
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
         const int t = threadIdx.x + i * NW * 64;
+        if (t >= kElems) {
+            break;
+        }
         const int l = t & 63, e = (t >> 6) & 3, h = t >> 8;  // source lane, element, column half
         float v = part[0][h][l][e];
 #pragma unroll
@@ -152,10 +229,10 @@ __device__ __forceinline__ void kslice_body(const GemmOperands &op, const EpiPar
 }
 
 // Any call: the whole GemmOperands and EpiParams as arguments.
-template <int NW, int ACT, int FORM>
+template <int NW, int CPW, int ACT, int FORM>
 __global__ __launch_bounds__(NW * 64) void gemm_f32_kslice_kernel(GemmOperands op, EpiParams ep, int tilesN)
 {
-    kslice_body<NW, ACT, FORM>(op, ep, tilesN);
+    kslice_body<NW, CPW, ACT, FORM>(op, ep, tilesN);
 }
 
 // A single-batch call in the f32 form: the fields it uses (120 bytes instead of 380). A smaller argument block
@@ -169,7 +246,7 @@ struct KsArgs {
     int bin, tilesN;
 };
 
-template <int NW, int ACT>
+template <int NW, int CPW, int ACT>
 __global__ __launch_bounds__(NW * 64) void gemm_f32_kslice_compact_kernel(KsArgs r)
 {
     GemmOperands op{};
@@ -198,7 +275,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32_kslice_compact_kernel(KsArgs
     ep.y_sm = r.y_sm;
     ep.y_sn = 1;
     ep.bdim[0] = ep.bdim[1] = ep.bdim[2] = 1;
-    kslice_body<NW, ACT, EPI_FORM_F32>(op, ep, r.tilesN);
+    kslice_body<NW, CPW, ACT, EPI_FORM_F32>(op, ep, r.tilesN);
 }
 
 }  // namespace
@@ -208,6 +285,50 @@ bool kudnn_kslice_eligible(const GemmOperands &op)
     return op.K > 0 && op.K % kChunk == 0 && op.lda % 4 == 0 && op.ldb % 4 == 0 &&
            reinterpret_cast<uintptr_t>(op.a) % 16 == 0 && reinterpret_cast<uintptr_t>(op.b) % 16 == 0;
 }
+
+namespace {
+
+template <int NW, int CPW>
+int launch_kslice(const GemmOperands &op, const EpiParams &ep, int64_t batches, int64_t tilesN, dim3 grid,
+                  hipStream_t stream)
+{
+    const bool f32Form = epi_form(ep, false) == EPI_FORM_F32;
+    if (f32Form && batches == 1 && (ep.bin == KUDNN_BINARY_NONE || ep.src_sn == 1) && ep.y_sn == 1) {
+        decltype(&gemm_f32_kslice_compact_kernel<NW, CPW, 0>) ck = nullptr;
+        switch (ep.act) {
+            case KUDNN_ACT_UNIMPLEMENTED: ck = gemm_f32_kslice_compact_kernel<NW, CPW, KUDNN_ACT_UNIMPLEMENTED>; break;
+            case KUDNN_ACT_RELU: ck = gemm_f32_kslice_compact_kernel<NW, CPW, KUDNN_ACT_RELU>; break;
+            case KUDNN_ACT_SWISH: ck = gemm_f32_kslice_compact_kernel<NW, CPW, KUDNN_ACT_SWISH>; break;
+            case KUDNN_ACT_GELU_TANH: ck = gemm_f32_kslice_compact_kernel<NW, CPW, KUDNN_ACT_GELU_TANH>; break;
+            case KUDNN_ACT_GELU_ERF: ck = gemm_f32_kslice_compact_kernel<NW, CPW, KUDNN_ACT_GELU_ERF>; break;
+            default: break;
+        }
+        if (ck != nullptr) {
+            const KsArgs r{op.a,   op.b,       ep.bias,    ep.src,    ep.y,    op.M,     op.N,     op.K,
+                           op.lda, op.ldb,     ep.bias_sm, ep.bias_sn, ep.src_sm, ep.y_sm, ep.alpha, ep.gamma,
+                           ep.act_alpha, ep.bin, static_cast<int>(tilesN)};
+            hipLaunchKernelGGL(ck, grid, dim3(NW * 64), 0, stream, r);
+            return hipGetLastError() == hipSuccess ? 0 : -1;
+        }
+    }
+    decltype(&gemm_f32_kslice_kernel<NW, CPW, 0, EPI_FORM_GENERIC>) kernel = gemm_f32_kslice_kernel<NW, CPW, 0, EPI_FORM_GENERIC>;
+    if (f32Form) {
+        switch (ep.act) {
+            case KUDNN_ACT_UNIMPLEMENTED:
+                kernel = gemm_f32_kslice_kernel<NW, CPW, KUDNN_ACT_UNIMPLEMENTED, EPI_FORM_F32>;
+                break;
+            case KUDNN_ACT_RELU: kernel = gemm_f32_kslice_kernel<NW, CPW, KUDNN_ACT_RELU, EPI_FORM_F32>; break;
+            case KUDNN_ACT_SWISH: kernel = gemm_f32_kslice_kernel<NW, CPW, KUDNN_ACT_SWISH, EPI_FORM_F32>; break;
+            case KUDNN_ACT_GELU_TANH: kernel = gemm_f32_kslice_kernel<NW, CPW, KUDNN_ACT_GELU_TANH, EPI_FORM_F32>; break;
+            case KUDNN_ACT_GELU_ERF: kernel = gemm_f32_kslice_kernel<NW, CPW, KUDNN_ACT_GELU_ERF, EPI_FORM_F32>; break;
+            default: break;
+        }
+    }
+    hipLaunchKernelGGL(kernel, grid, dim3(NW * 64), 0, stream, op, ep, static_cast<int>(tilesN));
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace
 
 int kudnn_launch_gemm_f32_kslice(const GemmOperands &op, const EpiParams &ep, int64_t batches, hipStream_t stream)
 {
@@ -219,39 +340,19 @@ int kudnn_launch_gemm_f32_kslice(const GemmOperands &op, const EpiParams &ep, in
         return -1;
     }
     const dim3 grid(static_cast<unsigned>(tilesM * tilesN), static_cast<unsigned>(batches));
-    constexpr int NW = 4;
-    const bool f32Form = epi_form(ep, false) == EPI_FORM_F32;
-    if (f32Form && batches == 1 && (ep.bin == KUDNN_BINARY_NONE || ep.src_sn == 1) && ep.y_sn == 1) {
-        decltype(&gemm_f32_kslice_compact_kernel<NW, 0>) ck = nullptr;
-        switch (ep.act) {
-            case KUDNN_ACT_UNIMPLEMENTED: ck = gemm_f32_kslice_compact_kernel<NW, KUDNN_ACT_UNIMPLEMENTED>; break;
-            case KUDNN_ACT_RELU: ck = gemm_f32_kslice_compact_kernel<NW, KUDNN_ACT_RELU>; break;
-            case KUDNN_ACT_SWISH: ck = gemm_f32_kslice_compact_kernel<NW, KUDNN_ACT_SWISH>; break;
-            case KUDNN_ACT_GELU_TANH: ck = gemm_f32_kslice_compact_kernel<NW, KUDNN_ACT_GELU_TANH>; break;
-            case KUDNN_ACT_GELU_ERF: ck = gemm_f32_kslice_compact_kernel<NW, KUDNN_ACT_GELU_ERF>; break;
-            default: break;
-        }
-        if (ck != nullptr) {
-            const KsArgs r{op.a,   op.b,       ep.bias,    ep.src,    ep.y,    op.M,     op.N,     op.K,
-                           op.lda, op.ldb,     ep.bias_sm, ep.bias_sn, ep.src_sm, ep.y_sm, ep.alpha, ep.gamma,
-                           ep.act_alpha, ep.bin, static_cast<int>(tilesN)};
-            hipLaunchKernelGGL(ck, grid, dim3(NW * 64), 0, stream, r);
-            return hipGetLastError() == hipSuccess ? 0 : -1;
-        }
-    }
-    decltype(&gemm_f32_kslice_kernel<NW, 0, EPI_FORM_GENERIC>) kernel = gemm_f32_kslice_kernel<NW, 0, EPI_FORM_GENERIC>;
-    if (f32Form) {
-        switch (ep.act) {
-            case KUDNN_ACT_UNIMPLEMENTED:
-                kernel = gemm_f32_kslice_kernel<NW, KUDNN_ACT_UNIMPLEMENTED, EPI_FORM_F32>;
-                break;
-            case KUDNN_ACT_RELU: kernel = gemm_f32_kslice_kernel<NW, KUDNN_ACT_RELU, EPI_FORM_F32>; break;
-            case KUDNN_ACT_SWISH: kernel = gemm_f32_kslice_kernel<NW, KUDNN_ACT_SWISH, EPI_FORM_F32>; break;
-            case KUDNN_ACT_GELU_TANH: kernel = gemm_f32_kslice_kernel<NW, KUDNN_ACT_GELU_TANH, EPI_FORM_F32>; break;
-            case KUDNN_ACT_GELU_ERF: kernel = gemm_f32_kslice_kernel<NW, KUDNN_ACT_GELU_ERF, EPI_FORM_F32>; break;
+    const int64_t chunks = op.K / kChunk;
+    // whole-line loads through LDS with 8 waves when K is a whole number of 16-chunk blocks, up to 8 of them
+    // (K <= 2048: at most 8 pairs of loads in flight per wave); otherwise 4 waves and the operand layout
+    if (chunks % 16 == 0) {
+        switch (chunks / 16) {
+            case 1: return launch_kslice<8, 2>(op, ep, batches, tilesN, grid, stream);
+            case 2: return launch_kslice<8, 4>(op, ep, batches, tilesN, grid, stream);
+            case 3: return launch_kslice<8, 6>(op, ep, batches, tilesN, grid, stream);
+            case 4: return launch_kslice<8, 8>(op, ep, batches, tilesN, grid, stream);
+            case 6: return launch_kslice<8, 12>(op, ep, batches, tilesN, grid, stream);
+            case 8: return launch_kslice<8, 16>(op, ep, batches, tilesN, grid, stream);
             default: break;
         }
     }
-    hipLaunchKernelGGL(kernel, grid, dim3(NW * 64), 0, stream, op, ep, static_cast<int>(tilesN));
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return launch_kslice<4, 0>(op, ep, batches, tilesN, grid, stream);
 }

@@ -187,6 +187,26 @@ def test_f32_kslice_shapes(dims, bias):
     compare(from_device(dc, O.F32), ref.buf, O.F32, plan.describe())
 
 
+@pytest.mark.parametrize("Kd", [512, 768, 1536, 3072])
+def test_f32_kslice_whole_line_forms(Kd):
+    # K in whole 256-element blocks: 8 waves loading whole lines through LDS, 1, 3, 6 (= 16 chunks / 8 waves x 2 .. 12
+    # chunks per wave) pairs per wave; K = 3072 (12 blocks) takes the 4-wave form. Edge tiles in M and N; C1's M and N
+    # otherwise
+    M, N = 120, 1000
+    x = Case([M, Kd], O.F32, seed=66)
+    w = Case([Kd, N], O.F32, "BA", seed=67)
+    b = Case([1, N], O.F32, seed=68, lo=-0.1, hi=0.1)
+    c = Case([M, N], O.F32, zero=True)
+    plan = K.LinearActivation(x.desc, w.desc, c.desc, b.desc, 0.0, 0.0, K.ACT_RELU)
+    assert "kslice" in plan.describe(), plan.describe()
+    dc = zeros_device(c)
+    plan.run(x.device(), w.device(), dc, b.device())
+    torch.cuda.synchronize()
+    ref = c.clone_empty()
+    O.linear_act(x.t, w.t, ref, b.t, O.ACT_RELU, 0.0)
+    compare(from_device(dc, O.F32), ref.buf, O.F32, plan.describe())
+
+
 def test_f32_kslice_batched_and_repeatable():
     # batches in grid.y (a weight per batch); two runs give the same bits
     x = Case([3, 2, 40, 264], O.F32, seed=64)
