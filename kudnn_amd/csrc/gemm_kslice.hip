@@ -3,8 +3,9 @@
 // waves splitting K. Each wave accumulates the whole 16 x 32 tile on v_mfma_f32_16x16x4_f32, the NW partial tiles are
 // summed through LDS in wave order, and the epilogue stores the tile. There is no workspace and no hand-off between
 // workgroups, so the kernel's latency is one pass of loads and MFMAs plus one LDS reduction. Two forms (kslice_body):
-// K a multiple of 256 up to 2048 (C1), 8 waves loading whole 128-byte lines through a per-wave LDS tile; otherwise 4
-// waves loading interleaved 16-element chunks (chunk c goes to wave c % NW) straight into the operand layout.
+// K = 256 c for c = 1, 2, 3, 4, 6, 8, 12, 16 (C1 included), 8 waves loading whole 128-byte lines through a per-wave
+// LDS tile; otherwise 4 waves loading interleaved 16-element chunks (chunk c goes to wave c % NW) straight into the
+// operand layout.
 //
 // Operand layout: A [M][K] and B [N][K], both contiguous along K, 16-byte aligned rows, K a multiple of 16 (the
 // planner packs otherwise, with zero padding up to a whole number of 32-element k-tiles).
@@ -35,8 +36,9 @@ constexpr int kAhead = 2;          // chunks per batch of loads (two batches in 
 // CPW > 0 (K = 16 NW CPW, CPW even): K is cut into pairs of chunks (32 k: one 128-byte line of each row) and wave w
 // takes pairs w, w + NW, w + 2 NW, ... (at any time the waves read neighbouring lines of each row). A pair is loaded
 // as whole lines: instruction i reads 8 of the wave's 48 rows (A's 16, then B's 32), lane -> row lane / 8, 16-byte
-// piece lane % 8. All of a wave's loads are issued before its first MFMA, as straight-line code, so the compiler's
-// wait before each pair counts only that pair's loads. Each pair then goes through the wave's own LDS tile (48 rows x
+// piece lane % 8. A wave's first 8 pairs of loads are issued before its first MFMA, as straight-line code, so the
+// compiler's wait before each pair counts only that pair's loads; past 8 pairs (K > 2048), 6 pairs stay in flight:
+// pair p + 6 is issued into pair p's registers once pair p is in LDS. Each pair then goes through the wave's own LDS tile (48 rows x
 // 8 pieces, piece j of row r in slot j ^ (r % 8): the row-wise writes and the operand-layout reads are both
 // conflict-free) into the MFMA operand layout. Measured on C1 (graph-replayed), with the MFMAs removed the operand
 // layout's loads (16 rows x 64 bytes per instruction) took 7.35 us and whole lines 4.15 us; the kernel went from 8.0
@@ -146,12 +148,16 @@ __device__ __forceinline__ void kslice_body(const GemmOperands &op, const EpiPar
             }
         }
         const int64_t kw = static_cast<int64_t>(wave) * 32 + 4 * lp;  // pair p of this wave: k from 32 (wave + NW p)
-        f32x4_t ld[NP][6];
+        // up to 8 pairs in flight per wave (192 VGPRs): all of them when NP <= 8; otherwise 6, pair p + 6 issued into
+        // pair p's registers as soon as pair p is in the LDS tile
+        constexpr int WIN = NP <= 8 ? NP : 6;
+        f32x4_t ld[WIN][6];
+        auto issue = [&](int p, f32x4_t (&dst)[6]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int p = 0; p < NP; ++p) {
+            for (int i = 0; i < 6; ++i) dst[i] = *reinterpret_cast<const f32x4_t *>(rowp[i] + kw + 32 * NW * p);
+        };
 #pragma unroll
-            for (int i = 0; i < 6; ++i) ld[p][i] = *reinterpret_cast<const f32x4_t *>(rowp[i] + kw + 32 * NW * p);
-        }
+        for (int p = 0; p < WIN; ++p) issue(p, ld[p]);
         __builtin_amdgcn_sched_barrier(0);
         f32x4_t *t = tile[wave];
         const int sw = r & 7;  // the swizzle of operand row r (and of rows 16 + r, 32 + r)
@@ -159,7 +165,12 @@ __device__ __forceinline__ void kslice_body(const GemmOperands &op, const EpiPar
         for (int p = 0; p < NP; ++p) {
             // row 8 i + lr, piece lp -> slot lp ^ lr (8 i is a multiple of 8)
 #pragma unroll
-            for (int i = 0; i < 6; ++i) t[(8 * i + lr) * 8 + (lp ^ lr)] = ld[p][i];
+            for (int i = 0; i < 6; ++i) t[(8 * i + lr) * 8 + (lp ^ lr)] = ld[p % WIN][i];
+            if (p + WIN < NP) {
+                __builtin_amdgcn_sched_barrier(0);
+                issue(p + WIN, ld[p % WIN]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -341,8 +352,8 @@ int kudnn_launch_gemm_f32_kslice(const GemmOperands &op, const EpiParams &ep, in
     }
     const dim3 grid(static_cast<unsigned>(tilesM * tilesN), static_cast<unsigned>(batches));
     const int64_t chunks = op.K / kChunk;
-    // whole-line loads through LDS with 8 waves when K is a whole number of 16-chunk blocks, up to 8 of them
-    // (K <= 2048: at most 8 pairs of loads in flight per wave); otherwise 4 waves and the operand layout
+    // whole-line loads through LDS with 8 waves when K is 256 times 1, 2, 3, 4, 6, 8, 12 or 16 (K <= 4096; past
+    // 2048, 6 pairs of loads in flight per wave); otherwise 4 waves and the operand layout
     if (chunks % 16 == 0) {
         switch (chunks / 16) {
             case 1: return launch_kslice<8, 2>(op, ep, batches, tilesN, grid, stream);
@@ -351,6 +362,8 @@ int kudnn_launch_gemm_f32_kslice(const GemmOperands &op, const EpiParams &ep, in
             case 4: return launch_kslice<8, 8>(op, ep, batches, tilesN, grid, stream);
             case 6: return launch_kslice<8, 12>(op, ep, batches, tilesN, grid, stream);
             case 8: return launch_kslice<8, 16>(op, ep, batches, tilesN, grid, stream);
+            case 12: return launch_kslice<8, 24>(op, ep, batches, tilesN, grid, stream);
+            case 16: return launch_kslice<8, 32>(op, ep, batches, tilesN, grid, stream);
             default: break;
         }
     }

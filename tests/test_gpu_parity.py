@@ -187,11 +187,11 @@ def test_f32_kslice_shapes(dims, bias):
     compare(from_device(dc, O.F32), ref.buf, O.F32, plan.describe())
 
 
-@pytest.mark.parametrize("Kd", [512, 768, 1536, 3072])
+@pytest.mark.parametrize("Kd", [512, 768, 1536, 3072, 4096, 2560])
 def test_f32_kslice_whole_line_forms(Kd):
-    # K in whole 256-element blocks: 8 waves loading whole lines through LDS, 1, 3, 6 (= 16 chunks / 8 waves x 2 .. 12
-    # chunks per wave) pairs per wave; K = 3072 (12 blocks) takes the 4-wave form. Edge tiles in M and N; C1's M and N
-    # otherwise
+    # K in whole 256-element blocks: 8 waves loading whole lines through LDS, 2, 3, 6 pairs per wave with all loads in
+    # flight, 12 and 16 pairs with 6 in flight (K = 3072, 4096); K = 2560 (10 blocks) takes the 4-wave form. Edge tiles
+    # in M and N
     M, N = 120, 1000
     x = Case([M, Kd], O.F32, seed=66)
     w = Case([Kd, N], O.F32, "BA", seed=67)
