@@ -20,6 +20,7 @@
 
 #include "../../include/kudnn_hip.h"
 #include "kernels.h"
+#include "kslice.h"
 #include "layout_table.h"
 #include "plan_types.h"
 
@@ -631,10 +632,12 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
         core.B.staticPack = false;
     }
     // The same for an fp32 weight stored [K][N] (the reference's Matmul mode passes W in ABCDE,
-    // matmul_gtest.cpp:248-257), read in place by the 4-wave fp32 kernels (128 x 128 and 64 x 64): it needs K a
-    // multiple of the 32-deep k-tile, N a multiple of 4 (whole 16-byte column chunks), 16-byte aligned k-rows and
-    // batches. The k-slice kernel of the smallest grids still packs it.
-    if (core.engine == ENGINE_MFMA_F32 && (core.cfg == KUDNN_CFG_F32_128x128 || core.cfg == KUDNN_CFG_F32_64x64) &&
+    // matmul_gtest.cpp:248-257), read in place by the 4-wave fp32 kernels (128 x 128 and 64 x 64) and by the k-slice
+    // kernel's whole-line form (K = 256 c, kudnn_kslice_whole_line): it needs K a multiple of the 32-deep k-tile, N a
+    // multiple of 4 (whole 16-byte column chunks), 16-byte aligned k-rows and batches.
+    const bool f32InPlaceCfg = core.cfg == KUDNN_CFG_F32_128x128 || core.cfg == KUDNN_CFG_F32_64x64 ||
+                               (core.cfg == KUDNN_CFG_F32_KSLICE_16x32 && kudnn_kslice_whole_line(core.K));
+    if (core.engine == ENGINE_MFMA_F32 && f32InPlaceCfg &&
         core.B.dt == KUDNN_DT_F32 && core.B.s_r == 1 && core.B.s_k >= core.N && core.B.s_k % 4 == 0 &&
         core.B.bs[0] % 4 == 0 && core.B.bs[1] % 4 == 0 && core.B.bs[2] % 4 == 0 && core.K % 32 == 0 &&
         core.N % 4 == 0 && !std::getenv("KUDNN_HIP_PACK_KMAJOR")) {

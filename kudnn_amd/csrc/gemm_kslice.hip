@@ -17,8 +17,11 @@
 // 16 k once each (the same permutation on both operands).
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "device_common.h"
 #include "kernels.h"
+#include "kslice.h"
 
 namespace {
 
@@ -45,16 +48,25 @@ constexpr int kAhead = 2;          // chunks per batch of loads (two batches in 
 // to 6.0-6.1 us (4 waves with contiguous K ranges 6.8, a barrier between the waves' pairs of loads 6.4, 16 waves 6.3).
 // Past the first pair's arrival the MFMAs bound it: C1 is 4096 cycles of v_mfma_f32_16x16x4_f32 per SIMD.
 // CPW = 0: any K, two batches of kAhead interleaved chunks in flight per wave, loaded in the operand layout.
-template <int NW, int CPW, int ACT, int FORM>
+// BKM (whole-line form only): B is stored [K][N] (N contiguous, k-row pitch ldb) and read in place. A pair's B lines
+// are then its 32 k-rows x the tile's 32 columns (128 bytes each): instruction i = 2..5 reads k-rows 8 (i - 2) + lane / 8,
+// columns 4 (lane % 8) .. + 3 (past N: clamped to the last whole chunk, read but never stored). They go to a second
+// region of the LDS tile, 32 k-rows at a pitch of 36 floats, and a lane reads its column's 4 consecutive k as 4 floats:
+// the 36-float pitch puts the four k-rows 4 q + s (q = 0..3) of one read in four different 16-bank groups, so each
+// ds_read_b32 is conflict-free. The MFMAs get the same k values in the same order as from a packed [N][K] weight.
+template <int NW, int CPW, int ACT, int FORM, bool BKM = false>
 __device__ __forceinline__ void kslice_body(const GemmOperands &op, const EpiParams &ep, int tilesN)
 {
+    static_assert(!BKM || CPW > 0, "only the whole-line form reads a [K][N] weight in place");
     constexpr int kElems = kTM * kTN;
     // output elements per thread in the epilogue (with more threads than elements, the first kElems take one each)
     constexpr int kPer = kElems > NW * 64 ? kElems / (NW * 64) : 1;
     static_assert(kPer * NW * 64 == kElems || (kPer == 1 && NW * 64 > kElems), "the tile must divide over the threads");
     __shared__ f32x4_t part[NW][2][64];
     constexpr int kRows = kTM + 2 * 16;  // a wave's rows: A's 16, B's 32
-    __shared__ f32x4_t tile[CPW > 0 ? NW : 1][kRows * 8];
+    constexpr int kBkmPitch = 36;        // floats per k-row of a [K][N] weight's region
+    constexpr int kTileQuads = BKM ? kTM * 8 + 32 * kBkmPitch / 4 : kRows * 8;
+    __shared__ f32x4_t tile[CPW > 0 ? NW : 1][kTileQuads];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: the K loop's branches are scalar
@@ -135,26 +147,34 @@ __device__ __forceinline__ void kslice_body(const GemmOperands &op, const EpiPar
         static_assert(CPW % 2 == 0, "whole chunk pairs");
         constexpr int NP = CPW / 2;  // pairs of chunks: 32 k, one 128-byte line of each row
         const int lr = lane >> 3, lp = lane & 7;
-        // the rows of load instruction i: A rows 8 i + lr (i < 2), B rows 8 (i - 2) + lr; past M / N: the last row
+        // the rows of load instruction i: A rows 8 i + lr (i < 2), B rows 8 (i - 2) + lr; past M / N: the last row.
+        // Pair p of this wave covers k from 32 (wave + NW p): rowp[i] + pstep[i] p is its line's first byte
         const float *rowp[6];
+        int64_t pstep[6];
 #pragma unroll
         for (int i = 0; i < 6; ++i) {
             if (i < 2) {
                 const int64_t m = m0 + 8 * i + lr;
-                rowp[i] = static_cast<const float *>(op.a) + aoff + (m < op.M ? m : op.M - 1) * op.lda;
+                rowp[i] = static_cast<const float *>(op.a) + aoff + (m < op.M ? m : op.M - 1) * op.lda + 32 * wave + 4 * lp;
+                pstep[i] = 32 * NW;
+            } else if constexpr (BKM) {
+                int64_t n = n0 + 4 * lp;
+                n = n + 4 <= op.N ? n : op.N - 4;
+                rowp[i] = static_cast<const float *>(op.b) + boff + (32 * wave + 8 * (i - 2) + lr) * op.ldb + n;
+                pstep[i] = 32 * NW * op.ldb;
             } else {
                 const int64_t n = n0 + 8 * (i - 2) + lr;
-                rowp[i] = static_cast<const float *>(op.b) + boff + (n < op.N ? n : op.N - 1) * op.ldb;
+                rowp[i] = static_cast<const float *>(op.b) + boff + (n < op.N ? n : op.N - 1) * op.ldb + 32 * wave + 4 * lp;
+                pstep[i] = 32 * NW;
             }
         }
-        const int64_t kw = static_cast<int64_t>(wave) * 32 + 4 * lp;  // pair p of this wave: k from 32 (wave + NW p)
         // up to 8 pairs in flight per wave (192 VGPRs): all of them when NP <= 8; otherwise 6, pair p + 6 issued into
         // pair p's registers as soon as pair p is in the LDS tile
         constexpr int WIN = NP <= 8 ? NP : 6;
         f32x4_t ld[WIN][6];
         auto issue = [&](int p, f32x4_t (&dst)[6]) __attribute__((always_inline)) {
 #pragma unroll
-            for (int i = 0; i < 6; ++i) dst[i] = *reinterpret_cast<const f32x4_t *>(rowp[i] + kw + 32 * NW * p);
+            for (int i = 0; i < 6; ++i) dst[i] = *reinterpret_cast<const f32x4_t *>(rowp[i] + pstep[i] * p);
         };
 #pragma unroll
         for (int p = 0; p < WIN; ++p) issue(p, ld[p]);
@@ -163,9 +183,16 @@ __device__ __forceinline__ void kslice_body(const GemmOperands &op, const EpiPar
         const int sw = r & 7;  // the swizzle of operand row r (and of rows 16 + r, 32 + r)
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            // row 8 i + lr, piece lp -> slot lp ^ lr (8 i is a multiple of 8)
+            // row 8 i + lr, piece lp -> slot lp ^ lr (8 i is a multiple of 8); a [K][N] weight's k-row 8 (i - 2) + lr,
+            // columns 4 lp .. + 3 -> its region at pitch kBkmPitch
 #pragma unroll
-            for (int i = 0; i < 6; ++i) t[(8 * i + lr) * 8 + (lp ^ lr)] = ld[p % WIN][i];
+            for (int i = 0; i < 6; ++i) {
+                if (BKM && i >= 2) {
+                    t[kTM * 8 + ((8 * (i - 2) + lr) * kBkmPitch + 4 * lp) / 4] = ld[p % WIN][i];
+                } else {
+                    t[(8 * i + lr) * 8 + (lp ^ lr)] = ld[p % WIN][i];
+                }
+            }
             if (p + WIN < NP) {
                 __builtin_amdgcn_sched_barrier(0);
                 issue(p + WIN, ld[p % WIN]);
@@ -180,8 +207,15 @@ __device__ __forceinline__ void kslice_body(const GemmOperands &op, const EpiPar
             for (int h = 0; h < 2; ++h) {
                 const int slot = (4 * h + q) ^ sw;
                 fa[h] = t[r * 8 + slot];
-                fb0[h] = t[(16 + r) * 8 + slot];
-                fb1[h] = t[(32 + r) * 8 + slot];
+                if constexpr (BKM) {
+                    // column r (and 16 + r) at k = 16 h + 4 q + s, s = 0..3
+                    const float *kb = reinterpret_cast<const float *>(t + kTM * 8) + (16 * h + 4 * q) * kBkmPitch + r;
+                    fb0[h] = f32x4_t{kb[0], kb[kBkmPitch], kb[2 * kBkmPitch], kb[3 * kBkmPitch]};
+                    fb1[h] = f32x4_t{kb[16], kb[kBkmPitch + 16], kb[2 * kBkmPitch + 16], kb[3 * kBkmPitch + 16]};
+                } else {
+                    fb0[h] = t[(16 + r) * 8 + slot];
+                    fb1[h] = t[(32 + r) * 8 + slot];
+                }
             }
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
@@ -240,10 +274,10 @@ __device__ __forceinline__ void kslice_body(const GemmOperands &op, const EpiPar
 }
 
 // Any call: the whole GemmOperands and EpiParams as arguments.
-template <int NW, int CPW, int ACT, int FORM>
+template <int NW, int CPW, int ACT, int FORM, bool BKM>
 __global__ __launch_bounds__(NW * 64) void gemm_f32_kslice_kernel(GemmOperands op, EpiParams ep, int tilesN)
 {
-    kslice_body<NW, CPW, ACT, FORM>(op, ep, tilesN);
+    kslice_body<NW, CPW, ACT, FORM, BKM>(op, ep, tilesN);
 }
 
 // A single-batch call in the f32 form: the fields it uses (120 bytes instead of 380). A smaller argument block
@@ -257,7 +291,7 @@ struct KsArgs {
     int bin, tilesN;
 };
 
-template <int NW, int CPW, int ACT>
+template <int NW, int CPW, int ACT, bool BKM>
 __global__ __launch_bounds__(NW * 64) void gemm_f32_kslice_compact_kernel(KsArgs r)
 {
     GemmOperands op{};
@@ -286,7 +320,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_f32_kslice_compact_kernel(KsArgs
     ep.y_sm = r.y_sm;
     ep.y_sn = 1;
     ep.bdim[0] = ep.bdim[1] = ep.bdim[2] = 1;
-    kslice_body<NW, CPW, ACT, EPI_FORM_F32>(op, ep, r.tilesN);
+    kslice_body<NW, CPW, ACT, EPI_FORM_F32, BKM>(op, ep, r.tilesN);
 }
 
 }  // namespace
@@ -299,19 +333,19 @@ bool kudnn_kslice_eligible(const GemmOperands &op)
 
 namespace {
 
-template <int NW, int CPW>
+template <int NW, int CPW, bool BKM>
 int launch_kslice(const GemmOperands &op, const EpiParams &ep, int64_t batches, int64_t tilesN, dim3 grid,
                   hipStream_t stream)
 {
     const bool f32Form = epi_form(ep, false) == EPI_FORM_F32;
     if (f32Form && batches == 1 && (ep.bin == KUDNN_BINARY_NONE || ep.src_sn == 1) && ep.y_sn == 1) {
-        decltype(&gemm_f32_kslice_compact_kernel<NW, CPW, 0>) ck = nullptr;
+        decltype(&gemm_f32_kslice_compact_kernel<NW, CPW, 0, BKM>) ck = nullptr;
         switch (ep.act) {
-            case KUDNN_ACT_UNIMPLEMENTED: ck = gemm_f32_kslice_compact_kernel<NW, CPW, KUDNN_ACT_UNIMPLEMENTED>; break;
-            case KUDNN_ACT_RELU: ck = gemm_f32_kslice_compact_kernel<NW, CPW, KUDNN_ACT_RELU>; break;
-            case KUDNN_ACT_SWISH: ck = gemm_f32_kslice_compact_kernel<NW, CPW, KUDNN_ACT_SWISH>; break;
-            case KUDNN_ACT_GELU_TANH: ck = gemm_f32_kslice_compact_kernel<NW, CPW, KUDNN_ACT_GELU_TANH>; break;
-            case KUDNN_ACT_GELU_ERF: ck = gemm_f32_kslice_compact_kernel<NW, CPW, KUDNN_ACT_GELU_ERF>; break;
+            case KUDNN_ACT_UNIMPLEMENTED: ck = gemm_f32_kslice_compact_kernel<NW, CPW, KUDNN_ACT_UNIMPLEMENTED, BKM>; break;
+            case KUDNN_ACT_RELU: ck = gemm_f32_kslice_compact_kernel<NW, CPW, KUDNN_ACT_RELU, BKM>; break;
+            case KUDNN_ACT_SWISH: ck = gemm_f32_kslice_compact_kernel<NW, CPW, KUDNN_ACT_SWISH, BKM>; break;
+            case KUDNN_ACT_GELU_TANH: ck = gemm_f32_kslice_compact_kernel<NW, CPW, KUDNN_ACT_GELU_TANH, BKM>; break;
+            case KUDNN_ACT_GELU_ERF: ck = gemm_f32_kslice_compact_kernel<NW, CPW, KUDNN_ACT_GELU_ERF, BKM>; break;
             default: break;
         }
         if (ck != nullptr) {
@@ -322,16 +356,16 @@ int launch_kslice(const GemmOperands &op, const EpiParams &ep, int64_t batches, 
             return hipGetLastError() == hipSuccess ? 0 : -1;
         }
     }
-    decltype(&gemm_f32_kslice_kernel<NW, CPW, 0, EPI_FORM_GENERIC>) kernel = gemm_f32_kslice_kernel<NW, CPW, 0, EPI_FORM_GENERIC>;
+    decltype(&gemm_f32_kslice_kernel<NW, CPW, 0, EPI_FORM_GENERIC, BKM>) kernel = gemm_f32_kslice_kernel<NW, CPW, 0, EPI_FORM_GENERIC, BKM>;
     if (f32Form) {
         switch (ep.act) {
             case KUDNN_ACT_UNIMPLEMENTED:
-                kernel = gemm_f32_kslice_kernel<NW, CPW, KUDNN_ACT_UNIMPLEMENTED, EPI_FORM_F32>;
+                kernel = gemm_f32_kslice_kernel<NW, CPW, KUDNN_ACT_UNIMPLEMENTED, EPI_FORM_F32, BKM>;
                 break;
-            case KUDNN_ACT_RELU: kernel = gemm_f32_kslice_kernel<NW, CPW, KUDNN_ACT_RELU, EPI_FORM_F32>; break;
-            case KUDNN_ACT_SWISH: kernel = gemm_f32_kslice_kernel<NW, CPW, KUDNN_ACT_SWISH, EPI_FORM_F32>; break;
-            case KUDNN_ACT_GELU_TANH: kernel = gemm_f32_kslice_kernel<NW, CPW, KUDNN_ACT_GELU_TANH, EPI_FORM_F32>; break;
-            case KUDNN_ACT_GELU_ERF: kernel = gemm_f32_kslice_kernel<NW, CPW, KUDNN_ACT_GELU_ERF, EPI_FORM_F32>; break;
+            case KUDNN_ACT_RELU: kernel = gemm_f32_kslice_kernel<NW, CPW, KUDNN_ACT_RELU, EPI_FORM_F32, BKM>; break;
+            case KUDNN_ACT_SWISH: kernel = gemm_f32_kslice_kernel<NW, CPW, KUDNN_ACT_SWISH, EPI_FORM_F32, BKM>; break;
+            case KUDNN_ACT_GELU_TANH: kernel = gemm_f32_kslice_kernel<NW, CPW, KUDNN_ACT_GELU_TANH, EPI_FORM_F32, BKM>; break;
+            case KUDNN_ACT_GELU_ERF: kernel = gemm_f32_kslice_kernel<NW, CPW, KUDNN_ACT_GELU_ERF, EPI_FORM_F32, BKM>; break;
             default: break;
         }
     }
@@ -353,19 +387,27 @@ int kudnn_launch_gemm_f32_kslice(const GemmOperands &op, const EpiParams &ep, in
     const dim3 grid(static_cast<unsigned>(tilesM * tilesN), static_cast<unsigned>(batches));
     const int64_t chunks = op.K / kChunk;
     // whole-line loads through LDS with 8 waves when K is 256 times 1, 2, 3, 4, 6, 8, 12 or 16 (K <= 4096; past
-    // 2048, 6 pairs of loads in flight per wave); otherwise 4 waves and the operand layout
-    if (chunks % 16 == 0) {
+    // 2048, 6 pairs of loads in flight per wave); otherwise 4 waves and the operand layout. A [K][N] weight (the
+    // planner gives one only with such a K) is read in place by the whole-line form.
+    auto whole = [&](auto bkm) -> int {
+        constexpr bool B = decltype(bkm)::value;
         switch (chunks / 16) {
-            case 1: return launch_kslice<8, 2>(op, ep, batches, tilesN, grid, stream);
-            case 2: return launch_kslice<8, 4>(op, ep, batches, tilesN, grid, stream);
-            case 3: return launch_kslice<8, 6>(op, ep, batches, tilesN, grid, stream);
-            case 4: return launch_kslice<8, 8>(op, ep, batches, tilesN, grid, stream);
-            case 6: return launch_kslice<8, 12>(op, ep, batches, tilesN, grid, stream);
-            case 8: return launch_kslice<8, 16>(op, ep, batches, tilesN, grid, stream);
-            case 12: return launch_kslice<8, 24>(op, ep, batches, tilesN, grid, stream);
-            case 16: return launch_kslice<8, 32>(op, ep, batches, tilesN, grid, stream);
-            default: break;
+            case 1: return launch_kslice<8, 2, B>(op, ep, batches, tilesN, grid, stream);
+            case 2: return launch_kslice<8, 4, B>(op, ep, batches, tilesN, grid, stream);
+            case 3: return launch_kslice<8, 6, B>(op, ep, batches, tilesN, grid, stream);
+            case 4: return launch_kslice<8, 8, B>(op, ep, batches, tilesN, grid, stream);
+            case 6: return launch_kslice<8, 12, B>(op, ep, batches, tilesN, grid, stream);
+            case 8: return launch_kslice<8, 16, B>(op, ep, batches, tilesN, grid, stream);
+            case 12: return launch_kslice<8, 24, B>(op, ep, batches, tilesN, grid, stream);
+            case 16: return launch_kslice<8, 32, B>(op, ep, batches, tilesN, grid, stream);
+            default: return -1;
         }
+    };
+    if (kudnn_kslice_whole_line(op.K)) {
+        return op.b_kmajor ? whole(std::true_type{}) : whole(std::false_type{});
     }
-    return launch_kslice<4, 0>(op, ep, batches, tilesN, grid, stream);
+    if (op.b_kmajor) {
+        return -1;
+    }
+    return launch_kslice<4, 0, false>(op, ep, batches, tilesN, grid, stream);
 }

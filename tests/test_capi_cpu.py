@@ -183,7 +183,8 @@ def test_decode_kernel_rule(monkeypatch):
 
 def test_f32_kmajor_weight_rule(monkeypatch):
     # an fp32 [K][N] weight (layout AB) is read in place by the 128 x 128 and 64 x 64 kernels when N is a multiple of 4
-    # and K of 32; otherwise, under the k-slice kernel, or with KUDNN_HIP_PACK_KMAJOR set, it is packed to [N][K]
+    # and K of 32, and by the k-slice kernel for K = 256 c; otherwise, or with KUDNN_HIP_PACK_KMAJOR set, it is packed
+    # to [N][K]
     def f32_plan(M, Kd, N):
         return K.Gemm(K.desc([M, Kd], K.F32), K.desc([Kd, N], K.F32, "AB"), K.desc([M, N], K.F32)).describe()
     for M, Kd, N in ((4096, 4608, 1152), (512, 512, 1024), (1024, 640, 772), (8192, 64, 4)):
@@ -192,7 +193,11 @@ def test_f32_kmajor_weight_rule(monkeypatch):
     for M, Kd, N in ((1024, 640, 1158), (1024, 648, 1160), (4096, 3256, 1152)):
         d = f32_plan(M, Kd, N)
         assert "packB" in d and "kmajorB" not in d, d
-    d = f32_plan(128, 1024, 1024)  # C1's shape in Matmul mode: the k-slice kernel packs the weight
+    # the k-slice kernel of small grids: in place when K = 256 c, c in 1, 2, 3, 4, 6, 8, 12, 16 (C1's shape in Matmul
+    # mode), packed otherwise (K = 1280)
+    d = f32_plan(128, 1024, 1024)
+    assert d.startswith("mfma_f32_kslice") and "kmajorB" in d and "packB" not in d, d
+    d = f32_plan(128, 1280, 1024)
     assert d.startswith("mfma_f32_kslice") and "packB" in d, d
     monkeypatch.setenv("KUDNN_HIP_PACK_KMAJOR", "1")
     assert "packB" in f32_plan(512, 512, 1024)

@@ -2,9 +2,11 @@
 passes the weight as [K][N] (Layout ABCDE, test/dnn/llt/gtest/src/matmul_gtest.cpp:248-257) and KML consumes it through
 the layout -> transpose mapping (src/dnn/src/kudnn_gemm.cpp:478-549). The 4-wave fp32 kernels (128 x 128 and 64 x 64,
 split along K on small grids) copy each k-tile of such a weight into LDS as 32 k-rows of the tile's columns and read one
-float per k. The cases cover full and edge tiles (N a multiple of 4 but not of the tile, so the last chunks of a k-row
-are clamped), batched and broadcast weights, every fixed epilogue form and the generic one (alpha, beta C, bias), the
-split-K instance, and the planner's own choice. Each runs against the oracle and, bit for bit, against the same plan
+float per k. The k-slice kernel of the smallest grids reads it in place too when K = 256 c (its whole-line form: 32
+k-rows of the tile's 32 columns per pair of chunks, through LDS). The cases cover full and edge tiles (N a multiple of
+4 but not of the tile, so the last chunks of a k-row are clamped), batched and broadcast weights, every fixed epilogue
+form and the generic one (alpha, beta C, bias), the split-K instance, the k-slice kernel, and the planner's own
+choice. Each runs against the oracle and, bit for bit, against the same plan
 with the weight packed to [N][K] (KUDNN_HIP_PACK_KMAJOR=1): both feed the MFMAs the same k values in the same order.
 Weights the kernels cannot read in place (N not a multiple of 4, K not a multiple of 32) are packed.
 """
@@ -71,6 +73,25 @@ def test_f32_kmajor_weight_in_place(monkeypatch, cfg, shape, act):
     ref = y.clone_empty()
     O.linear_postops(x.t, w.t, ref, b.t if b else None, act, 1.0, O.BIN_NONE, None)
     compare(got, ref.buf, O.F32, "f32 kmajor " + plan.describe())
+
+
+@pytest.mark.parametrize("shape", [([], 128, 1024, 1024, []), ([], 100, 512, 1000, []), ([], 64, 3072, 1024, []),
+                                   ([], 16, 4096, 4100, []), ([2], 40, 256, 700, [2]), ([3], 48, 768, 1000, [1])])
+@pytest.mark.parametrize("act", [K.ACT_UNIMPLEMENTED, K.ACT_RELU])
+def test_f32_kmajor_kslice_in_place(monkeypatch, shape, act):
+    # the k-slice kernel's whole-line form (grids too small for 64 x 64 tiles): C1's shape in Matmul mode; K = 512,
+    # 3072 and 4096 (2, 12 and 16 pairs of 32 k per wave); edge tiles (N a multiple of 4, not of 32); M = 16; batched and
+    # broadcast weights
+    lead, M, Kd, N, wlead = shape
+    x, w, b, y = _case(lead, M, Kd, N, wlead, act != K.ACT_UNIMPLEMENTED, 860)
+    dx, dw, db = x.device(), w.device(), b.device() if b else None
+    got, plan = _both(monkeypatch,
+                      lambda: K.LinearPostOps(x.desc, w.desc, y.desc, b.desc if b else None, act=act, act_alpha=0.0),
+                      lambda p, dy: p.run(dx, dw, dy, db), lambda: zeros_device(y))
+    assert plan.describe().startswith("mfma_f32_kslice"), plan.describe()
+    ref = y.clone_empty()
+    O.linear_postops(x.t, w.t, ref, b.t if b else None, act, 0.0, O.BIN_NONE, None)
+    compare(got, ref.buf, O.F32, "f32 kmajor kslice " + plan.describe())
 
 
 def test_f32_kmajor_gemm_generic_form(monkeypatch):
