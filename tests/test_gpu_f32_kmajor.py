@@ -154,3 +154,40 @@ def test_f32_kmajor_unaligned_is_packed(monkeypatch, M, Kd, N):
     ref = y.clone_empty()
     O.linear_postops(x.t, w.t, ref, b.t, K.ACT_GELU_TANH, 1.0, O.BIN_NONE, None)
     compare(from_device(dy, O.F32), ref.buf, O.F32, plan.describe())
+
+
+def _random_f32_kmajor_shapes(count=24, seed=2026):
+    # seeded (M, N, K) draws for an fp32 [K][N] weight: M in [1, 400] or [1, 4096] (the k-slice kernel's small grids,
+    # 64 x 64 and 128 x 128 grids of several rounds), N a multiple of 4 in [4, 4096] (edge tiles of every width), K a multiple of
+    # 32 in [32, 4096] (the k-slice kernel's whole-line K values and others, which pack), plus a few draws with N or K
+    # off those multiples (packed)
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        M = int(rng.integers(1, 401 if i % 2 else 4097))
+        N = 4 * int(rng.integers(1, 1025))
+        Kd = 32 * int(rng.integers(1, 129)) if i % 3 else 256 * int(rng.choice([1, 2, 3, 4, 6, 8, 12, 16]))
+        if i % 8 == 7:
+            N += 2 if i % 16 == 7 else 0
+            Kd += 8 if i % 16 == 15 else 0
+        out.append((M, N, Kd))
+    return out
+
+
+@pytest.mark.parametrize("M,N,Kd", _random_f32_kmajor_shapes())
+def test_f32_kmajor_random_shapes(M, N, Kd):
+    # the planner's own choice on each draw (k-slice, 64 x 64 or 128 x 128 kernel; in place or packed) against the
+    # oracle on sampled rows
+    x, w, b, y = _case([], M, Kd, N, [], True, 870)
+    plan = K.LinearPostOps(x.desc, w.desc, y.desc, b.desc, act=K.ACT_RELU)
+    inplace = N % 4 == 0 and Kd % 32 == 0 and ("kslice" not in plan.describe() or Kd in
+                                                  [256 * c for c in (1, 2, 3, 4, 6, 8, 12, 16)])
+    assert ("kmajorB" in plan.describe()) == inplace, plan.describe()
+    dy = zeros_device(y)
+    plan.run(x.device(), w.device(), dy, b.device())
+    torch.cuda.synchronize()
+    got = from_device(dy, O.F32).reshape(M, N)
+    rows = sample_rows(M, 24)
+    ref = O.empty((len(rows), N), (N, 1), O.F32)
+    O.linear_postops(dense_rows(x.t, rows), w.t, ref, b.t, K.ACT_RELU, 0.0, O.BIN_NONE, None)
+    compare(got[rows].reshape(-1), ref.buf, O.F32, f"f32 kmajor M={M} N={N} K={Kd} {plan.describe()}")
