@@ -72,6 +72,8 @@ def parse():
     p.add_argument("--summarize-counters", metavar="CSV", default=None,
                    help="print per-dispatch means of every counter of the C3 kernel in a rocprofv3 "
                         "run_counter_collection.csv, with its duration, clock and MFMA busy fraction (no GPU needed)")
+    p.add_argument("--counter-kernel", metavar="NAME", default=None,
+                   help="with --summarize-counters: summarise the kernel whose name contains NAME instead of C3's")
     return p.parse_args()
 
 
@@ -356,12 +358,13 @@ def _mean(xs):
     return sum(xs) / len(xs) if xs else float("nan")
 
 
-def summarize_counters(path):
-    """Per-dispatch means of the C3 kernel's counters in one capture, with the clock that GRBM_GUI_ACTIVE gives over
-    the dispatch time (the counter is summed over the 8 XCCs) and the MFMA busy fraction of the 1024 SIMDs."""
-    ds = counter_dispatches(path, C3_KERNEL)
+def summarize_counters(path, kernel=C3_KERNEL):
+    """Per-dispatch means of one kernel's counters in one capture (the C3 kernel unless another kernel-name substring
+    is given), with the clock that GRBM_GUI_ACTIVE gives over the dispatch time (the counter is summed over the 8 XCCs)
+    and the MFMA busy fraction of the 1024 SIMDs."""
+    ds = counter_dispatches(path, kernel)
     names = sorted({n for d in ds.values() for n in d["counters"]})
-    res = {"kernel": C3_KERNEL, "dispatches": len(ds), "mean_us": _mean(d["ns"] / 1e3 for d in ds.values())}
+    res = {"kernel": kernel, "dispatches": len(ds), "mean_us": _mean(d["ns"] / 1e3 for d in ds.values())}
     for n in names:
         res[n] = _mean(d["counters"][n] for d in ds.values() if n in d["counters"])
     if "GRBM_GUI_ACTIVE" in res:
@@ -648,7 +651,7 @@ def main():
         summarize_traffic(args.summarize_traffic)
         return
     if args.summarize_counters:
-        summarize_counters(args.summarize_counters)
+        summarize_counters(args.summarize_counters, args.counter_kernel or C3_KERNEL)
         return
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
