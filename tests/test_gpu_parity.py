@@ -1,8 +1,8 @@
 """GPU parity: the HIP path (through the C ABI) against the CPU oracle on identical seeded inputs.
 
-Small problems are checked in full; the BASELINE configs C1..C5 run at full size on the GPU and are
-checked on a sample of output rows (rows of a GEMM are independent, so the oracle computes exactly those
-rows from the matching rows of X).
+Small problems are checked in full. The configurations C1..C5 run at full size on the GPU. C1, C2, C3 and the C4 shapes
+are checked in every output element. C5 (2.3e12 flops) is checked on a sample of output rows: rows of a GEMM are
+independent, so the oracle computes exactly those rows from the matching rows of X.
 """
 import numpy as np
 import pytest
@@ -226,7 +226,8 @@ def test_f32_kslice_batched_and_repeatable():
     compare(outs[0], ref.buf, O.F32, plan.describe())
 
 
-def test_c2_fp32_silu_rows():
+def test_c2_fp32_silu_full():
+    # C2 at its full size, every output element against the oracle (about 1.4e11 flops of oracle time)
     M, Kd, N = 2048, 4096, 4096
     x = Case([M, Kd], O.F32, seed=0, dist="normal", lo=0.0, hi=1.0)
     w = Case([Kd, N], O.F32, "BA", seed=1, dist="normal", lo=0.0, hi=1.0 / 64)
@@ -236,14 +237,15 @@ def test_c2_fp32_silu_rows():
     dc = zeros_device(c)
     plan.run(x.device(), w.device(), dc, b.device())
     torch.cuda.synchronize()
-    got = from_device(dc, O.F32).reshape(M, N)
-    rows = sample_rows(M, 24)  # every 256-row tile row, the edges, and random rows
-    ref = O.empty((len(rows), N), (N, 1), O.F32)
-    O.linear_act(dense_rows(x.t, rows), w.t, ref, b.t, O.ACT_SWISH, 1.0)
-    compare(got[rows].reshape(-1), ref.buf, O.F32, "C2 " + plan.describe())
+    ref = c.clone_empty()
+    O.linear_act(x.t, w.t, ref, b.t, O.ACT_SWISH, 1.0)
+    maxnorm, _ = compare(from_device(dc, O.F32), ref.buf, O.F32, "C2 " + plan.describe())
+    print(f"C2 all {M} x {N}: max-normalised error {maxnorm:.3e}")
 
 
-def test_c3_bf16_gelu_residual_rows():
+def test_c3_bf16_gelu_residual_full():
+    # C3 at its full size (the bench workload's shape and inputs), every output element against the oracle (about
+    # 3.7e11 flops of oracle time)
     M, Kd, N = 4096, 4096, 11008
     x = Case([M, Kd], O.BF16, seed=0, dist="normal", lo=0.0, hi=1.0)
     w = Case([Kd, N], O.BF16, "BA", seed=1, dist="normal", lo=0.0, hi=0.02)
@@ -251,17 +253,15 @@ def test_c3_bf16_gelu_residual_rows():
     r = Case([M, N], O.BF16, seed=3, dist="normal", lo=0.0, hi=1.0)
     y = Case([M, N], O.BF16, zero=True)
     plan = K.LinearPostOps(x.desc, w.desc, y.desc, b.desc, act=K.ACT_GELU_TANH, binary=K.BIN_ADD, src=r.desc)
+    assert plan.describe().startswith("mfma_bf16_pingpong_256x256"), plan.describe()
     dy = zeros_device(y)
     plan.run(x.device(), w.device(), dy, b.device(), r.device())
     torch.cuda.synchronize()
-    got = from_device(dy, O.BF16).reshape(M, N)
-    rows = sample_rows(M, 32)  # every 256-row tile row, the edges, and random rows
-    xr, rr = dense_rows(x.t, rows), dense_rows(r.t, rows)
-    ref = O.empty((len(rows), N), (N, 1), O.BF16)
-    O.linear_postops(xr, w.t, ref, b.t, O.ACT_GELU_TANH, 0.0, O.BIN_ADD, rr)
-    why = PostOpsExplainer(xr, w.t, b.t, (len(rows), N), act=O.ACT_GELU_TANH, binary=O.BIN_ADD, src=rr)
-    maxnorm, exact = compare(got[rows].reshape(-1), ref.buf, O.BF16, "C3 " + plan.describe(), explain=why)
-    print(f"C3 rows {len(rows)}: max-normalised error {maxnorm:.3e}, bit-exact fraction {exact:.5f}, "
+    ref = y.clone_empty()
+    O.linear_postops(x.t, w.t, ref, b.t, O.ACT_GELU_TANH, 0.0, O.BIN_ADD, r.t)
+    why = PostOpsExplainer(x.t, w.t, b.t, (M, N), act=O.ACT_GELU_TANH, binary=O.BIN_ADD, src=r.t)
+    maxnorm, exact = compare(from_device(dy, O.BF16), ref.buf, O.BF16, "C3 " + plan.describe(), explain=why)
+    print(f"C3 all {M} x {N}: max-normalised error {maxnorm:.3e}, bit-exact fraction {exact:.5f}, "
           f"one-ulp exceptions {why.counts}")
 
 
