@@ -1,7 +1,8 @@
 """GPU test of kudnn_linear_postops_run_noalloc, the entry point that allocates nothing: through the C ABI its
 results equal kudnn_linear_postops_run's bit for bit (same kernels) on calls in a row, each smaller than the one
 before, with plans that use the workspace (the ping-pong kernel's K-slice sums, whole-grid or of the last partial
-round only, operand packs and the 4-wave kernel's split-K partials, which it takes from its static device scratch)."""
+round only, operand packs and the 4-wave kernels' split-K partials, bf16 and f32, which it takes from its static device
+scratch)."""
 import ctypes
 
 import numpy as np
@@ -23,14 +24,15 @@ def _gpu():
     K.lib()
 
 
-def _run_both(M, N, Kd, seed):
-    # weight in layout AB (K-major [K][N]): the ping-pong kernel reads it in place when N is a multiple of 8 and K of
-    # 64 (the plan says kmajorB); the 4-wave kernel, and K tails, pack it into the workspace (packB)
-    x = Case([M, Kd], O.BF16, seed=seed, dist="normal", lo=0.0, hi=1.0)
-    w = Case([Kd, N], O.BF16, "AB", seed=seed + 1, dist="normal", lo=0.0, hi=0.03)
-    b = Case([1, N], O.BF16, seed=seed + 2, lo=-0.1, hi=0.1)
-    s = Case([M, N], O.BF16, seed=seed + 3, lo=-1.0, hi=1.0)
-    y = Case([M, N], O.BF16, zero=True)
+def _run_both(M, N, Kd, seed, dt=O.BF16):
+    # weight in layout AB (K-major [K][N]). bf16: the ping-pong kernel reads it in place when N is a multiple of 8 and
+    # K of 64 (the plan says kmajorB); the 4-wave kernel, and K tails, pack it into the workspace (packB). f32: the
+    # 4-wave kernels read it in place when N is a multiple of 4 and K of 32, the k-slice kernel for whole-line K
+    x = Case([M, Kd], dt, seed=seed, dist="normal", lo=0.0, hi=1.0)
+    w = Case([Kd, N], dt, "AB", seed=seed + 1, dist="normal", lo=0.0, hi=0.03)
+    b = Case([1, N], dt, seed=seed + 2, lo=-0.1, hi=0.1)
+    s = Case([M, N], dt, seed=seed + 3, lo=-1.0, hi=1.0)
+    y = Case([M, N], dt, zero=True)
     plan = K.LinearPostOps(x.desc, w.desc, y.desc, b.desc, act=K.ACT_GELU_TANH, binary=K.BIN_ADD, src=s.desc)
     dx, dw, db, ds = x.device(), w.device(), b.device(), s.device()
     want, got = zeros_device(y), zeros_device(y)
@@ -40,7 +42,7 @@ def _run_both(M, N, Kd, seed):
                                                   db.data_ptr(), ds.data_ptr(), ctypes.c_float(1.0), stream)
     assert st == K.SUCCESS, K.last_error()
     torch.cuda.synchronize()
-    a, r = from_device(got, O.BF16), from_device(want, O.BF16)
+    a, r = from_device(got, dt), from_device(want, dt)
     assert np.array_equal(a, r), f"{plan.describe()}: {np.count_nonzero(a != r)} outputs differ"
     assert np.count_nonzero(a) > a.size // 2
     return plan
@@ -65,6 +67,17 @@ def test_noalloc_tail_slices_then_smaller():
     assert "kslices=4 tail=16" in p1.describe(), p1.describe()
     p2 = _run_both(512, 1024, 2048, seed=525)
     assert "kslices=" in p2.describe() and "tail=" not in p2.describe(), p2.describe()
+
+
+def test_noalloc_f32_kmajor_in_place(monkeypatch):
+    # f32 with the [K][N] weight read in place: 128 x 256 x 2048 on the 64 x 64 kernel split along K (its partial tiles
+    # and arrival counters in the scratch), then a smaller 64 x 1024 x 1024 on the k-slice kernel, which needs none
+    monkeypatch.setenv("KUDNN_HIP_FORCE_CFG", "11")
+    p1 = _run_both(128, 256, 2048, seed=530, dt=O.F32)
+    assert p1.describe().startswith("mfma_f32_64x64") and "kmajorB" in p1.describe(), p1.describe()
+    monkeypatch.delenv("KUDNN_HIP_FORCE_CFG")
+    p2 = _run_both(64, 1024, 1024, seed=535, dt=O.F32)
+    assert p2.describe().startswith("mfma_f32_kslice") and "kmajorB" in p2.describe(), p2.describe()
 
 
 def test_noalloc_refuses_what_it_cannot_do():
