@@ -15,8 +15,8 @@ the GPU raises its clocks over the first ~100 ms of sustained load, and a timed 
 reports the ramp rather than the kernel (10-15 % slower per step over the first tens of milliseconds).
 
 For profiling, --only c3 runs just the C3 step (JSON line without decode or CPU baseline), --only decode just the
-decode lines (--only decode-sweep: the decode step over M in 1..16 and N in 4096..28672, one JSON line each, the
-measurements behind the skinny dispatch rule), and --only copy runs an
+decode lines (--only decode-sweep: the decode step over M in 1..16 and N in 4096..28672, or the lists --sweep-m and
+--sweep-n give, one JSON line each, the measurements behind the skinny dispatch rule), and --only copy runs an
 elementwise copy-like kernel (y = -x, 512 MiB bf16 in, 512 MiB out) whose known traffic calibrates the
 FETCH_SIZE / WRITE_SIZE counters against which the C3 kernel's HBM traffic is read. --only dispatch times a bf16
 Linear + GELU(tanh) over prefill-like shapes under every kernel configuration (forced through KUDNN_HIP_FORCE_CFG and
@@ -74,6 +74,8 @@ def parse():
                         "run_counter_collection.csv, with its duration, clock and MFMA busy fraction (no GPU needed)")
     p.add_argument("--counter-kernel", metavar="NAME", default=None,
                    help="with --summarize-counters: summarise the kernel whose name contains NAME instead of C3's")
+    p.add_argument("--sweep-m", default="1,2,3,4,5,6,8,10,12,16", help="with --only decode-sweep: the values of M")
+    p.add_argument("--sweep-n", default="4096,8192,14336,28672", help="with --only decode-sweep: the values of N")
     return p.parse_args()
 
 
@@ -688,8 +690,8 @@ def main():
     if args.only == "decode-sweep":
         # the decode step (Linear then element-wise multiply, K = 4096) over M and N, under the planner's choice or
         # the configuration KUDNN_HIP_FORCE_CFG names: the measurements the skinny dispatch rule is drawn from
-        for m in (1, 2, 3, 4, 5, 6, 8, 10, 12, 16):
-            for n in (4096, 8192, 14336, 28672):
+        for m in (int(v) for v in args.sweep_m.split(",")):
+            for n in (int(v) for v in args.sweep_n.split(",")):
                 d = bench_decode(args, torch, K, n, m)
                 print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}), flush=True)
         return
