@@ -17,7 +17,9 @@
 //   memory phase M(t): read this wave's A fragments of k-tile t from LDS, issue its share of the next copies
 //                      (group 0: A(t+1), group 1: B(t+2)), read the B fragments of the first k16 step;
 //   compute phase C(t): 32 v_mfma_f32_32x32x16_bf16, B fragments of step s+1 read while step s issues.
-// While one wave of a SIMD is in its memory phase the other issues MFMAs.
+// While one wave of a SIMD is in its memory phase the other issues MFMAs. A wave raises its priority (s_setprio 1) for
+// its compute phase, so when both waves of a SIMD have an instruction ready the arbiter issues the MFMA wave's first
+// instead of the older wave's (measured on C3, alternating runs on one box: 1203-1209 TFLOP/s without, 1222-1225 with).
 //
 // LDS (160 KB): A tiles double-buffered, B tiles triple-buffered (5 x 32 KB). A(t) is read in phases 2t, 2t+1 and
 // rewritten by A(t+2) from phase 2t+2; B(t) is read in phases 2t .. 2t+2 and rewritten by B(t+3) at phase 2t+3.
@@ -678,7 +680,8 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        // ---- compute phase
+        // ---- compute phase, at raised wave priority
+        __builtin_amdgcn_s_setprio(1);
         sfor<4>([&](auto sc) __attribute__((always_inline)) {
             constexpr int s = decltype(sc)::value;
             if constexpr (s + 1 < 4) {
@@ -705,6 +708,7 @@ __global__ __launch_bounds__(512, 1) void gemm_pingpong_kernel(GemmOperands op, 
             }
             __builtin_amdgcn_sched_barrier(0);
         });
+        __builtin_amdgcn_s_setprio(0);
         // group 0's A(t+1) (its only copies in flight), which it reads in the next phase; (SK) group 1's B(t+1)
         if (g == 0) {
             wait_vmcnt<0>();
