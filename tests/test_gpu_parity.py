@@ -502,6 +502,33 @@ def test_c5_bf16_3d_silu_kmajor_rows():
     assert "kmajorB" in plan.describe() and "packB" not in plan.describe(), plan.describe()
 
 
+@pytest.fixture(scope="module")
+def c5_full():
+    # C5 at its full size with the bench's seeds, run once; the tests below check its output batch by batch
+    B, S, Kd, N = 8, 2048, 5120, 13824
+    x = Case([B, S, Kd], O.BF16, "ABC", seed=0, dist="normal", lo=0.0, hi=1.0)
+    w = Case([1, Kd, N], O.BF16, "ABC", seed=1, dist="normal", lo=0.0, hi=0.014)
+    b = Case([1, 1, N], O.BF16, "ABC", seed=2, dist="normal", lo=0.0, hi=0.02)
+    y = Case([B, S, N], O.BF16, "ABC", zero=True)
+    plan = K.LinearActivation(x.desc, w.desc, y.desc, b.desc, 1.0, 0.0, K.ACT_SWISH)
+    dy = zeros_device(y)
+    plan.run(x.device(), w.device(), dy, b.device())
+    torch.cuda.synchronize()
+    got = from_device(dy, O.BF16).reshape(B * S, N)
+    return x, w, b, got, plan.describe(), (B, S, Kd, N)
+
+
+@pytest.mark.parametrize("batch", range(8))
+def test_c5_bf16_3d_silu_kmajor_full(c5_full, batch):
+    # every output element of C5 (about 2.9e11 oracle flops per batch of 2048 rows)
+    x, w, b, got, desc, (B, S, Kd, N) = c5_full
+    rows = np.arange(batch * S, (batch + 1) * S)
+    ref = O.empty((S, N), (N, 1), O.BF16)
+    O.linear_act(dense_rows(x.t, rows), as2d(w.t), ref, as2d(b.t), O.ACT_SWISH, 1.0)
+    maxnorm, exact = compare(got[rows].reshape(-1), ref.buf, O.BF16, f"C5 batch {batch} {desc}")
+    print(f"C5 batch {batch}: max-normalised error {maxnorm:.3e}, bit-exact fraction {exact:.5f}")
+
+
 def _kmajor_case(dt, lead, M, Kd, N, wlead, act, bias, seed):
     x = Case(lead + [M, Kd], dt, seed=seed, dist="normal", lo=0.0, hi=1.0)
     w = Case(wlead + [Kd, N], dt, seed=seed + 1, dist="normal", lo=0.0, hi=0.05)  # standard layout: [K][N]
