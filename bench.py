@@ -25,8 +25,8 @@ planner's own choice, one JSON line per shape, then an f32 Gemm over grids of
 256-640 tiles of 128 x 128 under the 128 x 128 and 64 x 64 configurations: the measurements the dispatcher's rules are
 drawn from. --only refperf times KuDNN::Gemm on the reference's own perf shape sets (the matmul gtest's freParas and
 freParasMulti) in f32 and bf16, under the planner and under every forced configuration, one JSON line per shape and
-type. --only torch times C3's shape through PyTorch's own ops (the bf16 GEMM alone, then GEMM + GELU + add unfused)
-for comparison. --only c1 prints the C1 line alone.
+type. --only torch times C3's shape through PyTorch's own ops (the bf16 GEMM alone, then GEMM + GELU + add unfused),
+then C1, C2, C5 and the decode shapes the same way, for comparison. --only c1 prints the C1 line alone.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--prewarm-ms 300]
                        [--only c3|c1|copy|decode|decode-sweep|dispatch|refperf|torch]
@@ -224,6 +224,65 @@ def bench_torch_c3(args, torch):
         ms, _ = time_launches(fn, args.steps, args.warmup, torch, stream, args.prewarm_ms)
         print(json.dumps({"op": name, "M": M, "K": Kd, "N": N, "ms": round(ms, 4),
                           "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1)}), flush=True)
+
+
+def bench_torch_others(args, torch):
+    """C1, C2, C5 and the decode shapes through PyTorch's own ops, for comparison only (not this library): the GEMM
+    alone and the unfused Linear + post-op (hipBLASLt / rocBLAS on ROCm's PyTorch), with the inputs, the rotation over
+    input copies and the timing of this library's lines for the same configurations."""
+    F = torch.nn.functional
+    torch.backends.cuda.matmul.allow_tf32 = False
+    stream = torch.cuda.current_stream()
+
+    def emit(op, cfg, M, Kd, N, ms, flops, alg_bytes=None):
+        rec = {"op": op, "config": cfg, "M": M, "K": Kd, "N": N, "us": round(ms * 1e3, 2),
+               "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2)}
+        if alg_bytes is not None:
+            rec["GB/s"] = round(alg_bytes / (ms * 1e-3) / 1e9, 1)
+            rec["frac_hbm"] = round(alg_bytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
+        print(json.dumps(rec), flush=True)
+
+    for name in ("C1", "C2", "C5"):
+        if name == "C1":
+            M, Kd, N, dt, act, copies = 128, 1024, 1024, torch.float32, F.relu, 1
+            xd, wd, bd = ("uniform", -1.0, 1.0), ("uniform", -1.0, 1.0), ("uniform", -0.1, 0.1)
+        elif name == "C2":
+            M, Kd, N, dt, act, copies = 2048, 4096, 4096, torch.float32, F.silu, 4
+            xd, wd, bd = ("normal", 0.0, 1.0), ("normal", 0.0, 1.0 / 64), ("normal", 0.0, 0.02)
+        else:
+            M, Kd, N, dt, act, copies = 16384, 5120, 13824, torch.bfloat16, F.silu, 1
+            xd, wd, bd = ("normal", 0.0, 1.0), ("normal", 0.0, 0.014), ("normal", 0.0, 0.02)
+        xs = [synth(torch, (M, Kd), 0 + 16 * c, *xd, dt) for c in range(copies)]
+        bias = synth(torch, (1, N), 2, *bd, dt).reshape(N)
+        y = torch.empty(M, N, device="cuda", dtype=dt)
+        if name == "C5":  # the weight stored [K][N], as in the C5 line
+            w = synth(torch, (Kd, N), 1, *wd, dt)
+            xb = xs[0].reshape(8, 2048, Kd)
+            yb = y.reshape(8, 2048, N)
+            fns = (("GEMM only", lambda i=0: torch.matmul(xb, w, out=yb)),
+                   ("GEMM + bias + silu (unfused)", lambda i=0: act(torch.matmul(xb, w) + bias)))
+        else:  # nn.Linear weight [N][K]
+            ws = [synth(torch, (N, Kd), 1 + 16 * c, *wd, dt) for c in range(copies)]
+            fns = (("GEMM only", lambda i=0: torch.matmul(xs[i % copies], ws[i % copies].t(), out=y)),
+                   ("linear + bias + act (unfused)", lambda i=0: act(F.linear(xs[i % copies], ws[i % copies], bias))))
+        for op, fn in fns:
+            ms, _ = time_launches(fn, args.steps, max(args.warmup, copies), torch, stream, args.prewarm_ms)
+            emit(f"torch {op}", name, M, Kd, N, ms, 2.0 * M * N * Kd)
+
+    Kd = 4096
+    for N in (4096, 14336):
+        copies = max(2, -(-512 * 2**20 // (N * Kd * 2)))  # >= 512 MB of distinct weights, as in the decode lines
+        ws = [synth(torch, (N, Kd), 1 + 16 * c, "normal", 0.0, 0.02, torch.bfloat16) for c in range(copies)]
+        for M in (1, 4, 16):
+            x = synth(torch, (M, Kd), 0, "normal", 0.0, 1.0, torch.bfloat16)
+            m2 = synth(torch, (M, N), 3, "uniform", 0.5, 1.5, torch.bfloat16)
+            y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+            alg = 2 * (N * Kd + M * Kd + 2 * M * N)
+            for op, fn in (("linear only", lambda i=0: torch.matmul(x, ws[i % copies].t(), out=y)),
+                           ("linear * M2 (unfused)", lambda i=0: torch.mul(F.linear(x, ws[i % copies]), m2, out=y))):
+                steps = max(args.steps, 4 * copies)
+                ms, _ = time_launches(fn, steps, max(args.warmup, copies), torch, stream, args.prewarm_ms)
+                emit(f"torch {op}", "C4", M, Kd, N, ms, 2.0 * M * N * Kd, alg)
 
 
 def bench_decode(args, torch, K, N, M=1):
@@ -680,6 +739,7 @@ def main():
 
     if args.only == "torch":
         bench_torch_c3(args, torch)
+        bench_torch_others(args, torch)
         return
 
     if args.only == "c1":
