@@ -15,9 +15,8 @@
 //    32 consecutive rows at one logical k-chunk hits every bank once.
 //  - MFMA fragments of k16-substep s+1 are read from LDS while substep s's MFMAs issue.
 //  - bf16: v_mfma_f32_32x32x16_bf16; f16: v_mfma_f32_32x32x16_f16; s8: v_mfma_i32_32x32x32_i8 (int32 accumulators,
-//    kept in the same registers as bit patterns); fp32: v_mfma_f32_16x16x4f32 (v_mfma_f32_32x32x2f32 in the K-split
-//    instances) fed from one 16-byte LDS read per lane (four k values; MFMA q consumes element q of every lane group,
-//    which covers every k exactly once). The 16- and
+//    kept in the same registers as bit patterns); fp32: v_mfma_f32_32x32x2f32 fed from one 16-byte LDS read per lane
+//    (four k values; MFMA q consumes element q of both lane halves, which covers every k exactly once). The 16- and
 //    8-bit instructions all take 16 bytes of one row per lane, lane half h holding bytes 16h .. 16h+15 of each
 //    32-byte k step for both operands, so one data path serves all three: the sum over k does not depend on how the
 //    hardware orders the k values inside a lane, as long as both operands use the same order.
@@ -116,12 +115,10 @@ constexpr bool kSplittable = (CT == KUDNN_DT_F32 && BM == 64 && BN == 64) ||
 
 // CT: compute (operand) type, KUDNN_DT_F32 / BF16 / F16 / S8. SPLIT: grid.z splits K (see SplitArgs).
 // BKM (fp32 only): B is stored [K][N] (N contiguous, k-row pitch ldb) and read in place. A k-tile of B is then 32
-// k-rows of the tile's BN columns; the LDS DMA copies them as they lie, with each k-row's column groups permuted, and
-// a lane reads its column's 4 consecutive k as 4 single floats (gfx950 has no 32-bit transposing LDS read). The
-// permutation puts the lane groups' reads (different k-rows, see read_frags) in different banks, so each ds_read_b32
-// is conflict-free: k-row k's 16-column groups in the order g ^ ((k >> 2) & 3) within each 64 columns for the
-// 16 x 16 MFMAs, its 128-byte segments in the order seg ^ ((k >> 2) & 1) for the 32 x 32 ones (K-split instances,
-// lane halves reading k and k + 4). Needs K a multiple of 32, N of 4 (columns past N are
+// k-rows of the tile's BN columns; the LDS DMA copies them as they lie, k-row k's 128-byte column segments in the
+// order seg ^ ((k >> 2) & 1), and a lane reads its column's 4 consecutive k as 4 single floats (gfx950 has no 32-bit
+// transposing LDS read). The segment order puts the two lane halves' reads (k and k + 4, see read_frags) in different
+// halves of the 64 banks, so each ds_read_b32 is conflict-free. Needs K a multiple of 32, N of 4 (columns past N are
 // clamped to the last whole chunk, read but never stored), 16-byte aligned k-rows and batches.
 template <int CT, int BM, int BN, int WM, int WN, int ST, int ACT, int FORM, bool SPLIT = false, bool BKM = false>
 __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands op, EpiParams ep, int tilesM,
@@ -140,13 +137,6 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
     constexpr int GA = BM / 8 / NW;  // 8-row LDS DMA groups per wave per A tile
     constexpr int GB = BN / 8 / NW;
     static_assert(GA >= 1 && GB >= 1, "tile too small for the wave count");
-    // fp32 without a K split runs on 16 x 16 blocks (v_mfma_f32_16x16x4f32), the others on 32 x 32
-    // (v_mfma_f32_32x32x2f32). Both read the same bytes of LDS per MFMA flop; the 16 x 16 instruction takes 8 passes
-    // instead of 16 and keeps the fp32 pipe busier (a lab probe: 152.3 against 138.5 TFLOP/s, back-to-back MFMAs on
-    // every SIMD). A 32 x 32 block's accumulators are then four 16 x 16 blocks, acc4[j][i][2 jj + ii] holding rows
-    // 16 ii .. + 15 and columns 16 jj .. + 15 of it.
-    constexpr bool MI16 = F32 && !SPLIT;
-    constexpr int NSUB = MI16 ? kChunks / 4 : kChunks / 2;  // fragment substeps per k-tile
     static_assert(NW * TM * kStagePitch * 4 <= (BM + BN) * kChunks * 16 * ST, "epilogue staging exceeds LDS");
 
     // one LDS array: ST A stages, then ST B stages; reused as epilogue staging after the k-loop
@@ -188,14 +178,12 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
 #pragma unroll
     for (int j = 0; j < GB; ++j) {
         if constexpr (BKM) {
-            // LDS chunk p of the B tile holds k-row k = p / (BN / 4), position rem = p % (BN / 4): column chunk
-            // rem ^ (4 ((k >> 2) & 3)) for the 16 x 16 MFMAs (16-column groups permuted within each 64 columns), and
-            // segment (rem / 8) ^ ((k >> 2) & 1), chunk rem % 8 for the 32 x 32 ones
+            // LDS chunk p of the B tile holds k-row p / (BN / 4), segment position (p % (BN / 4)) / 8, chunk p % 8
             constexpr int kCpr = BN / 4;  // 16-byte chunks per k-row of the tile
             const int p = (wave * GB + j) * 64 + lane;
             const int k = p / kCpr, rem = p % kCpr;
-            const int src = MI16 ? rem ^ (((k >> 2) & 3) << 2) : ((((rem >> 3) ^ ((k >> 2) & 1)) << 3) | (rem & 7));
-            int64_t n = n0 + src * 4;
+            const int seg = (rem >> 3) ^ ((k >> 2) & 1);
+            int64_t n = n0 + seg * 32 + (rem & 7) * 4;
             n = n + 4 <= N ? n : N - 4;
             pb[j] = B + k * op.ldb + n;
         } else {
@@ -219,18 +207,12 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
     };
 
     f32x16_t acc[FN][FM];
-    f32x4_t acc4[FN][FM][4];
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
-            if constexpr (MI16) {
 #pragma unroll
-                for (int b = 0; b < 4; ++b) acc4[j][i][b] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-            } else {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.0f;
-            }
+            for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.0f;
         }
     }
 
@@ -262,33 +244,7 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
             issue_tile((kt + ST - 1) % ST, static_cast<int64_t>(kt0 + kt + ST - 1) * kBK);
         }
         uint4 va[2][FM], vb[2][FN];
-        uint4 va16[2][2 * FM], vb16[2][2 * FN];
         auto read_frags = [&](int slot, int s) {
-            if constexpr (MI16) {
-                // lane quarter q4 = lane / 16 reads 16-byte chunk 4 s + q4 of row lane % 16 of each 16-row block:
-                // k = 16 s + 4 q4 + e, and MFMA step e of the substep takes element e (the same for A and B)
-                const int c = s * 4 + (lane >> 4);
-#pragma unroll
-                for (int i = 0; i < 2 * FM; ++i) {
-                    const int row = wm * TM + i * 16 + (lane & 15);
-                    va16[slot][i] = sA[cur][row * kChunks + swz(row, c)];
-                }
-#pragma unroll
-                for (int j = 0; j < 2 * FN; ++j) {
-                    if constexpr (BKM) {
-                        // column wn TN + 16 j + lane % 16 at k = 16 s + 4 q4 + e, e = 0..3: those k-rows hold it at
-                        // position column ^ (16 q4), so the four lane quarters read four different bank groups
-                        const int pos = (wn * TN + j * 16 + (lane & 15)) ^ ((lane >> 4) << 4);
-                        const float *col = reinterpret_cast<const float *>(&sB[cur][0]) + (16 * s + 4 * (lane >> 4)) * BN + pos;
-                        vb16[slot][j] = make_uint4(__builtin_bit_cast(uint32_t, col[0]), __builtin_bit_cast(uint32_t, col[BN]),
-                                                   __builtin_bit_cast(uint32_t, col[2 * BN]), __builtin_bit_cast(uint32_t, col[3 * BN]));
-                    } else {
-                        const int row = wn * TN + j * 16 + (lane & 15);
-                        vb16[slot][j] = sB[cur][row * kChunks + swz(row, c)];
-                    }
-                }
-                return;
-            }
             const int c = s * 2 + lhalf;  // lane half h reads 16-byte chunk 2s+h of its row
 #pragma unroll
             for (int i = 0; i < FM; ++i) {
@@ -312,29 +268,15 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
         };
         read_frags(0, 0);
 #pragma unroll
-        for (int s = 0; s < NSUB; ++s) {
-            if (s + 1 < NSUB) {
+        for (int s = 0; s < kChunks / 2; ++s) {
+            if (s + 1 < kChunks / 2) {
                 read_frags((s + 1) & 1, s + 1);
             }
             // Keep the next substep's LDS reads ahead of this substep's MFMAs (the scheduler would
             // otherwise sink them next to their uses and expose the LDS latency every few MFMAs).
             __builtin_amdgcn_sched_barrier(0);
             const int sl = s & 1;
-            if constexpr (MI16) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-#pragma unroll
-                    for (int j = 0; j < 2 * FN; ++j) {
-#pragma unroll
-                        for (int i = 0; i < 2 * FM; ++i) {
-                            const f32x4_t a4 = __builtin_bit_cast(f32x4_t, va16[sl][i]);
-                            const f32x4_t b4 = __builtin_bit_cast(f32x4_t, vb16[sl][j]);
-                            f32x4_t &d = acc4[j >> 1][i >> 1][2 * (j & 1) + (i & 1)];
-                            d = __builtin_amdgcn_mfma_f32_16x16x4f32(b4[q], a4[q], d, 0, 0, 0);
-                        }
-                    }
-                }
-            } else if constexpr (F32) {
+            if constexpr (F32) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
 #pragma unroll
@@ -478,22 +420,11 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
         __syncthreads();  // previous strip fully read back (and, for j = 0, the k-loop's last LDS reads done)
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
-            if constexpr (MI16) {
-                // 16 x 16 block (ii, jj): lane -> row 16 ii + lane % 16, columns 16 jj + 4 (lane / 16) .. + 3
 #pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    const int ii = b & 1, jj = b >> 1;
-                    float *dst = stage + (i * 32 + ii * 16 + (lane & 15)) * kStagePitch + jj * 16 + (lane >> 4) * 4;
-                    const f32x4_t &v = acc4[j][i][b];
-                    *reinterpret_cast<float4 *>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-                }
-            } else {
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    float *dst = stage + (i * 32 + lrow) * kStagePitch + g * 8 + lhalf * 4;
-                    *reinterpret_cast<float4 *>(dst) =
-                        make_float4(acc[j][i][4 * g + 0], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2], acc[j][i][4 * g + 3]);
-                }
+            for (int g = 0; g < 4; ++g) {
+                float *dst = stage + (i * 32 + lrow) * kStagePitch + g * 8 + lhalf * 4;
+                *reinterpret_cast<float4 *>(dst) =
+                    make_float4(acc[j][i][4 * g + 0], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2], acc[j][i][4 * g + 3]);
             }
         }
         __syncthreads();
