@@ -9,7 +9,8 @@
 //  - k-tiles of 128 bytes per row (64 bf16 / 32 fp32) go straight from global memory into LDS with
 //    gfx950's global_load_lds_dwordx4 (no staging registers) through an ST-stage ring: the loads of tile k+ST-1
 //    are issued right after the barrier that opens tile k (ST = 2 for 256 x 256, up to 4 where the tiles are
-//    small enough, so that a small grid is not bound by one memory latency per k-tile).
+//    small enough, so that a small grid is not bound by one memory latency per k-tile). The copies are inline asm
+//    (dma16) and the ring's waits are explicit (wait_tiles), so they stay in flight during the k-tile's MFMAs.
 //  - A wave's LDS DMA instruction fills 8 rows x 128 bytes; lane l writes 16-byte slot l, and fetches the
 //    global chunk that the XOR swizzle (chunk ^ (row & 7)) assigns to that slot, so the ds_read_b128 of
 //    32 consecutive rows at one logical k-chunk hits every bank once.
@@ -86,6 +87,25 @@ __device__ __forceinline__ void wait_tiles(int ahead)
         }
     }
     wait_vmcnt<0>();
+}
+
+// LDS byte address of a __shared__ element.
+__device__ __forceinline__ uint32_t lds_byte(const uint4 *p)
+{
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void *)p));
+}
+
+// One LDS DMA copy: lane l's 16 bytes at src land in LDS at lds + 16 l. It is issued through inline asm so that the
+// compiler does not track it. With the builtin (__builtin_amdgcn_global_load_lds) the compiler cannot tell the ring's
+// stages apart, so it waited for every copy in flight (vmcnt(0)) before the first fragment read of each k-tile, which
+// also waited for the copy just issued for k-tile kt + ST - 1 and left no copy in flight during the MFMAs. The waits
+// are the kernel's own instead: wait_tiles before each k-tile's barrier. The s_nop before the M0 write covers the
+// wait states after the v_readfirstlane that produced its operand, the one after it those of the copy reading M0.
+__device__ __forceinline__ void dma16(const void *src, uint32_t lds)
+{
+    lds = __builtin_amdgcn_readfirstlane(lds);
+    asm volatile("s_nop 4\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+                 : "memory", "m0");
 }
 
 // Calls f(std::integral_constant<int, I>) for I = 0 .. N-1 (a loop whose index is a compile-time constant).
@@ -193,16 +213,16 @@ __global__ __launch_bounds__(WM *WN * 64, 1) void gemm_mfma_kernel(GemmOperands 
         }
     }
 
+    // LDS byte addresses of stage 0's A and B tiles (stage s adds s * BM (BN) rows of 128 bytes)
+    const uint32_t ldsA = lds_byte(&sA[0][0]), ldsB = lds_byte(&sB[0][0]);
     auto issue_tile = [&](int buf, int64_t k0) {
 #pragma unroll
         for (int j = 0; j < GA; ++j) {
-            __builtin_amdgcn_global_load_lds(static_cast<const void *>(pa[j] + k0),
-                                             (lds_void *)(&sA[buf][(wave * GA + j) * 64]), 16, 0, 0);
+            dma16(pa[j] + k0, ldsA + static_cast<uint32_t>((buf * BM * kChunks + (wave * GA + j) * 64) * 16));
         }
 #pragma unroll
         for (int j = 0; j < GB; ++j) {
-            __builtin_amdgcn_global_load_lds(static_cast<const void *>(pb[j] + (BKM ? k0 * op.ldb : k0)),
-                                             (lds_void *)(&sB[buf][(wave * GB + j) * 64]), 16, 0, 0);
+            dma16(pb[j] + (BKM ? k0 * op.ldb : k0), ldsB + static_cast<uint32_t>((buf * BN * kChunks + (wave * GB + j) * 64) * 16));
         }
     };
 
