@@ -577,7 +577,14 @@ int BuildCore(const kudnn_tensor_desc &a, const kudnn_tensor_desc &b, const kudn
             const int64_t kt = core.kp * DtSize(core.computeDt) / 128;
             const bool tailSplit = batches == 1 && t256 <= 64 && kt >= 128 && (t256 * kt + 255) / 256 >= 24;
             const bool slices = kudnn_kslice_rule(core.M, core.N, kt, batches, core.computeDt) >= 2;
-            core.cfg = t256 >= 80 || tailSplit || slices ? KUDNN_CFG_BF16_PINGPONG_256x256 : KUDNN_CFG_BF16_128x128;
+            // Except 32-64 tiles with at most 64 k-tiles and the weight stored [N][K]: there the 4-wave kernel's 128-256
+            // tiles of 128 x 128 beat two to four K slices (bf16, bench.py --only dispatch: 256 x 11008 x 4096 45 against
+            // 55 us, 256 x 14336 x 4096 45 against 58, 1024 x 4096 x 4096 46 against 62, 1024 x 2048 x 2048 26 against
+            // 35, 512 x 4096 x 4096 even; 16 tiles and 128 k-tiles stay sliced). A weight stored [K][N] keeps the
+            // ping-pong kernel, which reads it in place; the 4-wave kernel would pack it on every call.
+            const bool fourWave = batches == 1 && t256 >= 32 && t256 <= 64 && kt <= 64 && core.B.s_r != 1;
+            core.cfg = (t256 >= 80 || tailSplit || slices) && !fourWave ? KUDNN_CFG_BF16_PINGPONG_256x256
+                                                                        : KUDNN_CFG_BF16_128x128;
         }
     } else {
         core.engine = ENGINE_MFMA_F32;

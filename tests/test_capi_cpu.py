@@ -207,7 +207,7 @@ def test_kslice_rule():
     # small 16-bit grids: the ping-pong kernel with K slices (tiles x slices <= 128, slices of >= 16 k-tiles); not at
     # 64 tiles with < 64 k-tiles (the 4-wave kernel), nor from 97 tiles on, nor for M < 1024 above 64 tiles
     for (M, N, Kd), S in {(256, 4096, 4096): 4, (256, 4096, 14336): 8, (512, 4096, 14336): 4, (1024, 4096, 11008): 2,
-                          (256, 11008, 4096): 2, (4096, 1152, 4608): 2, (4096, 1536, 5120): 2}.items():
+                          (4096, 1152, 4608): 2, (4096, 1536, 5120): 2}.items():
         d = plan_of(M, Kd, N).describe()
         assert d.startswith("mfma_bf16_pingpong") and f" kslices={S}" in d, d
         assert f" kslices={S}" in plan_of(M, Kd, N, K.F16).describe()
@@ -215,6 +215,13 @@ def test_kslice_rule():
         assert "kslices" not in plan_of(M, Kd, N).describe(), (M, N, Kd)
     assert plan_of(2048, 2048, 2048).describe().startswith("mfma_bf16_128x128")
     assert "kslices" not in plan_of(256, 4096, 4096, K.F32).describe()
+    # 32-64 tiles with at most 64 k-tiles: the 4-wave kernel when the weight is stored [N][K]; stored [K][N], the
+    # ping-pong kernel reads it in place, in K slices
+    for M, N, Kd in ((256, 11008, 4096), (1024, 4096, 4096), (1024, 2048, 2048), (512, 4096, 4096)):
+        assert plan_of(M, Kd, N).describe().startswith("mfma_bf16_128x128"), (M, N, Kd)
+        assert plan_of(M, Kd, N, K.F16).describe().startswith("mfma_f16_128x128"), (M, N, Kd)
+        d = plan_of(M, Kd, N, wl="AB").describe()
+        assert d.startswith("mfma_bf16_pingpong") and "kslices=" in d and "kmajorB" in d, d
 
 
 def test_forced_mfma_config_keeps_decode_plans(monkeypatch):
@@ -262,7 +269,7 @@ def test_dispatcher_choices():
 @pytest.mark.parametrize("M,Kd,N,cfg", [
     (512, 4096, 11008, "pingpong"),   # 2 x 43 = 86 tiles of 256 x 256: from 80 on, the ping-pong kernel
     (3072, 14336, 4096, "pingpong"),  # 192 tiles: a partial round still goes to the ping-pong kernel
-    (1024, 4096, 4096, "pingpong"),   # 64 tiles, 64 k-tiles: K slices
+    (1024, 4096, 4096, "128x128"),    # 64 tiles, 64 k-tiles: the 4-wave kernel's 256 tiles of 128 x 128
     (1024, 11008, 4096, "pingpong"),  # 64 tiles, 172 k-tiles: K slices
     (512, 14336, 4096, "pingpong"),   # 32 tiles, 224 k-tiles: K slices
     (512, 11008, 4096, "pingpong"),   # 32 tiles, 172 k-tiles: K slices
