@@ -132,6 +132,32 @@ def test_planner_kslices(mnk, S):
     compare(got[rows].reshape(-1), ref.buf, O.BF16, plan.describe(), explain=why)
 
 
+@pytest.mark.parametrize("mnk,wl,start", [((1024, 4096, 4096), "BA", "mfma_bf16_128x128"),
+                                           ((256, 11008, 4096), "BA", "mfma_bf16_128x128"),
+                                           ((1024, 4096, 4096), "AB", "mfma_bf16_pingpong")])
+def test_planner_four_wave_or_slices(mnk, wl, start):
+    # 32-64 tiles with at most 64 k-tiles: the planner's 4-wave 128 x 128 kernel when the weight is stored [N][K]; the
+    # ping-pong kernel in K slices, reading the weight in place, when it is stored [K][N]
+    M, N, Kd = mnk
+    x = Case([M, Kd], O.BF16, seed=655, dist="normal", lo=0.0, hi=1.0)
+    w = Case([Kd, N], O.BF16, wl, seed=656, dist="normal", lo=0.0, hi=0.02)
+    b = Case([1, N], O.BF16, seed=657, lo=-0.2, hi=0.2)
+    y = Case([M, N], O.BF16, zero=True)
+    plan = K.LinearActivation(x.desc, w.desc, y.desc, b.desc, 0.0, 0.0, K.ACT_GELU_TANH)
+    desc = plan.describe()
+    assert desc.startswith(start) and (("kslices=2" in desc and "kmajorB" in desc) == (wl == "AB")), desc
+    dy = torch.zeros(M * N, dtype=torch.int16, device="cuda")
+    plan.run(x.device(), w.device(), dy, b.device())
+    torch.cuda.synchronize()
+    got = from_device(dy, O.BF16).reshape(M, N)
+    rows = sample_rows(M, 24)
+    xr = dense_rows(x.t, rows)
+    ref = O.empty((len(rows), N), (N, 1), O.BF16)
+    O.linear_act(xr, w.t, ref, b.t, O.ACT_GELU_TANH, 0.0)
+    why = explainer(O.BF16, xr, w.t, b.t, (len(rows), N), act=O.ACT_GELU_TANH)
+    compare(got[rows].reshape(-1), ref.buf, O.BF16, desc, explain=why)
+
+
 def test_kslices_graph_replays(slices):
     # both launches captured in a HIP graph (no memset nodes): every replay, with eager work between replays, equals
     # the eager result
